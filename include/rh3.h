@@ -1,0 +1,160 @@
+/* rh3.h — C ABI of the MI355X (gfx950) DiT hot-path library librh3.so.
+ *
+ * Plain pointers, int64 sizes and strides (in elements), a hipStream_t, and an int status
+ * (0 = success; on failure rh3_last_error() returns the message for the calling thread). Every
+ * pointer is device memory unless stated. Nothing here allocates device memory: callers own the
+ * outputs and, for attention, a workspace sized by rh3_attention_workspace_bytes().
+ *
+ * Element types travel as their bit patterns: bf16 as uint16_t, OCP e4m3fn as uint8_t.
+ *
+ * Each entry point names the reference interface it replaces (paths under
+ * /root/reference/custom_nodes/rapid_h3/). The reference reaches those through pybind11 modules
+ * built by torch.utils.cpp_extension; this library is loaded with ctypes instead.
+ */
+#ifndef RH3_H
+#define RH3_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RH3_OK 0
+#define RH3_EINVAL 1   /* bad argument: shape, stride, alignment, null pointer */
+#define RH3_ELAUNCH 2  /* HIP reported an error for a launch */
+
+#define RH3_DTYPE_BF16 1
+#define RH3_DTYPE_F32 2
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* rh3_last_error(void);
+/* Library ABI version (increments when a signature changes). */
+int rh3_abi_version(void);
+
+/* ---------------------------------------------------------------------------------------------
+ * Per-token activation quantizers: one HBM pass, s[m] = max(amax_m / QMAX, 1e-12),
+ * q = round_half_even(x / s) clamped (int8: +-127; fp8: +-448 then e4m3fn RNE).
+ * x [M, K] bf16 row stride ldx; q [M, K] row stride ldq; s [M] fp32. K % 8 == 0, ldx % 8 == 0,
+ * ldq % 8 == 0, 16-byte aligned rows.
+ * ------------------------------------------------------------------------------------------- */
+
+/* replaces triton_fp8.quant_rows_i8 (triton_fp8.py:57-64) and the int8_rowwise
+ * kernels.quantize_rows (kernels.py:75-80) */
+int rh3_quant_rows_i8(const uint16_t* x, int64_t ldx, int64_t M, int64_t K,
+                      int8_t* q, int64_t ldq, float* s, hipStream_t stream);
+
+/* replaces triton_fp8.quant_rows (triton_fp8.py:449-455) and the fp8 kernels.quantize_rows (kernels.py:81-82) */
+int rh3_quant_rows_fp8(const uint16_t* x, int64_t ldx, int64_t M, int64_t K,
+                       uint8_t* q, int64_t ldq, float* s, hipStream_t stream);
+
+/* RMSNorm + modulation prologue, then per-token int8:
+ *   v = ((x * rstd) * w) * (1 + scale[idx[m]]) + shift[idx[m]],  rstd = 1 / sqrt(sum(x^2) / K + eps)
+ * weight [K] bf16 or NULL; idx [M] int32; shift/scale [R, K] of tab_dtype (RH3_DTYPE_BF16 or
+ * RH3_DTYPE_F32) sharing row stride ld_tab, unit column stride.
+ * replaces triton_fp8.norm_mod_rot_quant_rows_i8 (triton_fp8.py:442-446), KIND 2 prologue
+ * (triton_fp8.py:141-147), for the int8_rowwise recipe (no ConvRot) */
+int rh3_quant_norm_mod_i8(const uint16_t* x, int64_t ldx, int64_t M, int64_t K,
+                          const uint16_t* weight, float eps, const int32_t* idx,
+                          const void* shift, const void* scale, int tab_dtype, int64_t ld_tab,
+                          int8_t* q, int64_t ldq, float* s, hipStream_t stream);
+
+/* Head-major attention output o [H, M, 128] bf16 (head stride ld_head, token stride ld_row) ->
+ * per-token int8 of the row [M, H*128] (column k = head k/128, dim k%128), without the transpose.
+ * replaces triton_fp8.rot_quant_heads_i8 (triton_fp8.py:429-434), KIND 3 gather (:133-135) */
+int rh3_quant_heads_i8(const uint16_t* o, int64_t H, int64_t M, int64_t ld_head, int64_t ld_row,
+                       int8_t* q, int64_t ldq, float* s, hipStream_t stream);
+
+/* x [M, 2F] = [gate | up] bf16 -> per-token int8 of (g * sigmoid(g)) * u, [M, F].
+ * replaces triton_fp8.swiglu_rot_quant_rows_i8 (triton_fp8.py:437-439), KIND 1 prologue (:137-139) */
+int rh3_quant_swiglu_i8(const uint16_t* x, int64_t ldx, int64_t M, int64_t F,
+                        int8_t* q, int64_t ldq, float* s, hipStream_t stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * Row-wise W8A8 GEMMs on int8 MFMA: acc[m,n] = sum_k xq[m,k] * wq[n,k] (int32, exact),
+ * y = (fp32(acc) * xs[m]) * ws[n]. xq [M, K] int8 (row stride ldx), wq [N, K] int8 (row stride ldw),
+ * xs [M], ws [N] fp32. K % 64 == 0, N % 8 == 0, strides % 16 == 0, 16-byte aligned rows.
+ * ------------------------------------------------------------------------------------------- */
+
+/* out = bf16_RNE(y [+ bias[n]]); bias [N] bf16 or NULL; out [M, N] row stride ldo.
+ * replaces cutlass_fp8.int8_gemm -> int8_rowwise_gemm (cutlass_fp8.py:37-39, fp8_rowwise.cu:546-584) */
+int rh3_gemm_i8(const int8_t* xq, int64_t ldx, const float* xs, const int8_t* wq, int64_t ldw,
+                const float* ws, const uint16_t* bias, uint16_t* out, int64_t ldo,
+                int64_t M, int64_t N, int64_t K, hipStream_t stream);
+
+/* SwiGLU epilogue for fc1 rows in swiglu_perm order ([g 4j..4j+3 | u 4j..4j+3] per 8 columns):
+ * g, u = bf16(y); h[m, n/2..] = bf16((g * sigmoid(g)) * u); out [M, N/2] row stride ldo.
+ * replaces cutlass_fp8.int8_gemm_swiglu (cutlass_fp8.py:65-67, fp8_rowwise.cu:611-629) */
+int rh3_gemm_i8_swiglu(const int8_t* xq, int64_t ldx, const float* xs, const int8_t* wq_perm, int64_t ldw,
+                       const float* ws_perm, uint16_t* out, int64_t ldo,
+                       int64_t M, int64_t N, int64_t K, hipStream_t stream);
+
+/* Gated residual, in place: resid[m,n] = bf16_RNE(fma(bf16(y), gate[n], resid[m,n])); gate [N] bf16;
+ * resid [M, N] row stride ldr.
+ * replaces cutlass_fp8.int8_gemm_gated_residual (cutlass_fp8.py:49-52, fp8_rowwise.cu:587-608) */
+int rh3_gemm_i8_gated(const int8_t* xq, int64_t ldx, const float* xs, const int8_t* wq, int64_t ldw,
+                      const float* ws, const uint16_t* gate, uint16_t* resid, int64_t ldr,
+                      int64_t M, int64_t N, int64_t K, hipStream_t stream);
+
+/* Verification: the raw int32 accumulators acc [M, N] (row stride ldc) of the same kernel.
+ * No reference counterpart as an entry point: it exposes the s32 accumulator of
+ * fp8_rowwise.cu:282-331 so tests can check it bit for bit. */
+int rh3_gemm_i8_acc(const int8_t* xq, int64_t ldx, const int8_t* wq, int64_t ldw, int32_t* acc, int64_t ldc,
+                    int64_t M, int64_t N, int64_t K, hipStream_t stream);
+
+/* FP8 (OCP e4m3fn) row-wise GEMM, fp32 accumulate, same epilogue as rh3_gemm_i8.
+ * replaces cutlass_fp8.fp8_gemm -> fp8_rowwise_gemm (cutlass_fp8.py:32-34, fp8_rowwise.cu:512-544) */
+int rh3_gemm_fp8(const uint8_t* xq, int64_t ldx, const float* xs, const uint8_t* wq, int64_t ldw,
+                 const float* ws, const uint16_t* bias, uint16_t* out, int64_t ldo,
+                 int64_t M, int64_t N, int64_t K, hipStream_t stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * INT8 flash attention, head_dim 128, non-causal. q [Sq, H, 128], k and v [Sk, H, 128] bf16 with any
+ * token / head strides (elements; the 128 channels contiguous). Q and K are quantized per
+ * (head, 128-token block); K is first mean-smoothed (kmean over all Sk tokens); Q.K^T runs on int8
+ * MFMA, softmax in fp32 (exp2 domain), P.V on bf16 MFMA. out [Sq, H, 128] bf16 with its own strides.
+ * ------------------------------------------------------------------------------------------- */
+
+/* Bytes of workspace the attention entry points need for (Sq, Sk, H). */
+int64_t rh3_attention_workspace_bytes(int64_t Sq, int64_t Sk, int64_t H);
+
+/* replaces attn_int8.attention -> int8_attention (attn_int8.py:30-34, attn_int8.cu:2660-2665) with
+ * per-128-block Q/K scales (attn_int8.cu:402-443) and bf16 P.V. Sq may differ from Sk
+ * (cross-attention); smooth_k 0 skips the K mean. */
+int rh3_int8_attention(const uint16_t* q, int64_t q_ss, int64_t q_sh,
+                       const uint16_t* k, int64_t k_ss, int64_t k_sh,
+                       const uint16_t* v, int64_t v_ss, int64_t v_sh,
+                       int64_t Sq, int64_t Sk, int64_t H, float scale, int smooth_k,
+                       uint16_t* out, int64_t o_ss, int64_t o_sh,
+                       void* workspace, int64_t workspace_bytes, hipStream_t stream);
+
+/* Same, with the per-head RMSNorm (weights qw/kw [128] bf16, eps) and split-half RoPE (table
+ * tab [S, rot/2, 2, 2] bf16 = (cos, -sin, sin, cos), rot 96 or 128) applied to raw q and k inside
+ * the pre-pass. Self-attention only (Sq == Sk == S).
+ * replaces attn_int8.attention_rr -> int8_attention_rr (attn_int8.py:42-48, attn_int8.cu:2669-2676) */
+int rh3_int8_attention_rr(const uint16_t* q, int64_t q_ss, int64_t q_sh,
+                          const uint16_t* k, int64_t k_ss, int64_t k_sh,
+                          const uint16_t* v, int64_t v_ss, int64_t v_sh,
+                          int64_t S, int64_t H, const uint16_t* tab, int rot,
+                          const uint16_t* qw, const uint16_t* kw, float eps, float scale, int smooth_k,
+                          uint16_t* out, int64_t o_ss, int64_t o_sh,
+                          void* workspace, int64_t workspace_bytes, hipStream_t stream);
+
+/* Pre-pass operands for verification (int8_prepass, attn_int8.cu:2851-2879): writes into the
+ * workspace and returns pointers to q8 [H, Sqpad, 128] int8, qs [H, Sqpad/128] fp32, k8, ks,
+ * kmean [H, 128] fp32 and vt [H, 128, Skpad] bf16 (keys permuted within 32-key groups).
+ * tab NULL: no RMSNorm/RoPE. */
+int rh3_attention_prepass(const uint16_t* q, int64_t q_ss, int64_t q_sh,
+                          const uint16_t* k, int64_t k_ss, int64_t k_sh,
+                          const uint16_t* v, int64_t v_ss, int64_t v_sh,
+                          int64_t Sq, int64_t Sk, int64_t H, const uint16_t* tab, int rot,
+                          const uint16_t* qw, const uint16_t* kw, float eps, int smooth_k,
+                          void* workspace, int64_t workspace_bytes, void** ptrs /* [6] */,
+                          hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RH3_H */

@@ -1,0 +1,147 @@
+"""CPU restatement of the reference's activation and weight quantizers (numpy, float32 arithmetic).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and bench.py's CPU baseline, as
+the checker. The product path never calls it.
+
+Semantics are the PyTorch path of the reference, which is the parity target:
+  * per-token INT8   /root/reference/custom_nodes/rapid_h3/kernels.py:75-80
+      s = max(amax/127, 1e-12) (fp32), q = clamp(round_half_even(fp32(x) / s), -127, 127)
+  * per-token FP8    kernels.py:81-82
+      s = max(amax/448, 1e-12), q = e4m3fn_RNE(clamp(x / s, -448, 448))
+  * per-channel weights, int8 / fp8   kernels.py:52-72 (same, along K of each output row; scale [1, N])
+  * fused prologues   triton_fp8.py:128-148 (KIND 1 SwiGLU, KIND 2 RMSNorm + modulation, KIND 3
+    head-major gather), with IEEE x / s as in kernels.py rather than the Triton x * (1/s).
+
+The RMSNorm sum of squares is order dependent. Its order here is the one the HIP kernel uses, stated
+once so both sides agree (the reference pins its own Triton layout instead, triton_fp8.py:216-232):
+one 64-lane wavefront per row; lane l owns columns 512*j + 8*l + e (j ascending, then e = 0..7) and
+accumulates ss += x*x in fp32 from 0 (x is bf16, so x*x is exact and fma == mul+add); the 64 lane sums
+are then added by a butterfly over lane distances 32, 16, 8, 4, 2, 1.
+"""
+import numpy as np
+
+from .numerics import F32, bf16_to_f32, f32_to_fp8_e4m3
+
+I8_MAX = F32(127.0)
+FP8_MAX = F32(448.0)
+EPS_SCALE = F32(1e-12)
+
+
+def _as_f32(x):
+    x = np.asarray(x)
+    return bf16_to_f32(x) if x.dtype == np.uint16 else x.astype(np.float32)
+
+
+def _quant_i8(v, s):
+    return np.clip(np.rint(v / s), -127, 127).astype(np.int8)
+
+
+def quantize_rows(x, mode="int8_rowwise"):
+    """kernels.quantize_rows (kernels.py:75-82): x [M, K] (bf16 bits or fp32) -> (q, s [M, 1] fp32).
+    int8 q is np.int8; fp8 q is e4m3fn bits (np.uint8)."""
+    v = _as_f32(x)
+    amax = np.abs(v).max(axis=-1, keepdims=True) if v.shape[-1] else np.zeros(v.shape[:-1] + (1,), F32)
+    if mode == "int8_rowwise":
+        s = np.maximum(amax / I8_MAX, EPS_SCALE).astype(F32)
+        return _quant_i8(v, s), s
+    if mode in ("fp8_rowwise", "fp8_rowwise_torch"):
+        s = np.maximum(amax / FP8_MAX, EPS_SCALE).astype(F32)
+        return f32_to_fp8_e4m3(np.clip(v / s, -FP8_MAX, FP8_MAX)), s
+    raise ValueError(mode)
+
+
+def quantize_weight(w, mode="int8_rowwise"):
+    """kernels.quantize_weight (kernels.py:52-72) for the row-wise modes: w [N, K] -> (q [N, K], scale [1, N]).
+    int8_rot applies ConvRot (blockdiag H256, triton_fp8.py:86-90) before the row-wise quantization."""
+    if mode == "int8_fast":
+        mode = "int8_rowwise"
+    v = _as_f32(w)
+    if mode == "int8_rot":
+        v = convrot(v)
+        mode = "int8_rowwise"
+    q, s = quantize_rows(v, mode)
+    return q, np.ascontiguousarray(s.T)
+
+
+def sumsq_rows(v):
+    """Row sums of squares of v [M, K] fp32 in the wavefront order stated in the module docstring."""
+    m, k = v.shape
+    kp = -(-k // 512) * 512
+    vp = np.zeros((m, kp), F32)
+    vp[:, :k] = v
+    t = vp.reshape(m, kp // 512, 64, 8)               # [row, j, lane, e]
+    lane = np.zeros((m, 64), F32)
+    for j in range(t.shape[1]):
+        for e in range(8):
+            x = t[:, j, :, e]
+            lane = (lane + x * x).astype(F32)
+    w = 32
+    while w >= 1:
+        lane = (lane[:, :w] + lane[:, w:2 * w]).astype(F32)
+        w //= 2
+    return lane[:, 0]
+
+
+def norm_mod(x, weight, eps, idx, shift, scale):
+    """RMSNorm + modulation prologue (triton_fp8.py:141-147, :165-172):
+    v = ((x * rstd) * w) * (1 + scale[idx]) + shift[idx], rstd = 1 / sqrt(sumsq / K + eps), all fp32.
+    weight [K] bf16 or None; idx [M] int32; shift / scale [R, K] (bf16 bits or fp32)."""
+    v = _as_f32(x)
+    k = v.shape[1]
+    ss = sumsq_rows(v)
+    rstd = (F32(1.0) / np.sqrt(ss / F32(k) + F32(eps))).astype(F32)
+    y = v * rstd[:, None]
+    if weight is not None:
+        y = y * _as_f32(weight)[None, :]
+    idx = np.asarray(idx, dtype=np.int64)
+    sc = _as_f32(scale)[idx]
+    sh = _as_f32(shift)[idx]
+    return (y * (F32(1.0) + sc) + sh).astype(F32)
+
+
+def norm_mod_quant_rows_i8(x, weight, eps, idx, shift, scale):
+    """triton_fp8.norm_mod_rot_quant_rows_i8 without the rotation (the int8_rowwise recipe)."""
+    return quantize_rows(norm_mod(x, weight, eps, idx, shift, scale), "int8_rowwise")
+
+
+def heads_to_rows(o):
+    """Head-major attention output o [H, M, 128] -> [M, H*128]: column k is head k // 128, dim k % 128
+    (triton_fp8.py:133-135)."""
+    h, m, d = o.shape
+    return np.ascontiguousarray(np.transpose(o, (1, 0, 2)).reshape(m, h * d))
+
+
+def heads_quant_rows_i8(o):
+    """triton_fp8.rot_quant_heads_i8 without the rotation."""
+    return quantize_rows(heads_to_rows(o), "int8_rowwise")
+
+
+def silu_mul(g, u):
+    """fp32 (g * sigmoid(g)) * u with sigmoid(g) = 1 / (1 + exp(-g)) (triton_fp8.py:138-139)."""
+    g = g.astype(F32)
+    sig = (F32(1.0) / (F32(1.0) + np.exp(-g))).astype(F32)
+    return ((g * sig) * u.astype(F32)).astype(F32)
+
+
+def swiglu_quant_rows_i8(x):
+    """triton_fp8.swiglu_rot_quant_rows_i8 without the rotation: x [M, 2F] = [gate | up]."""
+    v = _as_f32(x)
+    f = v.shape[1] // 2
+    return quantize_rows(silu_mul(v[:, :f], v[:, f:]), "int8_rowwise")
+
+
+def regular_hadamard(n):
+    """ConvRot matrix (triton_fp8.py:70-80): Kronecker powers of the 4x4 regular Hadamard, / sqrt(n)."""
+    h4 = np.array([[1, 1, 1, -1], [1, 1, -1, 1], [1, -1, 1, 1], [-1, 1, 1, 1]], dtype=np.float64)
+    h = h4
+    while h.shape[0] < n:
+        h = np.kron(h, h4)
+    return h / np.sqrt(n)
+
+
+def convrot(x, group=256):
+    """x @ blockdiag(H_group)^T (triton_fp8.py:86-90), computed in float64 and rounded once to fp32."""
+    v = _as_f32(x).astype(np.float64)
+    m, k = v.shape
+    h = regular_hadamard(group)
+    return (v.reshape(-1, group) @ h.T).reshape(m, k).astype(F32)

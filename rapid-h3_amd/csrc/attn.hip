@@ -1,0 +1,553 @@
+// INT8 flash attention for gfx950, head_dim 128, non-causal.
+//
+// Pre-pass (HBM-bound):
+//   stats_kernel   per (256-token chunk, head): float64 channel sums of K (after the optional per-head
+//                  RMSNorm + RoPE) -> part [H][nchunk][128]           (attn_int8.cu:80-109 semantics)
+//   kmean_kernel   kmean[h][d] = fp32(sum_chunks part / Sk)            (attn_int8.cu:95-109)
+//   quant_kernel   per (128-token block, head): [RMSNorm + RoPE] -> [- kmean] -> one scale per block
+//                  sc = max(amax, 1e-8) / 127, q = rint(x / sc)        (attn_int8.cu:402-443,
+//                  bench/attn_emulate.py:10-18) -> codes [H][Spad][128] int8, scales [H][Spad/128]
+//   vt_kernel      V [S][H][128] bf16 -> Vt [H][128][Skpad] bf16, keys permuted inside 32-key groups
+//                  so that the P.V operand of each lane is one 16-byte LDS read
+// Main kernel: per (128-query block, head) workgroup of 4 waves, 32 queries per wave.
+//   S^T = K8 . Q8^T on v_mfma_i32_32x32x32_i8 (keys on rows, queries on lanes), one fp32 dequant
+//   multiply per score c = qs[qblock] * ks[kblock] * scale * log2(e) (the 128x128 tile shares both
+//   block scales), online softmax in the exp2 domain, P rounded to bf16, and O^T += Vt . P^T on
+//   v_mfma_f32_32x32x16_bf16 (D on rows, queries on lanes, so the per-query rescale is per lane).
+//   The row sum l adds the same bf16-rounded P the MFMA consumes (attn_int8.cu:8-10, :652-656).
+//   K and Vt tiles (16 + 32 KiB) are double-buffered in LDS with XOR-swizzled 16-byte chunks.
+#include "rh3_common.hpp"
+
+namespace rh3 {
+namespace {
+
+constexpr int D = 128;
+constexpr int BLK = 128;     // quantization block and attention tile (tokens)
+constexpr int CHUNK = 256;   // statistics chunk (tokens)
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+
+struct RR {
+  const uint16_t* tab;  // [S][rot/2][2][2] bf16, nullptr = no RMSNorm/RoPE
+  const uint16_t* w;    // [128] bf16
+  float eps;
+  int rot;
+};
+
+__device__ __forceinline__ void load8(const uint16_t* p, float* v) {
+  unpack8(*reinterpret_cast<const uint4*>(p), v);
+}
+
+// Per-head RMSNorm + split-half RoPE of one 128-channel row held by 16 lanes (8 channels each,
+// lane l16 owns channels 8*l16..8*l16+7). Fixed order: per-lane x*x sum over e, then xor 8,4,2,1.
+__device__ __forceinline__ void rms_rope8(float* x, int lane, const RR& rr, int64_t s) {
+  const int l16 = lane & 15;
+  float ss = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ss = ss + x[e] * x[e];
+  ss = ss + __shfl_xor(ss, 8, 64);
+  ss = ss + __shfl_xor(ss, 4, 64);
+  ss = ss + __shfl_xor(ss, 2, 64);
+  ss = ss + __shfl_xor(ss, 1, 64);
+  const float r = 1.0f / sqrtf(ss / 128.0f + rr.eps);
+  float w[8];
+  load8(rr.w + 8 * l16, w);
+  float y[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) y[e] = round_bf((r * x[e]) * w[e]);
+  const int hr = rr.rot >> 1, step = hr >> 3;  // partner lane distance in 8-channel units
+  const int c0 = 8 * l16;
+  int src = l16;
+  if (c0 < hr) src = l16 + step;
+  else if (c0 < rr.rot) src = l16 - step;
+  float py[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) py[e] = __shfl(y[e], (lane & ~15) + src, 64);
+  if (c0 < rr.rot) {
+    const bool first = c0 < hr;
+    const int i0 = first ? c0 : c0 - hr;  // rotary pair index of channel e is i0 + e
+    const uint16_t* t = rr.tab + (s * hr + i0) * 4;
+    float tv[32];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) load8(t + 8 * q, tv + 8 * q);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float a = first ? y[e] : py[e];
+      const float b = first ? py[e] : y[e];
+      x[e] = first ? round_bf((a * tv[4 * e + 0]) + (b * tv[4 * e + 1]))
+                   : round_bf((a * tv[4 * e + 2]) + (b * tv[4 * e + 3]));
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = y[e];
+  }
+}
+
+// ------------------------------------------------------------------ statistics
+// grid (nchunk, H), 256 threads = 16 token slots x 16 lanes
+__global__ void __launch_bounds__(256) stats_kernel(const uint16_t* __restrict__ k, int64_t k_ss, int64_t k_sh,
+                                                    int64_t S, RR rr, double* __restrict__ part) {
+  __shared__ double red[16][D];
+  const int h = blockIdx.y, c = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
+  const int slot = tid >> 4, l16 = tid & 15;
+  double acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (int it = 0; it < CHUNK / 16; ++it) {
+    const int64_t s = static_cast<int64_t>(c) * CHUNK + it * 16 + slot;
+    const bool ok = s < S;  // uniform per 16-lane group
+    float x[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (ok) load8(k + s * k_ss + h * k_sh + 8 * l16, x);
+    if (rr.tab) {
+      // the shuffles inside rms_rope8 need every lane of the wave; out-of-range rows use token 0's table
+      rms_rope8(x, lane, rr, ok ? s : 0);
+    }
+    if (ok) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] += static_cast<double>(x[e]);
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) red[slot][8 * l16 + e] = acc[e];
+  __syncthreads();
+  if (tid < D) {
+    double t = 0.0;
+    for (int i = 0; i < 16; ++i) t += red[i][tid];
+    part[(static_cast<int64_t>(h) * gridDim.x + c) * D + tid] = t;
+  }
+}
+
+__global__ void zero_kernel(float* __restrict__ p, int64_t n) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0.0f;
+}
+
+__global__ void kmean_kernel(const double* __restrict__ part, int nchunk, int64_t S, float* __restrict__ kmean) {
+  const int h = blockIdx.x, d = threadIdx.x;
+  double t = 0.0;
+  for (int c = 0; c < nchunk; ++c) t += part[(static_cast<int64_t>(h) * nchunk + c) * D + d];
+  kmean[h * D + d] = static_cast<float>(t / static_cast<double>(S));
+}
+
+// ------------------------------------------------------------------ per-block quantizer
+// grid (Spad/128, H), 256 threads: wave w handles tokens w*32 .. w*32+31 of the block, 4 per pass
+__global__ void __launch_bounds__(256) quant_kernel(const uint16_t* __restrict__ x, int64_t x_ss, int64_t x_sh,
+                                                    int64_t S, int64_t Spad, RR rr, const float* __restrict__ mean,
+                                                    int8_t* __restrict__ codes, float* __restrict__ scales) {
+  __shared__ float wmax[4];
+  const int h = blockIdx.y, blk = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l16 = lane & 15, sub = lane >> 4;
+  float mv[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  if (mean) {
+    const float4 a = *reinterpret_cast<const float4*>(mean + h * D + 8 * l16);
+    const float4 b = *reinterpret_cast<const float4*>(mean + h * D + 8 * l16 + 4);
+    mv[0] = a.x; mv[1] = a.y; mv[2] = a.z; mv[3] = a.w; mv[4] = b.x; mv[5] = b.y; mv[6] = b.z; mv[7] = b.w;
+  }
+  float v[8][8];
+  float amax = 0.0f;
+#pragma unroll
+  for (int p = 0; p < 8; ++p) {
+    const int64_t s = static_cast<int64_t>(blk) * BLK + wave * 32 + p * 4 + sub;
+    const bool ok = s < S;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[p][e] = 0.0f;
+    if (ok) load8(x + s * x_ss + h * x_sh + 8 * l16, v[p]);
+    if (rr.tab) rms_rope8(v[p], lane, rr, ok ? s : 0);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      v[p][e] = ok ? v[p][e] - mv[e] : 0.0f;
+      amax = fmaxf(amax, fabsf(v[p][e]));
+    }
+  }
+  amax = wave_max(amax);
+  if (lane == 0) wmax[wave] = amax;
+  __syncthreads();
+  const float bm = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+  const float sc = fmaxf(bm, 1e-8f) / 127.0f;
+  const float inv = 1.0f / sc;
+  if (tid == 0) scales[static_cast<int64_t>(h) * (Spad / BLK) + blk] = sc;
+#pragma unroll
+  for (int p = 0; p < 8; ++p) {
+    const int64_t s = static_cast<int64_t>(blk) * BLK + wave * 32 + p * 4 + sub;
+    uint32_t b[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float r = fminf(fmaxf(rint_div(v[p][e], sc, inv), -127.0f), 127.0f);
+      b[e] = static_cast<uint32_t>(static_cast<int32_t>(r)) & 0xffu;
+    }
+    uint2 o;
+    o.x = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
+    o.y = b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24);
+    *reinterpret_cast<uint2*>(codes + (static_cast<int64_t>(h) * Spad + s) * D + 8 * l16) = o;
+  }
+}
+
+// ------------------------------------------------------------------ V transpose
+// Position p of a 32-key group holds key perm32(p): p = 16*m + 8*g + e  <->  key = 16*m + 8*(e/4) + 4*g + e%4,
+// the key order of lane group g's B fragment (registers 8m..8m+7 of the S^T accumulator).
+__device__ __forceinline__ int perm32(int p) {
+  const int m = p >> 4, g = (p >> 3) & 1, e = p & 7;
+  return 16 * m + 8 * (e >> 2) + 4 * g + (e & 3);
+}
+
+// grid (Skpad/64, H), 256 threads
+__global__ void __launch_bounds__(256) vt_kernel(const uint16_t* __restrict__ v, int64_t v_ss, int64_t v_sh,
+                                                 int64_t S, int64_t Spad, uint16_t* __restrict__ vt) {
+  constexpr int T = 64, P = D + 8;
+  __shared__ uint16_t tile[T * P];
+  const int h = blockIdx.y, tid = threadIdx.x;
+  const int64_t s0 = static_cast<int64_t>(blockIdx.x) * T;
+  for (int i = tid; i < T * D / 8; i += 256) {
+    const int r = i / (D / 8), c8 = (i % (D / 8)) * 8;
+    uint4 val = make_uint4(0, 0, 0, 0);
+    if (s0 + r < S) val = *reinterpret_cast<const uint4*>(v + (s0 + r) * v_ss + h * v_sh + c8);
+    *reinterpret_cast<uint4*>(&tile[r * P + c8]) = val;
+  }
+  __syncthreads();
+  for (int i = tid; i < D * (T / 8); i += 256) {
+    const int d = i / (T / 8), pc = (i % (T / 8)) * 8;  // positions pc..pc+7 of this 64-key slab
+    uint16_t o[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int p = pc + e;
+      const int key = (p & ~31) + perm32(p & 31);
+      o[e] = tile[key * P + d];
+    }
+    uint4 pk;
+    pk.x = o[0] | (static_cast<uint32_t>(o[1]) << 16);
+    pk.y = o[2] | (static_cast<uint32_t>(o[3]) << 16);
+    pk.z = o[4] | (static_cast<uint32_t>(o[5]) << 16);
+    pk.w = o[6] | (static_cast<uint32_t>(o[7]) << 16);
+    *reinterpret_cast<uint4*>(vt + (static_cast<int64_t>(h) * D + d) * Spad + s0 + pc) = pk;
+  }
+}
+
+// ------------------------------------------------------------------ main kernel
+struct FwdArgs {
+  const int8_t* q8;  // [H][Sqpad][128]
+  const float* qs;   // [H][Sqpad/128]
+  const int8_t* k8;  // [H][Skpad][128]
+  const float* ks;   // [H][Skpad/128]
+  const uint16_t* vt;  // [H][128][Skpad]
+  uint16_t* out;
+  int64_t o_ss, o_sh;
+  int64_t Sq, Sk, Sqpad, Skpad;
+  float scale_log2;
+};
+
+// K tile: 128 rows (keys) x 128 B, chunk c of row r at c ^ ((r ^ (r >> 3)) & 7)
+__device__ __forceinline__ int kswz(int r, int c) { return r * 128 + ((c ^ ((r ^ (r >> 3)) & 7)) << 4); }
+// Vt tile: 128 rows (d) x 256 B, chunk c of row r at c ^ (r & 15)
+__device__ __forceinline__ int vswz(int r, int c) { return r * 256 + ((c ^ (r & 15)) << 4); }
+
+__global__ void __launch_bounds__(256, 1) attn_fwd_kernel(const FwdArgs a) {
+  __shared__ __attribute__((aligned(16))) int8_t klds[2][BLK * D];
+  __shared__ __attribute__((aligned(16))) int8_t vlds[2][D * BLK * 2];
+  const int h = blockIdx.y, qb = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, g = lane >> 5;
+  const int64_t q = static_cast<int64_t>(qb) * BLK + wave * 32 + l32;
+
+  v4i qf[4];
+  {
+    const int8_t* qp = a.q8 + (static_cast<int64_t>(h) * a.Sqpad + q) * D + g * 16;
+#pragma unroll
+    for (int ds = 0; ds < 4; ++ds) qf[ds] = *reinterpret_cast<const v4i*>(qp + ds * 32);
+  }
+  const float qscale = a.qs[static_cast<int64_t>(h) * (a.Sqpad / BLK) + qb] * a.scale_log2;
+
+  const int8_t* kbase = a.k8 + static_cast<int64_t>(h) * a.Skpad * D;
+  const uint16_t* vbase = a.vt + static_cast<int64_t>(h) * D * a.Skpad;
+  const float* ksb = a.ks + static_cast<int64_t>(h) * (a.Skpad / BLK);
+  uint4 sk0, sk1, sk2, sk3, sv0, sv1, sv2, sv3, sv4, sv5, sv6, sv7;
+  // V^T tile chunk id = tid + 256 * i: row d = id / 16 = tid / 16 + 16 * i, 16-byte chunk c = tid % 16
+  const int vd = tid >> 4, vc = tid & 15;
+  const uint16_t* vrow = vbase + static_cast<int64_t>(vd) * a.Skpad + vc * 8;
+  const int64_t vstep = 16 * a.Skpad;
+#define RH3_GLOAD(kt)                                                                   \
+  do {                                                                                  \
+    const int8_t* kp = kbase + static_cast<int64_t>(kt) * BLK * D + tid * 16;           \
+    sk0 = *reinterpret_cast<const uint4*>(kp);                                          \
+    sk1 = *reinterpret_cast<const uint4*>(kp + 4096);                                   \
+    sk2 = *reinterpret_cast<const uint4*>(kp + 8192);                                   \
+    sk3 = *reinterpret_cast<const uint4*>(kp + 12288);                                  \
+    const uint16_t* vp = vrow + static_cast<int64_t>(kt) * BLK;                         \
+    sv0 = *reinterpret_cast<const uint4*>(vp);                                          \
+    sv1 = *reinterpret_cast<const uint4*>(vp + vstep);                                  \
+    sv2 = *reinterpret_cast<const uint4*>(vp + 2 * vstep);                              \
+    sv3 = *reinterpret_cast<const uint4*>(vp + 3 * vstep);                              \
+    sv4 = *reinterpret_cast<const uint4*>(vp + 4 * vstep);                              \
+    sv5 = *reinterpret_cast<const uint4*>(vp + 5 * vstep);                              \
+    sv6 = *reinterpret_cast<const uint4*>(vp + 6 * vstep);                              \
+    sv7 = *reinterpret_cast<const uint4*>(vp + 7 * vstep);                              \
+  } while (0)
+  // K tile chunk id = tid + 256 * i: row = id / 8, chunk = id % 8
+#define RH3_SSTORE(st)                                                                  \
+  do {                                                                                  \
+    *reinterpret_cast<uint4*>(&klds[st][kswz((tid >> 3) + 0, tid & 7)]) = sk0;          \
+    *reinterpret_cast<uint4*>(&klds[st][kswz((tid >> 3) + 32, tid & 7)]) = sk1;         \
+    *reinterpret_cast<uint4*>(&klds[st][kswz((tid >> 3) + 64, tid & 7)]) = sk2;         \
+    *reinterpret_cast<uint4*>(&klds[st][kswz((tid >> 3) + 96, tid & 7)]) = sk3;         \
+    *reinterpret_cast<uint4*>(&vlds[st][vswz(vd + 0, vc)]) = sv0;                       \
+    *reinterpret_cast<uint4*>(&vlds[st][vswz(vd + 16, vc)]) = sv1;                      \
+    *reinterpret_cast<uint4*>(&vlds[st][vswz(vd + 32, vc)]) = sv2;                      \
+    *reinterpret_cast<uint4*>(&vlds[st][vswz(vd + 48, vc)]) = sv3;                      \
+    *reinterpret_cast<uint4*>(&vlds[st][vswz(vd + 64, vc)]) = sv4;                      \
+    *reinterpret_cast<uint4*>(&vlds[st][vswz(vd + 80, vc)]) = sv5;                      \
+    *reinterpret_cast<uint4*>(&vlds[st][vswz(vd + 96, vc)]) = sv6;                      \
+    *reinterpret_cast<uint4*>(&vlds[st][vswz(vd + 112, vc)]) = sv7;                     \
+  } while (0)
+
+  v16f o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[i][r] = 0.0f;
+  float mrow = -INFINITY, lrow = 0.0f;
+
+  const int nkt = static_cast<int>(a.Skpad / BLK);
+  RH3_GLOAD(0);
+  RH3_SSTORE(0);
+  __syncthreads();
+  for (int kt = 0; kt < nkt; ++kt) {
+    const int cur = kt & 1;
+    if (kt + 1 < nkt) RH3_GLOAD(kt + 1);
+    const int8_t* kl = klds[cur];
+    const int8_t* vl = vlds[cur];
+
+    v16i s[4];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[kb][r] = 0;
+#pragma unroll
+    for (int ds = 0; ds < 4; ++ds) {
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        const v4i kf = *reinterpret_cast<const v4i*>(kl + kswz(kb * 32 + l32, ds * 2 + g));
+        s[kb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf, qf[ds], s[kb], 0, 0, 0);
+      }
+    }
+
+    // scores in log2 units; keys past Sk (last tile only) are masked
+    const float c = qscale * ksb[kt];
+    float t[4][16];
+    float mx = -INFINITY;
+    const int64_t key0 = static_cast<int64_t>(kt) * BLK;
+    const bool tail = key0 + BLK > a.Sk;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float x = static_cast<float>(s[kb][r]) * c;
+        if (tail) {
+          const int64_t key = key0 + kb * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+          if (key >= a.Sk) x = -INFINITY;
+        }
+        t[kb][r] = x;
+        mx = fmaxf(mx, x);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float mnew = fmaxf(mrow, mx);
+    const float alpha = __builtin_amdgcn_exp2f(mrow - mnew);
+    mrow = mnew;
+    float lsum = 0.0f;
+    uint32_t pk[4][8];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; r += 2) {
+        const float p0 = round_bf(__builtin_amdgcn_exp2f(t[kb][r] - mnew));
+        const float p1 = round_bf(__builtin_amdgcn_exp2f(t[kb][r + 1] - mnew));
+        lsum = lsum + p0 + p1;
+        pk[kb][r >> 1] = (__float_as_uint(p0) >> 16) | (__float_as_uint(p1) & 0xffff0000u);
+      }
+    lrow = lrow * alpha + lsum;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[db][r] = o[db][r] * alpha;
+
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        v4i pw;
+        pw[0] = pk[kb][4 * m + 0]; pw[1] = pk[kb][4 * m + 1]; pw[2] = pk[kb][4 * m + 2]; pw[3] = pk[kb][4 * m + 3];
+        const v8bf pf = __builtin_bit_cast(v8bf, pw);
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+          const v4i vw = *reinterpret_cast<const v4i*>(vl + vswz(db * 32 + l32, kb * 4 + m * 2 + g));
+          const v8bf vf = __builtin_bit_cast(v8bf, vw);
+          o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, o[db], 0, 0, 0);
+        }
+      }
+    }
+    if (kt + 1 < nkt) RH3_SSTORE(cur ^ 1);
+    __syncthreads();
+  }
+#undef RH3_GLOAD
+#undef RH3_SSTORE
+
+  const float lt = lrow + __shfl_xor(lrow, 32, 64);
+  const float il = 1.0f / lt;
+  if (q < a.Sq) {
+    uint16_t* op = a.out + q * a.o_ss + static_cast<int64_t>(h) * a.o_sh;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int rq = 0; rq < 4; ++rq) {
+        const int d = db * 32 + 8 * rq + 4 * g;
+        uint2 w;
+        w.x = pack_bf2(o[db][4 * rq + 0] * il, o[db][4 * rq + 1] * il);
+        w.y = pack_bf2(o[db][4 * rq + 2] * il, o[db][4 * rq + 3] * il);
+        *reinterpret_cast<uint2*>(op + d) = w;
+      }
+  }
+}
+
+// ------------------------------------------------------------------ host
+int64_t pad(int64_t s) { return (s + BLK - 1) / BLK * BLK; }
+int64_t up256(int64_t b) { return (b + 255) / 256 * 256; }
+
+struct Work {
+  int8_t* q8; float* qs; int8_t* k8; float* ks; float* kmean; double* part; uint16_t* vt;
+  int64_t bytes;
+};
+
+Work layout(void* base, int64_t Sq, int64_t Sk, int64_t H) {
+  const int64_t sqp = pad(Sq), skp = pad(Sk), nchunk = (Sk + CHUNK - 1) / CHUNK;
+  char* p = static_cast<char*>(base);
+  int64_t off = 0;
+  Work w{};
+  auto take = [&](int64_t n) { char* r = p ? p + off : nullptr; off += up256(n); return r; };
+  w.q8 = reinterpret_cast<int8_t*>(take(H * sqp * D));
+  w.qs = reinterpret_cast<float*>(take(H * (sqp / BLK) * 4));
+  w.k8 = reinterpret_cast<int8_t*>(take(H * skp * D));
+  w.ks = reinterpret_cast<float*>(take(H * (skp / BLK) * 4));
+  w.kmean = reinterpret_cast<float*>(take(H * D * 4));
+  w.part = reinterpret_cast<double*>(take(H * nchunk * D * 8));
+  w.vt = reinterpret_cast<uint16_t*>(take(H * D * skp * 2));
+  w.bytes = off;
+  return w;
+}
+
+int check_qkv(const char* name, const uint16_t* q, int64_t q_ss, int64_t q_sh, const uint16_t* k, int64_t k_ss,
+              int64_t k_sh, const uint16_t* v, int64_t v_ss, int64_t v_sh, int64_t Sq, int64_t Sk, int64_t H) {
+  RH3_REQUIRE(Sq > 0 && Sk > 0 && H > 0, "%s: sizes must be positive (Sq=%lld Sk=%lld H=%lld)", name, (long long)Sq,
+              (long long)Sk, (long long)H);
+  RH3_REQUIRE(pad(Sq) / BLK < 65536 * 32768ll && H < 65536, "%s: grid too large", name);
+  RH3_REQUIRE(q && k && v, "%s: null q/k/v", name);
+  RH3_REQUIRE(aligned16(q) && aligned16(k) && aligned16(v), "%s: q/k/v must be 16-byte aligned", name);
+  RH3_REQUIRE(q_ss % 8 == 0 && q_sh % 8 == 0 && k_ss % 8 == 0 && k_sh % 8 == 0 && v_ss % 8 == 0 && v_sh % 8 == 0,
+              "%s: token/head strides must be multiples of 8 elements", name);
+  return RH3_OK;
+}
+
+int prepass(const uint16_t* q, int64_t q_ss, int64_t q_sh, const uint16_t* k, int64_t k_ss, int64_t k_sh,
+            const uint16_t* v, int64_t v_ss, int64_t v_sh, int64_t Sq, int64_t Sk, int64_t H, const RR& rq,
+            const RR& rk, int smooth_k, const Work& w, hipStream_t st) {
+  const int64_t sqp = pad(Sq), skp = pad(Sk);
+  const int nchunk = static_cast<int>((Sk + CHUNK - 1) / CHUNK);
+  const float* mean = nullptr;
+  if (smooth_k) {
+    hipLaunchKernelGGL(stats_kernel, dim3(nchunk, H), dim3(256), 0, st, k, k_ss, k_sh, Sk, rk, w.part);
+    hipLaunchKernelGGL(kmean_kernel, dim3(H), dim3(D), 0, st, w.part, nchunk, Sk, w.kmean);
+    mean = w.kmean;
+  } else {
+    // a fill kernel, not hipMemsetAsync, so the call stays safe inside a captured HIP graph
+    hipLaunchKernelGGL(zero_kernel, dim3((H * D + 255) / 256), dim3(256), 0, st, w.kmean, H * D);
+  }
+  hipLaunchKernelGGL(quant_kernel, dim3(sqp / BLK, H), dim3(256), 0, st, q, q_ss, q_sh, Sq, sqp, rq,
+                     static_cast<const float*>(nullptr), w.q8, w.qs);
+  hipLaunchKernelGGL(quant_kernel, dim3(skp / BLK, H), dim3(256), 0, st, k, k_ss, k_sh, Sk, skp, rk, mean, w.k8,
+                     w.ks);
+  hipLaunchKernelGGL(vt_kernel, dim3(skp / 64, H), dim3(256), 0, st, v, v_ss, v_sh, Sk, skp, w.vt);
+  return launch_status("attention prepass");
+}
+
+int forward(const Work& w, int64_t Sq, int64_t Sk, int64_t H, float scale, uint16_t* out, int64_t o_ss,
+            int64_t o_sh, hipStream_t st) {
+  FwdArgs f{w.q8, w.qs, w.k8, w.ks, w.vt, out, o_ss, o_sh, Sq, Sk, pad(Sq), pad(Sk),
+            scale * 1.4426950408889634f};
+  hipLaunchKernelGGL(attn_fwd_kernel, dim3(pad(Sq) / BLK, H), dim3(256), 0, st, f);
+  return launch_status("attention forward");
+}
+
+int check_rr(const char* name, const uint16_t* tab, int rot, const uint16_t* qw, const uint16_t* kw) {
+  RH3_REQUIRE(tab && qw && kw, "%s: tab, qw and kw are required", name);
+  RH3_REQUIRE(rot == 96 || rot == 128, "%s: rot_dim %d (96 or 128 supported)", name, rot);
+  RH3_REQUIRE(aligned16(tab) && aligned16(qw) && aligned16(kw), "%s: tab/qw/kw must be 16-byte aligned", name);
+  return RH3_OK;
+}
+
+}  // namespace
+}  // namespace rh3
+
+using namespace rh3;
+
+extern "C" int64_t rh3_attention_workspace_bytes(int64_t Sq, int64_t Sk, int64_t H) {
+  if (Sq <= 0 || Sk <= 0 || H <= 0) return 0;
+  return layout(nullptr, Sq, Sk, H).bytes;
+}
+
+extern "C" int rh3_attention_prepass(const uint16_t* q, int64_t q_ss, int64_t q_sh, const uint16_t* k, int64_t k_ss,
+                                     int64_t k_sh, const uint16_t* v, int64_t v_ss, int64_t v_sh, int64_t Sq,
+                                     int64_t Sk, int64_t H, const uint16_t* tab, int rot, const uint16_t* qw,
+                                     const uint16_t* kw, float eps, int smooth_k, void* workspace,
+                                     int64_t workspace_bytes, void** ptrs, hipStream_t stream) {
+  clear_error();
+  if (int e = check_qkv("attention_prepass", q, q_ss, q_sh, k, k_ss, k_sh, v, v_ss, v_sh, Sq, Sk, H)) return e;
+  RH3_REQUIRE(ptrs, "attention_prepass: ptrs required");
+  const Work w = layout(workspace, Sq, Sk, H);
+  RH3_REQUIRE(workspace && aligned16(workspace) && workspace_bytes >= w.bytes,
+              "attention_prepass: workspace %lld bytes < required %lld", (long long)workspace_bytes,
+              (long long)w.bytes);
+  RR rq{nullptr, nullptr, 0.f, 0}, rk{nullptr, nullptr, 0.f, 0};
+  if (tab) {
+    if (int e = check_rr("attention_prepass", tab, rot, qw, kw)) return e;
+    RH3_REQUIRE(Sq == Sk, "attention_prepass: RMSNorm+RoPE needs self-attention (Sq == Sk)");
+    rq = RR{tab, qw, eps, rot};
+    rk = RR{tab, kw, eps, rot};
+  }
+  if (int e = prepass(q, q_ss, q_sh, k, k_ss, k_sh, v, v_ss, v_sh, Sq, Sk, H, rq, rk, smooth_k, w, stream)) return e;
+  ptrs[0] = w.q8; ptrs[1] = w.qs; ptrs[2] = w.k8; ptrs[3] = w.ks; ptrs[4] = w.kmean; ptrs[5] = w.vt;
+  return RH3_OK;
+}
+
+extern "C" int rh3_int8_attention(const uint16_t* q, int64_t q_ss, int64_t q_sh, const uint16_t* k, int64_t k_ss,
+                                  int64_t k_sh, const uint16_t* v, int64_t v_ss, int64_t v_sh, int64_t Sq, int64_t Sk,
+                                  int64_t H, float scale, int smooth_k, uint16_t* out, int64_t o_ss, int64_t o_sh,
+                                  void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+  clear_error();
+  if (int e = check_qkv("int8_attention", q, q_ss, q_sh, k, k_ss, k_sh, v, v_ss, v_sh, Sq, Sk, H)) return e;
+  RH3_REQUIRE(out && (reinterpret_cast<uintptr_t>(out) & 7) == 0 && o_ss % 4 == 0 && o_sh % 4 == 0,
+              "int8_attention: out must be 8-byte aligned with strides multiple of 4");
+  const Work w = layout(workspace, Sq, Sk, H);
+  RH3_REQUIRE(workspace && aligned16(workspace) && workspace_bytes >= w.bytes,
+              "int8_attention: workspace %lld bytes < required %lld", (long long)workspace_bytes, (long long)w.bytes);
+  const RR none{nullptr, nullptr, 0.f, 0};
+  if (int e = prepass(q, q_ss, q_sh, k, k_ss, k_sh, v, v_ss, v_sh, Sq, Sk, H, none, none, smooth_k, w, stream))
+    return e;
+  return forward(w, Sq, Sk, H, scale, out, o_ss, o_sh, stream);
+}
+
+extern "C" int rh3_int8_attention_rr(const uint16_t* q, int64_t q_ss, int64_t q_sh, const uint16_t* k, int64_t k_ss,
+                                     int64_t k_sh, const uint16_t* v, int64_t v_ss, int64_t v_sh, int64_t S,
+                                     int64_t H, const uint16_t* tab, int rot, const uint16_t* qw, const uint16_t* kw,
+                                     float eps, float scale, int smooth_k, uint16_t* out, int64_t o_ss, int64_t o_sh,
+                                     void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+  clear_error();
+  if (int e = check_qkv("int8_attention_rr", q, q_ss, q_sh, k, k_ss, k_sh, v, v_ss, v_sh, S, S, H)) return e;
+  if (int e = check_rr("int8_attention_rr", tab, rot, qw, kw)) return e;
+  RH3_REQUIRE(out && (reinterpret_cast<uintptr_t>(out) & 7) == 0 && o_ss % 4 == 0 && o_sh % 4 == 0,
+              "int8_attention_rr: out must be 8-byte aligned with strides multiple of 4");
+  const Work w = layout(workspace, S, S, H);
+  RH3_REQUIRE(workspace && aligned16(workspace) && workspace_bytes >= w.bytes,
+              "int8_attention_rr: workspace %lld bytes < required %lld", (long long)workspace_bytes,
+              (long long)w.bytes);
+  const RR rq{tab, qw, eps, rot}, rk{tab, kw, eps, rot};
+  if (int e = prepass(q, q_ss, q_sh, k, k_ss, k_sh, v, v_ss, v_sh, S, S, H, rq, rk, smooth_k, w, stream)) return e;
+  return forward(w, S, S, H, scale, out, o_ss, o_sh, stream);
+}

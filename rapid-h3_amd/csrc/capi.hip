@@ -1,0 +1,34 @@
+// C-ABI plumbing shared by every entry point: the per-thread last-error message and launch checks.
+#include "rh3_common.hpp"
+
+namespace rh3 {
+
+namespace {
+thread_local std::string g_error;
+}
+
+void set_error(const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_error = buf;
+}
+
+void clear_error() { g_error.clear(); }
+
+int launch_status(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_error("%s: launch failed: %s", what, hipGetErrorString(e));
+    return RH3_ELAUNCH;
+  }
+  return RH3_OK;
+}
+
+}  // namespace rh3
+
+extern "C" const char* rh3_last_error(void) { return rh3::g_error.c_str(); }
+
+extern "C" int rh3_abi_version(void) { return 1; }

@@ -1,0 +1,322 @@
+// Per-token activation quantizers (HBM-bound, one read of the input, one write of the codes).
+//
+// One 64-lane wavefront owns one row: lane l loads the 16-byte chunks at columns 512*j + 8*l
+// (j = 0..NCH-1), so each load instruction of a wave covers 1 KiB of contiguous row. The row stays
+// in VGPRs between the absmax and the quantize step (the reference's Triton kernels read it twice,
+// triton_fp8.py:37-54). Row absmax by a wavefront butterfly; s = max(amax / QMAX, 1e-12);
+// q = round_half_even(v / s) with IEEE quotient semantics (kernels.py:75-82).
+//
+// Prologues (triton_fp8.py:128-148):
+//   KIND_PLAIN   v = x
+//   KIND_SWIGLU  v = (g * sigmoid(g)) * u, x = [g | u]
+//   KIND_NORMMOD v = ((x * rstd) * w) * (1 + scale[idx]) + shift[idx], rstd = 1/sqrt(sum x^2 / K + eps)
+//   KIND_HEADS   v = o[k / 128][m][k % 128] (head-major attention output gathered per token)
+// The RMSNorm sum of squares is accumulated per lane over (j, e) in order, then added across lanes by
+// a butterfly over distances 32..1; the CPU oracle (oracle/quant.py sumsq_rows) uses the same order.
+#include "rh3_common.hpp"
+
+namespace rh3 {
+namespace {
+
+enum Kind { KIND_PLAIN = 0, KIND_SWIGLU = 1, KIND_NORMMOD = 2, KIND_HEADS = 3 };
+
+struct QuantArgs {
+  const uint16_t* x;
+  int64_t ldx;       // row stride (PLAIN, SWIGLU, NORMMOD) or token stride (HEADS)
+  int64_t ld_head;   // HEADS: head stride
+  int64_t M, K;      // K = quantized width (SWIGLU: F; HEADS: H * 128)
+  const uint16_t* w; // NORMMOD weight or nullptr
+  float eps;
+  const int32_t* idx;
+  const void* shift;
+  const void* scale;
+  int64_t ld_tab;
+  void* q;
+  int64_t ldq;
+  float* s;
+};
+
+template <typename T> __device__ __forceinline__ float tab_load(const void* p, int64_t i);
+template <> __device__ __forceinline__ float tab_load<float>(const void* p, int64_t i) {
+  return static_cast<const float*>(p)[i];
+}
+template <> __device__ __forceinline__ float tab_load<uint16_t>(const void* p, int64_t i) {
+  return bf2f(static_cast<const uint16_t*>(p)[i]);
+}
+
+__device__ __forceinline__ float silu_mul(float g, float u) {
+  const float sig = 1.0f / (1.0f + __expf(-g));
+  return (g * sig) * u;
+}
+
+// OCP e4m3fn encode, round to nearest even, |t| <= 448 (the caller clamps)
+__device__ __forceinline__ uint32_t fp8_e4m3(float t) {
+  const uint32_t u = __float_as_uint(t);
+  const uint32_t sign = (u >> 24) & 0x80u;
+  const uint32_t a = u & 0x7fffffffu;
+  uint32_t code;
+  if (a < 0x3c800000u) {  // |t| < 2^-6: subnormal grid step 2^-9, exact scaling then rint
+    code = static_cast<uint32_t>(rintf(__uint_as_float(a) * 512.0f));
+  } else {
+    const uint32_t r = a + 0x7ffffu + ((a >> 20) & 1u);
+    code = (r >> 20) - 960u;  // (biased exponent - 120) << 3 | top 3 mantissa bits
+  }
+  return code | sign;
+}
+
+template <int KIND>
+__device__ __forceinline__ void load_chunk(const QuantArgs& a, int64_t m, int64_t c, float* v) {
+  if (KIND == KIND_HEADS) {
+    const uint16_t* p = a.x + (c >> 7) * a.ld_head + m * a.ldx + (c & 127);
+    unpack8(*reinterpret_cast<const uint4*>(p), v);
+  } else if (KIND == KIND_SWIGLU) {
+    const uint16_t* p = a.x + m * a.ldx + c;
+    float g[8], u[8];
+    unpack8(*reinterpret_cast<const uint4*>(p), g);
+    unpack8(*reinterpret_cast<const uint4*>(p + a.K), u);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = silu_mul(g[e], u[e]);
+  } else {
+    unpack8(*reinterpret_cast<const uint4*>(a.x + m * a.ldx + c), v);
+  }
+}
+
+// NCH = 512-column chunks held in registers per lane (row width <= 512 * NCH)
+template <int NCH, int KIND, bool FP8, typename TabT>
+__global__ void __launch_bounds__(256) quant_rows_kernel(const QuantArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t m = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (m >= a.M) return;
+  float v[NCH][8];
+#pragma unroll
+  for (int j = 0; j < NCH; ++j) {
+    const int64_t c = 512 * j + 8 * lane;
+    if (c < a.K) load_chunk<KIND>(a, m, c, v[j]);
+    else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[j][e] = 0.0f;
+    }
+  }
+  if (KIND == KIND_NORMMOD) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NCH; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss = ss + v[j][e] * v[j][e];
+    ss = wave_sum_tree(ss);
+    const float rstd = 1.0f / sqrtf(ss / static_cast<float>(a.K) + a.eps);
+    const int64_t t = static_cast<int64_t>(a.idx[m]) * a.ld_tab;
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      const int64_t c = 512 * j + 8 * lane;
+      if (c < a.K) {
+        float wv[8];
+        if (a.w) unpack8(*reinterpret_cast<const uint4*>(a.w + c), wv);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          float y = v[j][e] * rstd;
+          if (a.w) y = y * wv[e];
+          const float sc = tab_load<TabT>(a.scale, t + c + e);
+          const float sh = tab_load<TabT>(a.shift, t + c + e);
+          v[j][e] = y * (1.0f + sc) + sh;
+        }
+      }
+    }
+  }
+  float amax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NCH; ++j)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[j][e]));
+  amax = wave_max(amax);
+  const float qmax = FP8 ? 448.0f : 127.0f;
+  const float s = fmaxf(amax / qmax, 1e-12f);
+  const float inv = 1.0f / s;
+  if (lane == 0) a.s[m] = s;
+#pragma unroll
+  for (int j = 0; j < NCH; ++j) {
+    const int64_t c = 512 * j + 8 * lane;
+    if (c >= a.K) continue;
+    uint32_t b[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      if (FP8) {
+        const float t = fminf(fmaxf(v[j][e] / s, -448.0f), 448.0f);
+        b[e] = fp8_e4m3(t);
+      } else {
+        const float r = fminf(fmaxf(rint_div(v[j][e], s, inv), -127.0f), 127.0f);
+        b[e] = static_cast<uint32_t>(static_cast<int32_t>(r)) & 0xffu;
+      }
+    }
+    uint2 out;
+    out.x = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
+    out.y = b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24);
+    *reinterpret_cast<uint2*>(static_cast<int8_t*>(a.q) + m * a.ldq + c) = out;
+  }
+}
+
+// Rows wider than 8192: same arithmetic, re-reading the row (from L2) instead of holding it.
+template <int KIND, bool FP8, typename TabT>
+__global__ void __launch_bounds__(256) quant_rows_wide_kernel(const QuantArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t m = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (m >= a.M) return;
+  const int64_t nch = (a.K + 511) / 512;
+  float rstd = 0.0f;
+  int64_t t = 0;
+  if (KIND == KIND_NORMMOD) {
+    float ss = 0.0f;
+    for (int64_t j = 0; j < nch; ++j) {
+      const int64_t c = 512 * j + 8 * lane;
+      float v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+      if (c < a.K) load_chunk<KIND>(a, m, c, v);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss = ss + v[e] * v[e];
+    }
+    ss = wave_sum_tree(ss);
+    rstd = 1.0f / sqrtf(ss / static_cast<float>(a.K) + a.eps);
+    t = static_cast<int64_t>(a.idx[m]) * a.ld_tab;
+  }
+  auto value = [&](int64_t c, float* v) {
+    load_chunk<KIND>(a, m, c, v);
+    if (KIND == KIND_NORMMOD) {
+      float wv[8];
+      if (a.w) unpack8(*reinterpret_cast<const uint4*>(a.w + c), wv);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float y = v[e] * rstd;
+        if (a.w) y = y * wv[e];
+        v[e] = y * (1.0f + tab_load<TabT>(a.scale, t + c + e)) + tab_load<TabT>(a.shift, t + c + e);
+      }
+    }
+  };
+  float amax = 0.0f;
+  for (int64_t j = 0; j < nch; ++j) {
+    const int64_t c = 512 * j + 8 * lane;
+    if (c >= a.K) continue;
+    float v[8];
+    value(c, v);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[e]));
+  }
+  amax = wave_max(amax);
+  const float qmax = FP8 ? 448.0f : 127.0f;
+  const float s = fmaxf(amax / qmax, 1e-12f);
+  const float inv = 1.0f / s;
+  if (lane == 0) a.s[m] = s;
+  for (int64_t j = 0; j < nch; ++j) {
+    const int64_t c = 512 * j + 8 * lane;
+    if (c >= a.K) continue;
+    float v[8];
+    value(c, v);
+    uint32_t b[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      if (FP8) {
+        b[e] = fp8_e4m3(fminf(fmaxf(v[e] / s, -448.0f), 448.0f));
+      } else {
+        const float r = fminf(fmaxf(rint_div(v[e], s, inv), -127.0f), 127.0f);
+        b[e] = static_cast<uint32_t>(static_cast<int32_t>(r)) & 0xffu;
+      }
+    }
+    uint2 out;
+    out.x = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
+    out.y = b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24);
+    *reinterpret_cast<uint2*>(static_cast<int8_t*>(a.q) + m * a.ldq + c) = out;
+  }
+}
+
+template <int KIND, bool FP8, typename TabT>
+int launch(const QuantArgs& a, hipStream_t st, const char* name) {
+  if (a.M == 0) return RH3_OK;
+  const dim3 grid(static_cast<unsigned>((a.M + 3) / 4)), block(256);
+  const int64_t nch = (a.K + 511) / 512;
+  if (nch <= 1) hipLaunchKernelGGL((quant_rows_kernel<1, KIND, FP8, TabT>), grid, block, 0, st, a);
+  else if (nch <= 2) hipLaunchKernelGGL((quant_rows_kernel<2, KIND, FP8, TabT>), grid, block, 0, st, a);
+  else if (nch <= 4) hipLaunchKernelGGL((quant_rows_kernel<4, KIND, FP8, TabT>), grid, block, 0, st, a);
+  else if (nch <= 6) hipLaunchKernelGGL((quant_rows_kernel<6, KIND, FP8, TabT>), grid, block, 0, st, a);
+  else if (nch <= 8) hipLaunchKernelGGL((quant_rows_kernel<8, KIND, FP8, TabT>), grid, block, 0, st, a);
+  else if (nch <= 12) hipLaunchKernelGGL((quant_rows_kernel<12, KIND, FP8, TabT>), grid, block, 0, st, a);
+  else if (nch <= 16) hipLaunchKernelGGL((quant_rows_kernel<16, KIND, FP8, TabT>), grid, block, 0, st, a);
+  else hipLaunchKernelGGL((quant_rows_wide_kernel<KIND, FP8, TabT>), grid, block, 0, st, a);
+  return launch_status(name);
+}
+
+int check_common(const void* x, int64_t M, int64_t K, const void* q, int64_t ldq, const float* s) {
+  RH3_REQUIRE(M >= 0 && K >= 0, "quant: negative size (M=%lld, K=%lld)", (long long)M, (long long)K);
+  RH3_REQUIRE(K % 8 == 0, "quant: K=%lld must be a multiple of 8", (long long)K);
+  if (M == 0) return RH3_OK;
+  RH3_REQUIRE(K > 0, "quant: K must be positive");
+  RH3_REQUIRE(x && q && s, "quant: null pointer");
+  RH3_REQUIRE(ldq >= K && ldq % 8 == 0, "quant: output row stride %lld (K=%lld) must be >= K and a multiple of 8",
+              (long long)ldq, (long long)K);
+  RH3_REQUIRE(aligned16(x) && (reinterpret_cast<uintptr_t>(q) & 7) == 0, "quant: x must be 16-byte and q 8-byte aligned");
+  return RH3_OK;
+}
+
+}  // namespace
+}  // namespace rh3
+
+using namespace rh3;
+
+extern "C" int rh3_quant_rows_i8(const uint16_t* x, int64_t ldx, int64_t M, int64_t K, int8_t* q, int64_t ldq,
+                                 float* s, hipStream_t stream) {
+  clear_error();
+  if (int e = check_common(x, M, K, q, ldq, s)) return e;
+  RH3_REQUIRE(M == 0 || (ldx >= K && ldx % 8 == 0), "quant_rows_i8: row stride %lld invalid for K=%lld",
+              (long long)ldx, (long long)K);
+  QuantArgs a{x, ldx, 0, M, K, nullptr, 0.f, nullptr, nullptr, nullptr, 0, q, ldq, s};
+  return launch<KIND_PLAIN, false, float>(a, stream, "quant_rows_i8");
+}
+
+extern "C" int rh3_quant_rows_fp8(const uint16_t* x, int64_t ldx, int64_t M, int64_t K, uint8_t* q, int64_t ldq,
+                                  float* s, hipStream_t stream) {
+  clear_error();
+  if (int e = check_common(x, M, K, q, ldq, s)) return e;
+  RH3_REQUIRE(M == 0 || (ldx >= K && ldx % 8 == 0), "quant_rows_fp8: row stride %lld invalid for K=%lld",
+              (long long)ldx, (long long)K);
+  QuantArgs a{x, ldx, 0, M, K, nullptr, 0.f, nullptr, nullptr, nullptr, 0, q, ldq, s};
+  return launch<KIND_PLAIN, true, float>(a, stream, "quant_rows_fp8");
+}
+
+extern "C" int rh3_quant_norm_mod_i8(const uint16_t* x, int64_t ldx, int64_t M, int64_t K, const uint16_t* weight,
+                                     float eps, const int32_t* idx, const void* shift, const void* scale,
+                                     int tab_dtype, int64_t ld_tab, int8_t* q, int64_t ldq, float* s,
+                                     hipStream_t stream) {
+  clear_error();
+  if (int e = check_common(x, M, K, q, ldq, s)) return e;
+  if (M == 0) return RH3_OK;
+  RH3_REQUIRE(ldx >= K && ldx % 8 == 0, "quant_norm_mod_i8: row stride %lld invalid for K=%lld", (long long)ldx,
+              (long long)K);
+  RH3_REQUIRE(idx && shift && scale, "quant_norm_mod_i8: idx, shift and scale are required");
+  RH3_REQUIRE(ld_tab >= K, "quant_norm_mod_i8: table row stride %lld < K=%lld", (long long)ld_tab, (long long)K);
+  RH3_REQUIRE(!weight || aligned16(weight), "quant_norm_mod_i8: weight must be 16-byte aligned");
+  RH3_REQUIRE(tab_dtype == RH3_DTYPE_F32 || tab_dtype == RH3_DTYPE_BF16, "quant_norm_mod_i8: tab_dtype %d",
+              tab_dtype);
+  QuantArgs a{x, ldx, 0, M, K, weight, eps, idx, shift, scale, ld_tab, q, ldq, s};
+  if (tab_dtype == RH3_DTYPE_F32) return launch<KIND_NORMMOD, false, float>(a, stream, "quant_norm_mod_i8");
+  return launch<KIND_NORMMOD, false, uint16_t>(a, stream, "quant_norm_mod_i8");
+}
+
+extern "C" int rh3_quant_heads_i8(const uint16_t* o, int64_t H, int64_t M, int64_t ld_head, int64_t ld_row,
+                                  int8_t* q, int64_t ldq, float* s, hipStream_t stream) {
+  clear_error();
+  RH3_REQUIRE(H > 0, "quant_heads_i8: H=%lld", (long long)H);
+  if (int e = check_common(o, M, H * 128, q, ldq, s)) return e;
+  if (M == 0) return RH3_OK;
+  RH3_REQUIRE(ld_head % 8 == 0 && ld_row % 8 == 0 && ld_row >= 0 && ld_head >= 0,
+              "quant_heads_i8: strides must be multiples of 8 elements");
+  QuantArgs a{o, ld_row, ld_head, M, H * 128, nullptr, 0.f, nullptr, nullptr, nullptr, 0, q, ldq, s};
+  return launch<KIND_HEADS, false, float>(a, stream, "quant_heads_i8");
+}
+
+extern "C" int rh3_quant_swiglu_i8(const uint16_t* x, int64_t ldx, int64_t M, int64_t F, int8_t* q, int64_t ldq,
+                                   float* s, hipStream_t stream) {
+  clear_error();
+  if (int e = check_common(x, M, F, q, ldq, s)) return e;
+  if (M == 0) return RH3_OK;
+  RH3_REQUIRE(ldx >= 2 * F && ldx % 8 == 0, "quant_swiglu_i8: row stride %lld invalid for 2F=%lld", (long long)ldx,
+              (long long)(2 * F));
+  QuantArgs a{x, ldx, 0, M, F, nullptr, 0.f, nullptr, nullptr, nullptr, 0, q, ldq, s};
+  return launch<KIND_SWIGLU, false, float>(a, stream, "quant_swiglu_i8");
+}

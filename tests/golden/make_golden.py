@@ -1,0 +1,133 @@
+"""Write the golden fixtures in tests/golden/*.npz: seeded small inputs and the oracle's outputs.
+
+    python tests/golden/make_golden.py
+
+Inputs come from numpy's PCG64 (seeded), so they are the same on every machine; expected outputs
+come from the CPU oracle (oracle/), which tests/test_oracle.py pins independently against torch's
+CPU kernels, closed forms and invariants. The GPU tests load these files, so the GPU box needs
+neither the reference nor the oracle's run time to check the fixture cases.
+"""
+import os
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.dirname(os.path.dirname(HERE)))
+
+from oracle import attn as oa  # noqa: E402
+from oracle import gemm as og  # noqa: E402
+from oracle import quant as oq  # noqa: E402
+from oracle.numerics import f32_to_bf16  # noqa: E402
+
+
+def bf16(a):
+    return f32_to_bf16(np.asarray(a, np.float32))
+
+
+def outlier_acts(rng, m, k, frac=0.01, mult=20.0):
+    """C1/C2 activation recipe: N(0,1) with 1 % of channels scaled x20 (bench/int8_bench.py:39-40)."""
+    x = rng.standard_normal((m, k), dtype=np.float32)
+    idx = rng.permutation(k)[: max(1, int(round(frac * k)))]
+    x[:, idx] *= mult
+    return x
+
+
+def quant_case(rng):
+    x = outlier_acts(rng, 61, 3072)
+    x[3] = 0.0                                   # all-zero row -> s = 1e-12, q = 0
+    x[5, :] = 0.0
+    x[5, 0] = 127.0                              # s = 1 exactly; ties at k + 0.5 round to even
+    x[5, 1:9] = [0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 126.5, -126.5]
+    xb = bf16(x)
+    qi, si = oq.quantize_rows(xb, "int8_rowwise")
+    qf, sf = oq.quantize_rows(xb, "fp8_rowwise")
+    np.savez_compressed(os.path.join(HERE, "quant_rows.npz"), x=xb, q_i8=qi, s_i8=si, q_fp8=qf, s_fp8=sf)
+
+
+def norm_mod_case(rng):
+    m, k, r = 53, 3072, 3
+    x = bf16(outlier_acts(rng, m, k) * 3.0 + 0.5)
+    w = bf16(1.0 + 0.3 * rng.standard_normal(k))
+    idx = rng.integers(0, r, size=m).astype(np.int32)
+    shift = (0.1 * rng.standard_normal((r, k))).astype(np.float32)
+    scale = (0.2 * rng.standard_normal((r, k))).astype(np.float32)
+    q32, s32 = oq.norm_mod_quant_rows_i8(x, w, 1e-6, idx, shift, scale)
+    shb, scb = bf16(shift), bf16(scale)
+    qb, sb = oq.norm_mod_quant_rows_i8(x, w, 1e-6, idx, shb, scb)
+    qn, sn = oq.norm_mod_quant_rows_i8(x, None, 1e-6, idx, shift, scale)
+    np.savez_compressed(os.path.join(HERE, "norm_mod.npz"), x=x, w=w, idx=idx, shift=shift, scale=scale,
+                        q_f32=q32, s_f32=s32, shift_bf=shb, scale_bf=scb, q_bf=qb, s_bf=sb, q_now=qn, s_now=sn,
+                        eps=np.float32(1e-6))
+
+
+def heads_case(rng):
+    o = bf16(rng.standard_normal((24, 37, 128)) * np.exp(0.5 * rng.standard_normal((24, 1, 128))))
+    q, s = oq.heads_quant_rows_i8(o)
+    g = bf16(2.0 * rng.standard_normal((29, 2 * 1536)))
+    qs, ss = oq.swiglu_quant_rows_i8(g)
+    np.savez_compressed(os.path.join(HERE, "heads_swiglu.npz"), o=o, q=q, s=s, g=g, q_sw=qs, s_sw=ss)
+
+
+def gemm_case(rng):
+    m, n, k = 300, 264, 320                      # ragged M and N against the 256 x 256 tile
+    x = bf16(outlier_acts(rng, m, k))
+    w = bf16(0.02 * rng.standard_normal((n, k)))
+    xq, xs = oq.quantize_rows(x, "int8_rowwise")
+    wq, ws = oq.quantize_weight(w, "int8_rowwise")
+    bias = bf16(0.1 * rng.standard_normal(n))
+    acc = og.int8_acc(xq, wq)
+    out = og.int8_gemm(xq, xs, wq, ws)
+    out_b = og.int8_gemm(xq, xs, wq, ws, bias)
+    gate = bf16(rng.standard_normal(n))
+    resid = bf16(rng.standard_normal((m, n)))
+    gated = og.int8_gemm_gated_residual(xq, xs, wq, ws, gate, resid)
+    n2 = 512
+    w1 = bf16(0.02 * rng.standard_normal((n2, k)))
+    w1q, w1s = oq.quantize_weight(w1, "int8_rowwise")
+    perm = og.swiglu_perm(n2)
+    h = og.int8_gemm_swiglu(xq, xs, w1q[perm], w1s[:, perm])
+    fq, fs = oq.quantize_rows(x, "fp8_rowwise")
+    fwq, fws = oq.quantize_weight(w, "fp8_rowwise")
+    fout = og.fp8_gemm(fq, fs, fwq, fws)
+    np.savez_compressed(os.path.join(HERE, "gemm.npz"), x=x, w=w, xq=xq, xs=xs, wq=wq, ws=ws, bias=bias, acc=acc,
+                        out=out, out_bias=out_b, gate=gate, resid=resid, gated=gated, w1=w1, w1q=w1q, w1s=w1s,
+                        perm=perm, h=h, fq=fq, fs=fs, fwq=fwq, fws=fws, fout=fout)
+
+
+def attn_case(rng):
+    s, h = 300, 2
+    q = bf16(rng.standard_normal((s, h, 128)))
+    k = bf16(rng.standard_normal((s, h, 128)) + 2.0 * rng.standard_normal((1, h, 128)))
+    v = bf16(rng.standard_normal((s, h, 128)))
+    q8, qs, k8, ks, km = oa.prepass(q, k)
+    out = oa.attention_from_codes(q8, qs, k8, ks, v, 128 ** -0.5)[:s]
+    tab = bf16(oa.rope_table(np.arange(s) % 37, rot=96).reshape(s, 48, 2, 2))
+    qw = bf16(1.0 + 0.3 * rng.standard_normal(128))
+    kw = bf16(1.0 + 0.3 * rng.standard_normal(128))
+    rq8, rqs, rk8, rks, rkm = oa.prepass(q, k, rr=(tab, qw, kw, 1e-5))
+    rout = oa.attention_from_codes(rq8, rqs, rk8, rks, v, 128 ** -0.5)[:s]
+    # cross-attention: 300 queries over 200 keys
+    kc = k[:200]
+    vc = v[:200]
+    cq8, cqs, ck8, cks, ckm = oa.prepass(q, kc)
+    cout = oa.attention_from_codes(cq8, cqs, ck8, cks, vc, 128 ** -0.5)[:s]
+    np.savez_compressed(os.path.join(HERE, "attention.npz"), q=q, k=k, v=v, q8=q8, qs=qs, k8=k8, ks=ks, kmean=km,
+                        out=out, tab=tab, qw=qw, kw=kw, rq8=rq8, rqs=rqs, rk8=rk8, rks=rks, rkmean=rkm, rout=rout,
+                        ck8=ck8, cks=cks, ckmean=ckm, cout=cout)
+
+
+def main():
+    rng = np.random.default_rng(0)
+    quant_case(rng)
+    norm_mod_case(rng)
+    heads_case(rng)
+    gemm_case(rng)
+    attn_case(rng)
+    for f in sorted(os.listdir(HERE)):
+        if f.endswith(".npz"):
+            print(f, os.path.getsize(os.path.join(HERE, f)))
+
+
+if __name__ == "__main__":
+    main()

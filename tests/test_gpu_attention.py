@@ -1,0 +1,143 @@
+"""GPU parity of the INT8 attention (librh3 rh3_int8_attention*, rh3_attention_prepass) against the CPU
+oracle: bit-exact Q/K int8 codes, per-block scales and kmean; V^T layout exact; output within
+rel-L2 1e-2 of the oracle's float64 attention on the same int8 operands."""
+import numpy as np
+import pytest
+
+from conftest import to_dev, to_np
+from oracle import attn as oa
+from oracle.gemm import rel_l2
+from oracle.numerics import bf16_to_f32, f32_to_bf16
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-2
+
+
+def _bf(a):
+    return f32_to_bf16(np.asarray(a, np.float32))
+
+
+def _perm_keys(skp):
+    """Key held at each position of the V^T layout (keys permuted inside 32-key groups)."""
+    p = np.arange(skp)
+    w = p & 31
+    m, g, e = w >> 4, (w >> 3) & 1, w & 7
+    return (p & ~31) + 16 * m + 8 * (e >> 2) + 4 * g + (e & 3)
+
+
+def _check_prepass(pp, q8, qs, k8, ks, km, v, s):
+    assert np.array_equal(to_np(pp["q8"]), q8)
+    assert np.array_equal(to_np(pp["qs"]), qs)
+    assert np.array_equal(to_np(pp["k8"]), k8)
+    assert np.array_equal(to_np(pp["ks"]), ks)
+    assert np.array_equal(to_np(pp["kmean"]), km)
+    vt = to_np(pp["vt"])                                   # [H, 128, Skpad]
+    keys = _perm_keys(vt.shape[2])
+    vpad = np.zeros((vt.shape[2],) + v.shape[1:], np.uint16)
+    vpad[:s] = v
+    assert np.array_equal(vt, vpad[keys].transpose(1, 2, 0))
+
+
+def test_attention_golden(dev, golden):
+    from rapid_h3 import attention
+    g = golden("attention")
+    q, k, v = (to_dev(g[n], dev) for n in ("q", "k", "v"))
+    pp = attention.prepass(q, k, v)
+    _check_prepass(pp, g["q8"], g["qs"], g["k8"], g["ks"], g["kmean"], g["v"], g["v"].shape[0])
+    out = bf16_to_f32(to_np(attention.attention(q, k, v)))
+    assert rel_l2(out, g["out"]) < TOL
+
+
+def test_attention_rr_golden(dev, golden):
+    import torch
+    from rapid_h3 import attention
+    g = golden("attention")
+    q, k, v = (to_dev(g[n], dev) for n in ("q", "k", "v"))
+    s = g["q"].shape[0]
+    tab = to_dev(g["tab"], dev).view(1, s, 1, 48, 2, 2)
+    qw, kw = to_dev(g["qw"], dev), to_dev(g["kw"], dev)
+    pp = attention.prepass(q, k, v, tab, qw, kw, 1e-5)
+    _check_prepass(pp, g["rq8"], g["rqs"], g["rk8"], g["rks"], g["rkmean"], g["v"], s)
+    q0, k0 = q.clone(), k.clone()
+    out = attention.attention_rr(q, k, v, tab, qw, kw, 1e-5)
+    assert torch.equal(q, q0) and torch.equal(k, k0)        # q, k untouched
+    assert rel_l2(bf16_to_f32(to_np(out)), g["rout"]) < TOL
+
+
+def test_cross_attention_golden(dev, golden):
+    from rapid_h3 import attention
+    g = golden("attention")
+    q = to_dev(g["q"], dev)
+    k = to_dev(g["k"][:200], dev)
+    v = to_dev(g["v"][:200], dev)
+    pp = attention.prepass(q, k, v)
+    assert np.array_equal(to_np(pp["k8"]), g["ck8"]) and np.array_equal(to_np(pp["ks"]), g["cks"])
+    out = bf16_to_f32(to_np(attention.attention(q, k, v)))
+    assert rel_l2(out, g["cout"]) < TOL
+
+
+@pytest.mark.parametrize("sq,sk,h", [(1, 1, 1), (129, 129, 3), (77, 512, 2), (1000, 257, 1)])
+def test_attention_ragged(dev, sq, sk, h):
+    from rapid_h3 import attention
+    rng = np.random.default_rng(sq * 7 + sk * 3 + h)
+    q = _bf(rng.standard_normal((sq, h, 128)))
+    k = _bf(rng.standard_normal((sk, h, 128)) + 2.0 * rng.standard_normal((1, h, 128)))
+    v = _bf(rng.standard_normal((sk, h, 128)))
+    out = bf16_to_f32(to_np(attention.attention(to_dev(q, dev), to_dev(k, dev), to_dev(v, dev))))
+    q8, qs, k8, ks, _ = oa.prepass(q, k)
+    ref = oa.attention_from_codes(q8, qs, k8, ks, v, 128 ** -0.5)[:sq]
+    assert rel_l2(out, ref) < TOL
+
+
+def test_attention_strided_out(dev):
+    """q/k/v as views of one [S, 3*H*128] qkv buffer; output into a head-major [1, H, S, D] buffer
+    through out=o[0].transpose(0, 1) (the _fused_block call, __init__.py:283-291)."""
+    import torch
+    from rapid_h3 import attention
+    s, h = 700, 4
+    rng = np.random.default_rng(11)
+    buf = _bf(rng.standard_normal((s, 3 * h * 128)))
+    bt = to_dev(buf, dev)
+    q, k, v = (t.view(s, h, 128) for t in bt.split(h * 128, dim=-1))
+    o = torch.empty(1, h, s, 128, dtype=torch.bfloat16, device=dev)
+    attention.attention(q, k, v, out=o[0].transpose(0, 1))
+    b = buf.reshape(s, 3, h, 128)
+    q8, qs, k8, ks, _ = oa.prepass(b[:, 0], b[:, 1])
+    ref = oa.attention_from_codes(q8, qs, k8, ks, b[:, 2], 128 ** -0.5)[:s]
+    got = bf16_to_f32(to_np(o[0].transpose(0, 1)))
+    assert rel_l2(got, ref) < TOL
+
+
+def test_attention_full_size_sampled(dev):
+    """C4: S = 145,152, H = 24, D = 128 with a per-head K offset ~ N(0, 2). Codes, scales and kmean of 2
+    sampled heads bit-exact; output on 48 sampled query rows x those heads within tolerance, and
+    against the unquantized float64 attention within 3 %."""
+    import torch
+    from rapid_h3 import attention
+    s, h = 145152, 24
+    gen = torch.Generator(device="cpu").manual_seed(0)
+    q = torch.randn(s, h, 128, generator=gen).to(torch.bfloat16)
+    k = (torch.randn(s, h, 128, generator=gen) + 2.0 * torch.randn(1, h, 128, generator=gen)).to(torch.bfloat16)
+    v = torch.randn(s, h, 128, generator=gen).to(torch.bfloat16)
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    pp = attention.prepass(qd, kd, vd)
+    out = attention.attention(qd, kd, vd)
+    heads = [3, 17]
+    rows = np.sort(np.random.default_rng(3).choice(s, 48, replace=False))
+    qn = q.view(torch.int16).numpy().view(np.uint16)
+    kn = k.view(torch.int16).numpy().view(np.uint16)
+    vn = v.view(torch.int16).numpy().view(np.uint16)
+    for hh in heads:
+        q8, qs, k8, ks, km = oa.prepass(qn[:, hh:hh + 1], kn[:, hh:hh + 1])
+        assert np.array_equal(to_np(pp["q8"][hh]), q8[0])
+        assert np.array_equal(to_np(pp["qs"][hh]), qs[0])
+        assert np.array_equal(to_np(pp["k8"][hh]), k8[0])
+        assert np.array_equal(to_np(pp["ks"][hh]), ks[0])
+        assert np.array_equal(to_np(pp["kmean"][hh]), km[0])
+        ref = oa.attention_from_codes(q8, qs, k8, ks, vn[:, hh:hh + 1], 128 ** -0.5, rows=rows)[:, 0]
+        got = bf16_to_f32(to_np(out[torch.from_numpy(rows).to(dev), hh]))
+        assert rel_l2(got, ref) < TOL
+        exact = oa.attention_exact(qn[:, hh:hh + 1], kn[:, hh:hh + 1], vn[:, hh:hh + 1], 128 ** -0.5,
+                                   rows=rows)[:, 0]
+        assert rel_l2(got, exact) < 0.03

@@ -1,0 +1,115 @@
+"""GPU parity of the W8A8 / FP8 GEMMs (librh3 rh3_gemm_*) against the CPU oracle: bit-exact int32
+accumulators and bf16 epilogue outputs for int8 (SwiGLU: exp-dependent, within one bf16 ulp);
+FP8 within rel-L2 1e-2 of the exact-product emulation."""
+import numpy as np
+import pytest
+
+from conftest import to_dev, to_np
+from oracle import gemm as og
+from oracle import quant as oq
+from oracle.numerics import bf16_to_f32, f32_to_bf16
+
+pytestmark = pytest.mark.gpu
+
+
+def _bf(a):
+    return f32_to_bf16(np.asarray(a, np.float32))
+
+
+def _bf16_ulps(a, b):
+    """Distance in bf16 ulps between two bf16 bit arrays of finite values."""
+    def key(u):
+        u = u.astype(np.int32)
+        return np.where(u & 0x8000, -(u & 0x7FFF), u)
+    return np.abs(key(a) - key(b))
+
+
+def test_gemm_golden(dev, golden):
+    from rapid_h3 import gemm
+    g = golden("gemm")
+    xq, xs = to_dev(g["xq"], dev), to_dev(g["xs"], dev)
+    wq, ws = to_dev(g["wq"], dev), to_dev(g["ws"], dev)
+    assert np.array_equal(to_np(gemm.int8_gemm_acc(xq, wq)), g["acc"])
+    assert np.array_equal(to_np(gemm.int8_gemm(xq, xs, wq, ws)), g["out"])
+    assert np.array_equal(to_np(gemm.int8_gemm(xq, xs, wq, ws, bias=to_dev(g["bias"], dev))), g["out_bias"])
+    resid = to_dev(g["resid"], dev)
+    r = gemm.int8_gemm_gated_residual(xq, xs, wq, ws, to_dev(g["gate"], dev), resid)
+    assert r is resid
+    assert np.array_equal(to_np(resid), g["gated"])
+
+
+def test_swiglu_golden(dev, golden):
+    from rapid_h3 import gemm
+    g = golden("gemm")
+    xq, xs = to_dev(g["xq"], dev), to_dev(g["xs"], dev)
+    perm = to_dev(g["perm"].astype(np.int64), dev)
+    assert np.array_equal(to_np(gemm.swiglu_perm(512, dev)), g["perm"])
+    w1q, w1s = to_dev(g["w1q"], dev), to_dev(g["w1s"], dev)
+    h = to_np(gemm.int8_gemm_swiglu(xq, xs, w1q[perm].contiguous(), w1s[:, perm].contiguous()))
+    d = _bf16_ulps(h, g["h"])
+    assert d.max() <= 1 and (d > 0).mean() < 0.01
+
+
+def test_fp8_golden(dev, golden):
+    from rapid_h3 import gemm
+    g = golden("gemm")
+    out = gemm.fp8_gemm(to_dev(g["fq"], dev, "fp8"), to_dev(g["fs"], dev), to_dev(g["fwq"], dev, "fp8"),
+                        to_dev(g["fws"], dev))
+    got = bf16_to_f32(to_np(out))
+    assert og.rel_l2(got, bf16_to_f32(g["fout"])) < 1e-2
+    # and against the bf16 product of the unquantized operands (the reference's error metric)
+    ref = bf16_to_f32(g["x"]).astype(np.float64) @ bf16_to_f32(g["w"]).astype(np.float64).T
+    assert og.rel_l2(got, ref) < 0.08
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 8, 64), (17, 40, 128), (256, 256, 64), (513, 264, 1024), (64, 520, 8192),
+                                   (1000, 3072, 3072)])
+def test_gemm_shapes(dev, m, n, k):
+    from rapid_h3 import gemm
+    rng = np.random.default_rng(m + 7 * n + 13 * k)
+    xq = rng.integers(-127, 128, size=(m, k), dtype=np.int8)
+    wq = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
+    xs = (rng.random((m, 1)) * 1e-3).astype(np.float32)
+    ws = (rng.random((1, n)) * 1e-3).astype(np.float32)
+    xt, wt = to_dev(xq, dev), to_dev(wq, dev)
+    assert np.array_equal(to_np(gemm.int8_gemm_acc(xt, wt)), og.int8_acc(xq, wq))
+    out = gemm.int8_gemm(xt, to_dev(xs, dev), wt, to_dev(ws, dev))
+    assert np.array_equal(to_np(out), og.int8_gemm(xq, xs, wq, ws))
+
+
+def test_gemm_rejects_bad_shapes(dev):
+    import torch
+    from rapid_h3 import gemm
+    xq = torch.zeros(4, 96, dtype=torch.int8, device=dev)
+    wq = torch.zeros(8, 96, dtype=torch.int8, device=dev)
+    with pytest.raises(RuntimeError, match="multiple of 64"):
+        gemm.int8_gemm(xq, torch.ones(4, 1, device=dev), wq, torch.ones(1, 8, device=dev))
+    with pytest.raises(RuntimeError):
+        gemm.int8_gemm(xq[:, :64], torch.ones(4, 1, device=dev), wq[:7, :64], torch.ones(1, 7, device=dev))
+
+
+def test_gemm_full_size_qkv(dev):
+    """C2 QKV at M = 145,152, N = 9216, K = 3072: int32 accumulators bit-exact on 256 sampled rows, the
+    bf16 output on the same rows, and an exact checksum of checksums over every accumulator:
+    sum_m acc[m, n] == sum_k (sum_m xq[m, k]) * wq[n, k]."""
+    import torch
+    from rapid_h3 import gemm, quant
+    m, n, k = 145152, 9216, 3072
+    gen = torch.Generator(device="cpu").manual_seed(0)
+    x = torch.randn(m, k, generator=gen)
+    x[:, torch.randperm(k, generator=gen)[:31]] *= 20
+    xt = x.to(torch.bfloat16).to(dev)
+    del x
+    w = (torch.randn(n, k, generator=gen) * 0.02).to(torch.bfloat16).to(dev)
+    xq, xs = quant.quant_rows_i8(xt)
+    wq, ws = quant.quant_rows_i8(w)
+    acc = gemm.int8_gemm_acc(xq, wq)
+    out = gemm.int8_gemm(xq, xs, wq, ws.t())
+    rows = torch.from_numpy(np.sort(np.random.default_rng(2).choice(m, 256, replace=False))).to(dev)
+    xr = to_np(xq[rows])
+    wn = to_np(wq)
+    assert np.array_equal(to_np(acc[rows]), og.int8_acc(xr, wn))
+    assert np.array_equal(to_np(out[rows]), og.int8_gemm(xr, to_np(xs[rows]), wn, to_np(ws).T))
+    lhs = acc.double().sum(dim=0)
+    rhs = wq.double() @ xq.double().sum(dim=0)
+    assert bool(torch.equal(lhs, rhs))
