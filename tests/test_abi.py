@@ -1,0 +1,104 @@
+"""CPU tests of the C-ABI boundary and the host logic: librh3.so loads without a GPU, exports every
+function include/rh3.h declares with the ctypes signatures the host uses, and rejects bad arguments
+with a message before touching the device."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def header_functions():
+    text = open(os.path.join(ROOT, "include", "rh3.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(rh3_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_symbols_exported_and_bound():
+    from rapid_h3 import _native
+    lib = _native.lib()
+    names = header_functions()
+    assert len(names) >= 16
+    for n in names:
+        assert hasattr(lib, n), n
+        assert n in _native.SIGNATURES, f"{n} declared in rh3.h but not bound in _native"
+    assert set(_native.SIGNATURES) == set(names)
+    assert lib.rh3_abi_version() == 1
+
+
+def test_argument_validation_without_gpu():
+    from rapid_h3 import _native as nat
+    lib = nat.lib()
+    fake = ctypes.c_void_p(0x1000)          # never dereferenced: validation fails first
+    st = lib.rh3_gemm_i8(fake, 96, fake, fake, 96, fake, None, fake, 16, 4, 16, 96, None)
+    assert st == 1 and "multiple of 64" in nat.last_error()
+    st = lib.rh3_gemm_i8(fake, 64, fake, fake, 64, fake, None, fake, 16, 4, 12, 64, None)
+    assert st == 1 and "multiple of 8" in nat.last_error()
+    st = lib.rh3_quant_rows_i8(fake, 12, 4, 12, fake, 16, fake, None)
+    assert st == 1 and "multiple of 8" in nat.last_error()
+    st = lib.rh3_quant_norm_mod_i8(fake, 64, 4, 64, None, 1e-6, None, None, None, 2, 64, fake, 64, fake, None)
+    assert st == 1 and "idx, shift and scale" in nat.last_error()
+    st = lib.rh3_int8_attention(fake, 128, 128, fake, 128, 128, fake, 128, 128, 10, 10, 1, 0.1, 1, fake, 128, 128,
+                                fake, 16, None)
+    assert st == 1 and "workspace" in nat.last_error()
+    st = lib.rh3_int8_attention_rr(fake, 128, 128, fake, 128, 128, fake, 128, 128, 10, 1, fake, 64, fake, fake,
+                                   1e-5, 0.1, 1, fake, 128, 128, fake, 1 << 30, None)
+    assert st == 1 and "rot_dim" in nat.last_error()
+    with pytest.raises(RuntimeError, match="multiple of 64"):
+        nat.call("rh3_gemm_i8", fake, 96, fake, fake, 96, fake, None, fake, 16, 4, 16, 96, None)
+
+
+def test_empty_inputs_are_no_ops():
+    from rapid_h3 import _native as nat
+    lib = nat.lib()
+    assert lib.rh3_quant_rows_i8(None, 0, 0, 64, None, 64, None, None) == 0
+    assert lib.rh3_gemm_i8(None, 64, None, None, 64, None, None, None, 8, 0, 8, 64, None) == 0
+
+
+def test_workspace_size_matches_layout():
+    from rapid_h3 import _native as nat
+    lib = nat.lib()
+    s, h = 145152, 24
+    n = lib.rh3_attention_workspace_bytes(s, s, h)
+    sp = (s + 127) // 128 * 128
+    nchunk = (s + 255) // 256
+    expect = 2 * h * sp * 128 + 2 * h * (sp // 128) * 4 + h * 128 * 4 + h * nchunk * 128 * 8 + h * 128 * sp * 2
+    assert expect <= n < expect + 7 * 256
+    assert lib.rh3_attention_workspace_bytes(0, 5, 1) == 0
+
+
+def test_host_wrappers_refuse_cpu_tensors():
+    import torch
+    from rapid_h3 import attention, gemm, quant
+    x = torch.zeros(4, 64, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="GPU"):
+        quant.quant_rows_i8(x)
+    with pytest.raises(RuntimeError, match="GPU"):
+        gemm.int8_gemm(torch.zeros(4, 64, dtype=torch.int8), torch.ones(4, 1), torch.zeros(8, 64, dtype=torch.int8),
+                       torch.ones(1, 8))
+    q = torch.zeros(8, 2, 128, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="GPU"):
+        attention.attention(q, q, q)
+    with pytest.raises(RuntimeError, match="128"):
+        attention.attention(q[..., :64], q[..., :64], q[..., :64])
+
+
+def test_dropin_modules_keep_reference_names():
+    from rapid_h3 import attn_int8, cutlass_fp8, kernels, triton_fp8
+    for mod, names in ((kernels, ["QWeight", "quantize_weight", "quantize_rows", "linear", "gemm_config"]),
+                       (cutlass_fp8, ["ext", "fp8_gemm", "int8_gemm", "int8_gemm_qkv_prep", "int8_gemm_gated_residual",
+                                      "swiglu_perm", "int8_gemm_swiglu"]),
+                       (triton_fp8, ["quant_rows_i8", "quant_rows", "rot_quant_rows_i8", "rot_quant_heads_i8",
+                                     "swiglu_rot_quant_rows_i8", "norm_mod_rot_quant_rows_i8", "convrot",
+                                     "regular_hadamard", "ROT_GROUP"]),
+                       (attn_int8, ["ext", "attention", "attention_bhsd", "attention_rr", "attention_pre",
+                                    "attention_rr_bias"])):
+        for n in names:
+            assert hasattr(mod, n), f"{mod.__name__}.{n}"
+    import torch
+    p = cutlass_fp8.swiglu_perm(16, "cpu")
+    assert p.tolist() == [0, 1, 2, 3, 8, 9, 10, 11, 4, 5, 6, 7, 12, 13, 14, 15]
+    with pytest.raises(ValueError):
+        kernels.quantize_rows(torch.zeros(2, 8, dtype=torch.bfloat16), "bogus")

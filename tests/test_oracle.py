@@ -1,0 +1,357 @@
+"""CPU tests that pin the oracle (oracle/) independently of its own formulas.
+
+The reference holds no golden tensors for this path (its tests are torch.equal checks between CUDA
+kernels), so each oracle function is pinned by something it does not share code with:
+  * torch's CPU kernels for the same operations (bf16 / e4m3fn casts, division + round, _int_mm,
+    addcmul_, silu, scaled_dot_product_attention);
+  * closed forms and invariants (absmax code 127, |x - q s| <= s/2, ties to even, zero rows, RoPE
+    at angle 0, rotation preserves pair norms, softmax shift invariance under K smoothing);
+  * brute-force scalar loops on tiny inputs (the stated reduction orders).
+A planted mistake (dropped term, wrong index, transposed operand, wrong rounding) fails at least one.
+"""
+import math
+import struct
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attn as oa
+from oracle import gemm as og
+from oracle import quant as oq
+from oracle.numerics import bf16_to_f32, f32_to_bf16, f32_to_fp8_e4m3, fp8_e4m3_to_f32, round_bf16
+
+
+def t_bf16(u16):
+    return torch.from_numpy(np.ascontiguousarray(u16).view(np.int16)).view(torch.bfloat16)
+
+
+def np_bf16(t):
+    return t.contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def f32(x):
+    """Round a Python float to fp32 (double rounding is exact for +,-,*,/ of fp32 operands)."""
+    return struct.unpack("f", struct.pack("f", x))[0]
+
+
+def rb(x):
+    """Round a Python float (an fp32 value) to bf16, as a Python float."""
+    return float(round_bf16(np.array([x], np.float32))[0])
+
+
+# ----------------------------------------------------------------------------- number formats
+def test_bf16_matches_torch():
+    rng = np.random.default_rng(0)
+    x = np.concatenate([rng.standard_normal(100000).astype(np.float32) * 10 ** rng.uniform(-30, 30, 100000),
+                        np.array([0.0, -0.0, np.inf, -np.inf, 1e-45, 3.4e38], np.float32)]).astype(np.float32)
+    ours = f32_to_bf16(x)
+    theirs = np_bf16(torch.from_numpy(x).to(torch.bfloat16))
+    assert np.array_equal(ours, theirs)
+    assert np.array_equal(bf16_to_f32(ours), t_bf16(ours).float().numpy())
+
+
+def test_fp8_matches_torch_exhaustive():
+    # every bf16 value in [-448, 448] plus random fp32 values: RNE with subnormals, as torch casts
+    allb = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    v = bf16_to_f32(allb)
+    v = v[np.isfinite(v) & (np.abs(v) <= 448)]
+    rng = np.random.default_rng(1)
+    r = (rng.uniform(-448, 448, 200000) * 10 ** rng.uniform(-6, 0, 200000)).astype(np.float32)
+    x = np.concatenate([v, r]).astype(np.float32)
+    ours = f32_to_fp8_e4m3(x)
+    theirs = torch.from_numpy(x).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(ours, theirs)
+    codes = np.arange(256, dtype=np.uint8)
+    dec = fp8_e4m3_to_f32(codes)
+    tdec = torch.from_numpy(codes).view(torch.float8_e4m3fn).float().numpy()
+    ok = ~np.isnan(tdec)
+    assert np.array_equal(dec[ok], tdec[ok]) and np.isnan(dec[~ok]).all()
+    with pytest.raises(ValueError):
+        f32_to_fp8_e4m3(np.array([449.0], np.float32))
+
+
+# ----------------------------------------------------------------------------- quantizers
+def _torch_quant_rows(xb, fp8):
+    """kernels.quantize_rows (kernels.py:75-82) in torch CPU ops."""
+    x = t_bf16(xb)
+    amax = x.abs().amax(dim=-1, keepdim=True).float()
+    if fp8:
+        s = (amax / 448.0).clamp_min(1e-12)
+        return (x.float() / s).clamp(-448.0, 448.0).to(torch.float8_e4m3fn).view(torch.uint8).numpy(), s.numpy()
+    s = (amax / 127.0).clamp_min(1e-12)
+    return (x.float() / s).round().clamp(-127, 127).to(torch.int8).numpy(), s.numpy()
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+def test_quantize_rows_matches_torch(fp8, golden):
+    g = golden("quant_rows")
+    q, s = oq.quantize_rows(g["x"], "fp8_rowwise" if fp8 else "int8_rowwise")
+    tq, ts = _torch_quant_rows(g["x"], fp8)
+    assert np.array_equal(q, tq) and np.array_equal(s, ts)
+    assert np.array_equal(q, g["q_fp8" if fp8 else "q_i8"]) and np.array_equal(s, g["s_fp8" if fp8 else "s_i8"])
+
+
+def test_quantize_rows_invariants(golden):
+    x = bf16_to_f32(golden("quant_rows")["x"])
+    q, s = oq.quantize_rows(f32_to_bf16(x))
+    nz = np.abs(x).max(axis=1) > 0
+    assert (np.abs(q[nz]).max(axis=1) == 127).all()
+    assert np.all(np.abs(x - q * s) <= s * (0.5 + 2 ** -14))
+    assert s[3, 0] == np.float32(1e-12) and not q[3].any()          # zero row
+    # row 5: s = 127 / 127 = 1 exactly, so x / s = x and x.5 ties go to even
+    assert s[5, 0] == 1.0
+    assert list(q[5, 1:9]) == [0, 2, 2, 0, -2, -2, 126, -126]
+
+
+def test_quantize_rows_bruteforce():
+    rng = np.random.default_rng(2)
+    x = f32_to_bf16(rng.standard_normal((3, 24)).astype(np.float32) * 5)
+    q, s = oq.quantize_rows(x)
+    for i in range(3):
+        row = [float(v) for v in bf16_to_f32(x[i])]
+        amax = max(abs(v) for v in row)
+        si = max(f32(amax / 127.0), f32(1e-12))
+        assert s[i, 0] == np.float32(si)
+        for j, v in enumerate(row):
+            t = f32(v / si)
+            n = math.floor(t)
+            r = n + 1 if (t - n > 0.5 or (t - n == 0.5 and n % 2)) else n
+            assert q[i, j] == max(-127, min(127, r))
+
+
+def test_quantize_weight_layout():
+    rng = np.random.default_rng(3)
+    w = f32_to_bf16((0.02 * rng.standard_normal((40, 64))).astype(np.float32))
+    q, s = oq.quantize_weight(w, "int8_rowwise")
+    assert q.shape == (40, 64) and s.shape == (1, 40)
+    tw = t_bf16(w).float()
+    ts = (tw.abs().amax(dim=1, keepdim=True) / 127.0).clamp_min(1e-12)
+    assert np.array_equal(q, (tw / ts).round().clamp(-127, 127).to(torch.int8).numpy())
+    assert np.array_equal(s, ts.t().contiguous().numpy())
+
+
+def test_sumsq_order_and_value():
+    rng = np.random.default_rng(4)
+    v = round_bf16(rng.standard_normal((5, 1300)).astype(np.float32))
+    ss = oq.sumsq_rows(v)
+    exact = (v.astype(np.float64) ** 2).sum(axis=1)
+    assert np.allclose(ss, exact, rtol=1e-6)
+    # the stated order, as scalar loops: lane l owns 512 j + 8 l + e, then a butterfly 32..1
+    for i in range(2):
+        lane = [0.0] * 64
+        for j in range(3):
+            for ln in range(64):
+                for e in range(8):
+                    c = 512 * j + 8 * ln + e
+                    xv = float(v[i, c]) if c < 1300 else 0.0
+                    lane[ln] = f32(lane[ln] + f32(xv * xv))
+        w = 32
+        while w >= 1:
+            lane = [f32(lane[a] + lane[a + w]) for a in range(w)]
+            w //= 2
+        assert np.float32(lane[0]) == ss[i]
+
+
+def test_norm_mod_closed_forms():
+    rng = np.random.default_rng(5)
+    m, k = 6, 1024
+    x = f32_to_bf16((rng.standard_normal((m, k)) * 3 + 1).astype(np.float32))
+    idx = np.zeros(m, np.int32)
+    zero = np.zeros((1, k), np.float32)
+    v = oq.norm_mod(x, None, 0.0, idx, zero, zero)
+    assert np.allclose(np.sqrt((v.astype(np.float64) ** 2).mean(axis=1)), 1.0, atol=1e-5)
+    # modulation: (1 + scale) multiplies, shift adds, per table row idx[m]
+    tabs = np.stack([np.full(k, 0.5, np.float32), np.full(k, -0.25, np.float32)])
+    idx2 = np.array([0, 1, 0, 1, 1, 0], np.int32)
+    v2 = oq.norm_mod(x, None, 0.0, idx2, tabs, tabs)
+    sc = tabs[idx2, :1]
+    assert np.allclose(v2, v * (1 + sc) + sc, rtol=1e-6, atol=1e-6)
+    # against torch rms_norm-style ops (different sum order: tolerance)
+    w = f32_to_bf16((1 + 0.3 * rng.standard_normal(k)).astype(np.float32))
+    tx = t_bf16(x).float()
+    ref = tx * torch.rsqrt(tx.pow(2).mean(-1, keepdim=True) + 1e-6) * t_bf16(w).float()
+    v3 = oq.norm_mod(x, w, 1e-6, idx, zero, zero)
+    assert np.allclose(v3, ref.numpy(), rtol=1e-5, atol=1e-5)
+
+
+def test_heads_and_swiglu_layout():
+    o = np.arange(3 * 5 * 128, dtype=np.float32).reshape(3, 5, 128)
+    r = oq.heads_to_rows(o)
+    for m in range(5):
+        for c in (0, 127, 128, 300, 383):
+            assert r[m, c] == o[c // 128, m, c % 128]
+    rng = np.random.default_rng(6)
+    g = f32_to_bf16((2 * rng.standard_normal((4, 64))).astype(np.float32))
+    tg = t_bf16(g).float()
+    ref = torch.nn.functional.silu(tg[:, :32]) * tg[:, 32:]
+    v = oq.silu_mul(bf16_to_f32(g)[:, :32], bf16_to_f32(g)[:, 32:])
+    assert np.allclose(v, ref.numpy(), rtol=1e-6, atol=1e-7)
+
+
+def test_convrot_orthonormal():
+    h = oq.regular_hadamard(256)
+    assert np.allclose(h @ h.T, np.eye(256), atol=1e-12)
+    assert np.allclose(np.abs(h), 1 / 16)
+    x = np.random.default_rng(7).standard_normal((3, 512)).astype(np.float32)
+    y = oq.convrot(x)
+    assert np.allclose(np.linalg.norm(y.reshape(-1, 256), axis=1), np.linalg.norm(x.reshape(-1, 256), axis=1),
+                       rtol=1e-5)
+
+
+# ----------------------------------------------------------------------------- GEMM
+def test_int8_acc_matches_int_mm_and_bruteforce():
+    rng = np.random.default_rng(8)
+    a = rng.integers(-127, 128, (33, 128), dtype=np.int8)
+    b = rng.integers(-127, 128, (40, 128), dtype=np.int8)
+    acc = og.int8_acc(a, b)
+    assert np.array_equal(acc, torch._int_mm(torch.from_numpy(a), torch.from_numpy(b).t().contiguous()).numpy())
+    for i, j in ((0, 0), (32, 39), (5, 17)):
+        assert acc[i, j] == sum(int(a[i, t]) * int(b[j, t]) for t in range(128))
+    big = np.full((2, 8192), 127, np.int8)
+    assert og.int8_acc(big, -big)[0, 0] == -8192 * 127 * 127
+
+
+def test_gemm_epilogues_match_torch(golden):
+    g = golden("gemm")
+    acc = torch.from_numpy(g["acc"])
+    xs, ws = torch.from_numpy(g["xs"]), torch.from_numpy(g["ws"])
+    y = acc.float() * xs * ws                                   # kernels.py:137
+    assert np.array_equal(og.int8_gemm(g["xq"], g["xs"], g["wq"], g["ws"]), np_bf16(y.to(torch.bfloat16)))
+    yb = y + t_bf16(g["bias"]).float()
+    assert np.array_equal(g["out_bias"], np_bf16(yb.to(torch.bfloat16)))
+    r = t_bf16(g["resid"]).clone()
+    r.addcmul_(y.to(torch.bfloat16), t_bf16(g["gate"]))          # ComfyUI _mod_gate semantics
+    assert np.array_equal(g["gated"], np_bf16(r))
+
+
+def test_swiglu_perm_and_epilogue(golden):
+    p = og.swiglu_perm(32)
+    assert sorted(p) == list(range(32))
+    for j in range(4):
+        assert list(p[8 * j:8 * j + 4]) == [4 * j + i for i in range(4)]
+        assert list(p[8 * j + 4:8 * j + 8]) == [16 + 4 * j + i for i in range(4)]
+    g = golden("gemm")
+    perm = g["perm"]
+    y = og.int8_gemm(g["xq"], g["xs"], g["w1q"], g["w1s"])      # unpermuted [gate | up]
+    gt, ut = t_bf16(y).float().chunk(2, dim=1)
+    ref = np_bf16((gt * torch.sigmoid(gt) * ut).to(torch.bfloat16))  # bench/swiglu_epi_test.py:28-35
+    d = np.abs(bf16_to_f32(g["h"]).astype(np.float64) - bf16_to_f32(ref))
+    assert (d > 0).mean() < 0.01 and np.all(d <= np.abs(bf16_to_f32(ref)) * 2 ** -7 + 1e-30)
+    assert np.array_equal(og.swiglu_from_interleaved(y[:, perm]), g["h"])
+
+
+def test_fp8_gemm_against_torch(golden):
+    g = golden("gemm")
+    a = torch.from_numpy(g["fq"]).view(torch.float8_e4m3fn).float()
+    b = torch.from_numpy(g["fwq"]).view(torch.float8_e4m3fn).float()
+    y = (a.double() @ b.double().t()).float() * torch.from_numpy(g["fs"]) * torch.from_numpy(g["fws"])
+    assert np.array_equal(g["fout"], np_bf16(y.to(torch.bfloat16)))
+
+
+# ----------------------------------------------------------------------------- attention
+def test_block_quant_invariants():
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal((300, 2, 128)).astype(np.float32)
+    x[200:] *= 10
+    codes, sc = oa.block_quant(x)
+    assert codes.shape == (2, 384, 128) and sc.shape == (2, 3)
+    assert not codes[:, 300:].any()                            # padding rows
+    for h in range(2):
+        for b in range(3):
+            blk = x[b * 128:min(300, (b + 1) * 128), h]
+            assert sc[h, b] == np.float32(np.float32(np.abs(blk).max()) / np.float32(127))
+            assert np.abs(codes[h, b * 128:b * 128 + len(blk)]).max() == 127
+            assert np.all(np.abs(blk - codes[h, b * 128:b * 128 + len(blk)] * sc[h, b]) <= sc[h, b] * 0.5001)
+    # emulation form (bench/attn_emulate.py:10-18): q8(x, dim=1, group=128) on one head
+    t = torch.from_numpy(x[:, 0])
+    a = t.abs().amax(dim=1, keepdim=True)
+    a = torch.nn.functional.pad(a, (0, 0, 0, (-a.shape[0]) % 128))
+    a = a.view(-1, 128, 1).amax(1, keepdim=True).expand(-1, 128, 1).reshape(-1, 1)[:300]
+    s2 = a.clamp_min(1e-8) / 127
+    assert np.array_equal(codes[0, :300], (t / s2).round().clamp(-127, 127).to(torch.int8).numpy())
+
+
+def test_kmean_closed_form():
+    k = np.zeros((500, 2, 128), np.float32)
+    k[:, 0] = 1.5
+    k[:, 1, :] = np.arange(500, dtype=np.float32)[:, None]
+    km = oa.kmean(f32_to_bf16(k))
+    assert np.all(km[0] == 1.5) and np.all(km[1] == np.float32(249.5))
+
+
+def test_rms_rope_pins():
+    rng = np.random.default_rng(10)
+    s, h = 7, 3
+    x = f32_to_bf16(rng.standard_normal((s, h, 128)).astype(np.float32) * 4)
+    w = f32_to_bf16((1 + 0.3 * rng.standard_normal(128)).astype(np.float32))
+    eps = 1e-5
+    # angle 0 -> plain RMSNorm (bf16((r x) w))
+    tab0 = f32_to_bf16(oa.rope_table(np.zeros(s), rot=96))
+    y0 = oa.rms_rope(x, tab0, w, eps)
+    xf = t_bf16(x).float()
+    ref = (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)) * t_bf16(w).float()
+    assert np.allclose(y0, ref.to(torch.bfloat16).float().numpy(), rtol=2 ** -7, atol=1e-6)
+    # rotation preserves each (i, i + 48) pair norm and leaves channels >= 96 alone
+    tab = f32_to_bf16(oa.rope_table(np.arange(s) * 3.7, rot=96))
+    y = oa.rms_rope(x, tab, w, eps)
+    assert np.array_equal(y[..., 96:], y0[..., 96:])
+    n0 = np.hypot(y0[..., :48], y0[..., 48:96])
+    n1 = np.hypot(y[..., :48], y[..., 48:96])
+    assert np.allclose(n0, n1, rtol=0.02, atol=1e-3)
+    # the stated order on one row, as scalar loops
+    row = [float(v) for v in bf16_to_f32(x[2, 1])]
+    lanes = []
+    for ln in range(16):
+        a = 0.0
+        for e in range(8):
+            a = f32(a + f32(row[8 * ln + e] * row[8 * ln + e]))
+        lanes.append(a)
+    for wd in (8, 4, 2, 1):
+        lanes = [f32(lanes[i] + lanes[i + wd]) for i in range(wd)]
+    r = f32(1.0 / f32(math.sqrt(f32(f32(lanes[0] / 128.0) + f32(eps)))))
+    wf = [float(v) for v in bf16_to_f32(w)]
+    yb = [rb(f32(f32(r * row[d]) * wf[d])) for d in range(128)]
+    tb = bf16_to_f32(tab[2])
+    for i in (0, 17, 47):
+        a, b = yb[i], yb[i + 48]
+        o1 = rb(f32(f32(a * float(tb[i, 0, 0])) + f32(b * float(tb[i, 0, 1]))))
+        o2 = rb(f32(f32(a * float(tb[i, 1, 0])) + f32(b * float(tb[i, 1, 1]))))
+        assert y[2, 1, i] == o1 and y[2, 1, i + 48] == o2
+
+
+def test_attention_oracles_agree_with_sdpa():
+    rng = np.random.default_rng(11)
+    s, h = 200, 2
+    q = f32_to_bf16(rng.standard_normal((s, h, 128)).astype(np.float32))
+    k = f32_to_bf16((rng.standard_normal((s, h, 128)) + 2 * rng.standard_normal((1, h, 128))).astype(np.float32))
+    v = f32_to_bf16(rng.standard_normal((s, h, 128)).astype(np.float32))
+    ex = oa.attention_exact(q, k, v, 128 ** -0.5)
+    tq, tk, tv = (t_bf16(a).double().permute(1, 0, 2) for a in (q, k, v))
+    sd = torch.nn.functional.scaled_dot_product_attention(tq[None], tk[None], tv[None])[0].permute(1, 0, 2)
+    assert np.allclose(ex, sd.numpy(), atol=1e-5)
+    # K smoothing is exact for softmax: subtracting kmean shifts every logit of a query equally
+    km = oa.kmean(k)
+    ksm = (bf16_to_f32(k) - km[None]).astype(np.float32)
+    assert np.allclose(oa.attention_exact(q, ksm, v, 128 ** -0.5), ex, atol=1e-5)
+    # the int8 pipeline stays within the reference's observed error band of the exact result
+    q8, qs, k8, ks, _ = oa.prepass(q, k)
+    out = oa.attention_from_codes(q8, qs, k8, ks, v, 128 ** -0.5)[:s]
+    assert og.rel_l2(out, ex) < 0.03
+    # and smoothing matters: without it the per-block K scale spans the offset, error grows
+    q8n, qsn, k8n, ksn, _ = oa.prepass(q, k, smooth_k=False)
+    outn = oa.attention_from_codes(q8n, qsn, k8n, ksn, v, 128 ** -0.5)[:s]
+    assert og.rel_l2(outn, ex) > og.rel_l2(out, ex)
+
+
+def test_golden_fixtures_regenerate(golden):
+    """The committed fixtures are what the oracle computes today (guards silent oracle drift)."""
+    g = golden("attention")
+    q8, qs, k8, ks, km = oa.prepass(g["q"], g["k"])
+    assert np.array_equal(q8, g["q8"]) and np.array_equal(k8, g["k8"]) and np.array_equal(km, g["kmean"])
+    n = golden("norm_mod")
+    q, s = oq.norm_mod_quant_rows_i8(n["x"], n["w"], float(n["eps"]), n["idx"], n["shift"], n["scale"])
+    assert np.array_equal(q, n["q_f32"]) and np.array_equal(s, n["s_f32"])
+    h = golden("heads_swiglu")
+    q, s = oq.heads_quant_rows_i8(h["o"])
+    assert np.array_equal(q, h["q"]) and np.array_equal(s, h["s"])
