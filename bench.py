@@ -1,0 +1,239 @@
+"""Benchmark of the MI355X DiT hot path: one step = one full-size DiT block through the fused INT8 chain
+(rapid_h3.block.fused_block) at M = S = 145,152 tokens, hidden 3072, 24 x 128 heads, FFN 8192:
+
+  RMSNorm+modulation INT8 quantizer -> QKV W8A8 GEMM -> q/k RMSNorm+RoPE INT8 attention pre-pass ->
+  INT8 attention (int8 Q.K^T, bf16 P.V) -> head-major INT8 quantizer -> out-proj GEMM + gated residual ->
+  RMSNorm+modulation quantizer -> FFN-up GEMM + SwiGLU -> INT8 quantizer -> FFN-down GEMM + gated residual
+
+value = algorithmic int8-MFMA work of the block (4 GEMMs 2*M*N*K + attention 4*S^2*D*H) / time, in
+TOPS, inputs and weights resident in HBM before the timed region. Synthetic data: activations N(0,1)
+with 1 % of channels x20, weights N(0, 0.02) random init, modulation and norm weights random.
+
+    python bench.py [--gpus 1] [--steps 3] [--warmup 1] [--tokens 145152] [--no-cpu]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "rapid-h3_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "INT8 attn + W8A8 GEMM TOPS (frac of MFMA peak) at 145k tokens; ms/DiT block"
+PEAK_INT8_TOPS = 5033.0        # MI355X dense int8 MFMA
+PEAK_BF16_TFLOPS = 2517.0      # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
+HIDDEN, HEADS, D, FFN = 3072, 24, 128, 8192
+GRID = (36, 48, 84)            # latent frames x patch rows x patch columns = 145,152 tokens
+
+
+def rope_table(s, device):
+    """Split-half RoPE table [1, S, 1, 48, 2, 2] bf16 = (cos, -sin, sin, cos) over (t, h, w) positions of
+    the latent grid, 16 frequencies per axis (the H3 layout of bench/rmsrope_fuse.py:22-33)."""
+    import torch
+    t, hh, ww = GRID
+    idx = torch.arange(s, device=device)
+    pos = torch.stack([(idx // (hh * ww)) % t, (idx // ww) % hh, idx % ww], 1).float()
+    inv = 1.0 / (10000.0 ** (torch.arange(16, dtype=torch.float32, device=device) / 16))
+    a = torch.cat((pos.unsqueeze(-1) * inv.view(1, 1, -1)).unbind(1), -1)      # [S, 48]
+    c, sn = torch.cos(a), torch.sin(a)
+    return torch.stack([c, -sn, sn, c], -1).reshape(1, s, 1, 48, 2, 2).to(torch.bfloat16)
+
+
+def block_ops(m):
+    gemms = {"gemm_qkv": 2 * m * 3 * HIDDEN * HIDDEN, "gemm_out_gated": 2 * m * HIDDEN * HIDDEN,
+             "gemm_up_swiglu": 2 * m * 2 * FFN * HIDDEN, "gemm_down_gated": 2 * m * HIDDEN * FFN}
+    return gemms, 4 * m * m * D * HEADS
+
+
+def quant_bytes(m):
+    """Algorithmic HBM bytes of each quantizer phase: input read once, int8 codes + fp32 scale written."""
+    k_in = {"quant_norm1": HIDDEN, "quant_heads": HIDDEN, "quant_norm2": HIDDEN, "quant_h": FFN}
+    return {n: m * k * 2 + m * k + 4 * m for n, k in k_in.items()}
+
+
+def setup(m, device):
+    import torch
+    from rapid_h3 import gemm, kernels
+    from rapid_h3.block import BlockWeights
+    g = torch.Generator(device=device).manual_seed(0)
+
+    def randn(*shape, std=1.0):
+        return torch.randn(*shape, generator=g, device=device) * std
+
+    x = randn(m, HIDDEN)
+    x[:, torch.randperm(HIDDEN, generator=g, device=device)[:HIDDEN // 100]] *= 20
+    x = x.to(torch.bfloat16)
+    qw = {}
+    for name, n, k in (("qkv", 3 * HIDDEN, HIDDEN), ("out", HIDDEN, HIDDEN), ("fc1", 2 * FFN, HIDDEN),
+                       ("fc2", HIDDEN, FFN)):
+        qw[name] = kernels.quantize_weight(randn(n, k, std=0.02).to(torch.bfloat16), "int8_rowwise")
+    perm = gemm.swiglu_perm(2 * FFN, device)
+    fc1 = kernels.QWeight(qw["fc1"].q[perm].contiguous(), qw["fc1"].scale[:, perm].contiguous())
+
+    def nw(n):
+        return (1 + 0.3 * randn(n)).to(torch.bfloat16)
+
+    w = BlockWeights(qkv=qw["qkv"], out=qw["out"], fc1_perm=fc1, fc2=qw["fc2"], norm1_w=nw(HIDDEN),
+                     norm2_w=nw(HIDDEN), q_norm_w=nw(D), k_norm_w=nw(D), heads=HEADS)
+    mod = tuple(randn(1, HIDDEN, std=0.1) for _ in range(6))
+    segments = [(0, m, 0)]
+    tab = rope_table(m, device)
+    torch.cuda.synchronize()
+    return x, w, mod, segments, tab
+
+
+def cpu_baseline(m):
+    """The CPU oracle (numpy port of the reference's PyTorch path) on a bounded sample of the same
+    block: every quantizer and GEMM at 2,048 of the M tokens, attention for 128 query rows x all S
+    keys x 1 head, each extrapolated linearly to the full block."""
+    import numpy as np
+    from oracle import attn as oa
+    from oracle import gemm as og
+    from oracle import quant as oq
+    from oracle.numerics import f32_to_bf16
+    try:
+        from threadpoolctl import threadpool_info
+        cores = max([i.get("num_threads", 1) for i in threadpool_info()] + [1])
+    except Exception:  # noqa: BLE001
+        cores = os.cpu_count()
+    rng = np.random.default_rng(0)
+    ms = 2048
+    t_gemm = 0.0
+    x = f32_to_bf16(rng.standard_normal((ms, HIDDEN)).astype(np.float32))
+    for n, k in ((3 * HIDDEN, HIDDEN), (HIDDEN, HIDDEN), (2 * FFN, HIDDEN), (HIDDEN, FFN)):
+        a = x if k == HIDDEN else f32_to_bf16(rng.standard_normal((ms, k)).astype(np.float32))
+        wq, ws = oq.quantize_weight(f32_to_bf16((0.02 * rng.standard_normal((n, k))).astype(np.float32)))
+        t0 = time.perf_counter()
+        xq, xs = oq.quantize_rows(a)
+        og.int8_gemm(xq, xs, wq, ws)
+        t_gemm += time.perf_counter() - t0
+    rows, s = 128, m
+    q = f32_to_bf16(rng.standard_normal((s, 1, D)).astype(np.float32))
+    k = f32_to_bf16(rng.standard_normal((s, 1, D)).astype(np.float32))
+    v = f32_to_bf16(rng.standard_normal((s, 1, D)).astype(np.float32))
+    t0 = time.perf_counter()
+    q8, qs, k8, ks, _ = oa.prepass(q[:rows], k)
+    oa.attention_from_codes(q8, qs, k8, ks, v, D ** -0.5, rows=np.arange(rows))
+    t_attn = time.perf_counter() - t0
+    gemms, attn_ops = block_ops(m)
+    t_full = t_gemm * (m / ms) + t_attn * (s / rows) * HEADS
+    total = sum(gemms.values()) + attn_ops
+    return {"value": round(total / t_full / 1e12, 4), "unit": "TOPS", "cores": int(cores), "kind": "port",
+            "sample": (f"oracle quantizers+4 GEMMs at M={ms} (x{m / ms:.1f}) and attention {rows} query rows x "
+                       f"{s} keys x 1 head (x{s / rows * HEADS:.0f}); {t_gemm + t_attn:.1f} s measured, "
+                       f"{t_full:.0f} s extrapolated per block"),
+            "seconds_per_block": round(t_full, 1)}
+
+
+def traffic_from_profile():
+    """HBM bytes per launch of the attention main kernel from the committed rocprofv3 --pmc summary
+    (FETCH_SIZE + WRITE_SIZE, calibrated against a copy kernel), or None if there is none."""
+    p = os.path.join(ROOT, "profiles", "attn_main_traffic.json")
+    if not os.path.exists(p):
+        return None
+    with open(p) as f:
+        return json.load(f).get("bytes_per_launch")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--tokens", type=int, default=GRID[0] * GRID[1] * GRID[2])
+    ap.add_argument("--no-cpu", action="store_true")
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {a.gpus} is not supported (no multi-GPU path)",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from rapid_h3.block import PHASES, fused_block
+    dev = torch.device("cuda:0")
+    m = a.tokens
+    x, w, mod, segments, tab = setup(m, dev)
+
+    for _ in range(a.warmup):
+        fused_block(x, w, mod, segments, tab)
+    torch.cuda.synchronize()
+
+    events = []
+
+    def mark(name):
+        e = torch.cuda.Event(enable_timing=True)
+        e.record()                      # torch's current stream: the stream every rh3 launch uses
+        events[-1].append((name, e))
+
+    t0 = time.perf_counter()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(a.steps):
+        b = torch.cuda.Event(enable_timing=True)
+        b.record()
+        events.append([("begin", b)])
+        fused_block(x, w, mod, segments, tab, mark=mark)
+    end.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = start.elapsed_time(end) / a.steps
+
+    phase_ms = {p: 0.0 for p in PHASES}
+    for ev in events:
+        for (_, e0), (name, e1) in zip(ev[:-1], ev[1:]):
+            phase_ms[name] += e0.elapsed_time(e1) / a.steps
+    gemms, attn_ops = block_ops(m)
+    qbytes = quant_bytes(m)
+    total_ops = sum(gemms.values()) + attn_ops
+    value = total_ops / (ms_step * 1e-3) / 1e12
+    parts = {}
+    for p in PHASES:
+        t = phase_ms[p]
+        if p in gemms:
+            tops = gemms[p] / (t * 1e-3) / 1e12
+            parts[p] = {"ms": round(t, 3), "tops": round(tops, 1), "frac_int8_peak": round(tops / PEAK_INT8_TOPS, 4)}
+        elif p == "attn_main":
+            tops = attn_ops / (t * 1e-3) / 1e12
+            mixed = 1.0 / (0.5 / PEAK_INT8_TOPS + 0.5 / PEAK_BF16_TFLOPS)
+            parts[p] = {"ms": round(t, 3), "tops": round(tops, 1), "frac_int8_peak": round(tops / PEAK_INT8_TOPS, 4),
+                        "frac_mixed_roofline": round(tops / mixed, 4)}
+        elif p in qbytes:
+            gbs = qbytes[p] / (t * 1e-3) / 1e9
+            parts[p] = {"ms": round(t, 3), "gbs": round(gbs, 0), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4)}
+        else:
+            parts[p] = {"ms": round(t, 3)}
+    t_attn = phase_ms["attn_main"]
+    achieved = attn_ops / (t_attn * 1e-3) / 1e12
+    traffic = traffic_from_profile()
+    gemm_ms = sum(phase_ms[p] for p in gemms)
+    out = {
+        "metric": METRIC, "value": round(value, 2), "unit": "TOPS", "n_gpus": 1, "steps": a.steps,
+        "warmup": a.warmup, "ms_per_step": round(ms_step, 3), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int8", "data": "synthetic",
+        "config": {"workload": "full-size DiT block: fused quantizers + 4 W8A8 GEMMs (C2) + INT8 attention (C4)",
+                   "tokens": m, "hidden": HIDDEN, "heads": HEADS, "head_dim": D, "ffn": FFN,
+                   "recipe": "int8_rowwise, per-128-block Q/K, K smoothing, bf16 P.V", "parallelism": "none"},
+        "ms_per_block": round(ms_step, 3),
+        "gemm_tops": round(sum(gemms.values()) / (gemm_ms * 1e-3) / 1e12, 1),
+        "gemm_frac_int8_peak": round(sum(gemms.values()) / (gemm_ms * 1e-3) / 1e12 / PEAK_INT8_TOPS, 4),
+        "attn_tops": round(achieved, 1), "attn_frac_int8_peak": round(achieved / PEAK_INT8_TOPS, 4),
+        "parts": parts,
+        "roofline": {"kernel": "attn_fwd_kernel", "bound": "mfma", "achieved": round(achieved, 1),
+                     "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_INT8_TOPS, 4),
+                     "traffic": traffic,
+                     "per_launch": f"4*S^2*D*H = {attn_ops:.4e} int8+bf16 MFMA ops (S={m}, D={D}, H={HEADS})",
+                     "avg_launch_ms": round(t_attn, 3)},
+        "wall_s_timed": round(wall, 2),
+    }
+    if not a.no_cpu:
+        out["cpu_baseline"] = cpu_baseline(m)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -153,6 +153,13 @@ int rh3_attention_prepass(const uint16_t* q, int64_t q_ss, int64_t q_sh,
                           void* workspace, int64_t workspace_bytes, void** ptrs /* [6] */,
                           hipStream_t stream);
 
+/* The main kernel alone, on a workspace rh3_attention_prepass filled for the same (Sq, Sk, H): the
+ * second half of int8_attention (attn_int8.cu:2749-2849 after prepass()). Lets a caller time or
+ * schedule the pre-pass and the main kernel separately. */
+int rh3_attention_forward(int64_t Sq, int64_t Sk, int64_t H, float scale,
+                          uint16_t* out, int64_t o_ss, int64_t o_sh,
+                          void* workspace, int64_t workspace_bytes, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -516,6 +516,19 @@ extern "C" int rh3_attention_prepass(const uint16_t* q, int64_t q_ss, int64_t q_
   return RH3_OK;
 }
 
+extern "C" int rh3_attention_forward(int64_t Sq, int64_t Sk, int64_t H, float scale, uint16_t* out, int64_t o_ss,
+                                     int64_t o_sh, void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+  clear_error();
+  RH3_REQUIRE(Sq > 0 && Sk > 0 && H > 0, "attention_forward: sizes must be positive");
+  RH3_REQUIRE(out && (reinterpret_cast<uintptr_t>(out) & 7) == 0 && o_ss % 4 == 0 && o_sh % 4 == 0,
+              "attention_forward: out must be 8-byte aligned with strides multiple of 4");
+  const Work w = layout(workspace, Sq, Sk, H);
+  RH3_REQUIRE(workspace && aligned16(workspace) && workspace_bytes >= w.bytes,
+              "attention_forward: workspace %lld bytes < required %lld", (long long)workspace_bytes,
+              (long long)w.bytes);
+  return forward(w, Sq, Sk, H, scale, out, o_ss, o_sh, stream);
+}
+
 extern "C" int rh3_int8_attention(const uint16_t* q, int64_t q_ss, int64_t q_sh, const uint16_t* k, int64_t k_ss,
                                   int64_t k_sh, const uint16_t* v, int64_t v_ss, int64_t v_sh, int64_t Sq, int64_t Sk,
                                   int64_t H, float scale, int smooth_k, uint16_t* out, int64_t o_ss, int64_t o_sh,

@@ -33,6 +33,7 @@ SIGNATURES = {
     "rh3_int8_attention": ([_P, _I, _I, _P, _I, _I, _P, _I, _I, _I, _I, _I, _F, _C, _P, _I, _I, _P, _I, _P], _C),
     "rh3_int8_attention_rr": ([_P, _I, _I, _P, _I, _I, _P, _I, _I, _I, _I, _P, _C, _P, _P, _F, _F, _C, _P, _I, _I,
                                _P, _I, _P], _C),
+    "rh3_attention_forward": ([_I, _I, _I, _F, _P, _I, _I, _P, _I, _P], _C),
     "rh3_attention_prepass": ([_P, _I, _I, _P, _I, _I, _P, _I, _I, _I, _I, _I, _P, _C, _P, _P, _F, _C, _P, _I,
                                ctypes.POINTER(ctypes.c_void_p), _P], _C),
 }

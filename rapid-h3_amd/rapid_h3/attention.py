@@ -127,5 +127,18 @@ def prepass(q, k, v, tab=None, qw=None, kw=None, eps=1e-5, smooth_k=True):
         "q8": view(0, (h, sqp, D), torch.int8), "qs": view(1, (h, sqp // 128), torch.float32),
         "k8": view(2, (h, skp, D), torch.int8), "ks": view(3, (h, skp // 128), torch.float32),
         "kmean": view(4, (h, D), torch.float32), "vt": view(5, (h, D, skp), torch.bfloat16),
-        "_ws": ws,
+        "_ws": ws, "_sk": sk,
     }
+
+
+def forward(pp, sq, out=None, scale=None):
+    """The main kernel alone on operands prepass() produced (same workspace): out [Sq, H, 128] bf16."""
+    h = pp["q8"].shape[0]
+    sk = pp["_sk"]
+    scale = D ** -0.5 if scale is None else scale
+    if out is None:
+        out = torch.empty((sq, h, D), device=pp["q8"].device, dtype=torch.bfloat16)
+    ws = pp["_ws"]
+    nat.call("rh3_attention_forward", sq, sk, h, float(scale), nat.ptr(out), out.stride(0), out.stride(1),
+             nat.ptr(ws), ws.numel(), nat.stream(out.device))
+    return out

@@ -1,0 +1,109 @@
+"""The fused INT8 DiT block chain on the HIP kernels: the call sequence of the reference's
+_fused_block (/root/reference/custom_nodes/rapid_h3/__init__.py:207-321) for the int8_rowwise recipe,
+plus _row_index (:189-200) and the per-segment gated residual (:242-251).
+
+    x [S, hidden] bf16 residual stream (updated in place and returned)
+    RMSNorm + modulation -> INT8 (one pass)        rh3_quant_norm_mod_i8
+    QKV GEMM                                       rh3_gemm_i8
+    q/k RMSNorm + RoPE + INT8 attention            rh3_int8_attention_rr (head-major output)
+    head-major gather -> INT8                      rh3_quant_heads_i8
+    out-proj GEMM + gated residual, per segment    rh3_gemm_i8_gated
+    RMSNorm + modulation -> INT8                   rh3_quant_norm_mod_i8
+    FFN-up GEMM + SwiGLU epilogue                  rh3_gemm_i8_swiglu
+    INT8 of h                                      rh3_quant_rows_i8
+    FFN-down GEMM + gated residual, per segment    rh3_gemm_i8_gated
+
+ComfyUI objects (the block module, adaln_proj, model management) are outside this build: the caller
+passes the weights and the modulation tables as tensors.
+"""
+from dataclasses import dataclass
+
+import torch
+
+from . import attention as _attn
+from . import gemm as _gemm
+from . import quant as _quant
+from .kernels import QWeight
+
+D = 128
+
+
+@dataclass
+class BlockWeights:
+    """Quantized weights of one DiT block (each QWeight: q [N, K] int8, scale [1, N] fp32).
+    fc1 holds [gate | up] rows already permuted with swiglu_perm (the reference caches that order,
+    __init__.py:231-240)."""
+    qkv: QWeight
+    out: QWeight
+    fc1_perm: QWeight
+    fc2: QWeight
+    norm1_w: torch.Tensor
+    norm2_w: torch.Tensor
+    q_norm_w: torch.Tensor
+    k_norm_w: torch.Tensor
+    heads: int
+    eps: float = 1e-6
+    qk_eps: float = 1e-6
+
+
+def row_index(segments, s, device):
+    """Per-token modulation-row index (int32 [S]) from [(start, stop, row)] (__init__.py:189-200)."""
+    idx = torch.empty(s, dtype=torch.int32, device=device)
+    for a, b, row in segments:
+        idx[a:b] = row.to(device=device, dtype=torch.int32) if torch.is_tensor(row) else int(row)
+    return idx
+
+
+def gemm_gated(xq, xs, qw, x, gate, segments):
+    """x += gate[row] * (xq @ W^T) per modality segment, in the GEMM epilogue (__init__.py:242-251).
+    gate: [R, N] table (bf16 or fp32); each segment's row is rounded to bf16 like _mod_row."""
+    for a, b, row in segments:
+        if torch.is_tensor(row):
+            raise NotImplementedError("per-token gate rows: the reference falls back to _mod_gate here")
+        g = gate[int(row)].to(torch.bfloat16).reshape(-1).contiguous()
+        _gemm.int8_gemm_gated_residual(xq[a:b], xs[a:b], qw.q, qw.scale, g, x[a:b])
+    return x
+
+
+PHASES = ("quant_norm1", "gemm_qkv", "attn_prepass", "attn_main", "quant_heads", "gemm_out_gated", "quant_norm2",
+          "gemm_up_swiglu", "quant_h", "gemm_down_gated")
+
+
+def fused_block(x, w: BlockWeights, mod, segments, rope_tab, idx=None, mark=None):
+    """One DiT block forward on x [S, hidden] bf16 (modified in place). mod = (shift_msa, scale_msa,
+    gate_msa, shift_mlp, scale_mlp, gate_mlp), each [R, hidden]; rope_tab [1, S, 1, rot/2, 2, 2] bf16.
+    mark: optional callable, called with each name of PHASES after that phase is enqueued (a timer
+    records a stream event there); the kernels and their order are the same with or without it."""
+    shift_msa, scale_msa, gate_msa, shift_mlp, scale_mlp, gate_mlp = mod
+    tick = mark or (lambda name: None)
+    s = x.shape[0]
+    h = w.heads
+    if idx is None:
+        idx = row_index(segments, s, x.device)
+    xq, xs = _quant.norm_mod_quant_rows_i8(x, w.norm1_w, w.eps, idx, shift_msa, scale_msa)
+    tick("quant_norm1")
+    qkv = _gemm.int8_gemm(xq, xs, w.qkv.q, w.qkv.scale)
+    tick("gemm_qkv")
+    q, k, v = (t.view(s, h, D) for t in qkv.split(h * D, dim=-1))
+    o = torch.empty(1, h, s, D, dtype=x.dtype, device=x.device)
+    # attention_rr = pre-pass (RMSNorm + RoPE + stats + INT8) then the main kernel, as two calls
+    pp = _attn.prepass(q, k, v, rope_tab, w.q_norm_w, w.k_norm_w, w.qk_eps)
+    tick("attn_prepass")
+    _attn.forward(pp, s, out=o[0].transpose(0, 1))
+    tick("attn_main")
+    del qkv, pp
+    oq, os_ = _quant.heads_quant_rows_i8(o[0])
+    tick("quant_heads")
+    del o
+    x = gemm_gated(oq, os_, w.out, x, gate_msa, segments)
+    tick("gemm_out_gated")
+    xq, xs = _quant.norm_mod_quant_rows_i8(x, w.norm2_w, w.eps, idx, shift_mlp, scale_mlp)
+    tick("quant_norm2")
+    hh = _gemm.int8_gemm_swiglu(xq, xs, w.fc1_perm.q, w.fc1_perm.scale)
+    tick("gemm_up_swiglu")
+    hq, hs = _quant.quant_rows_i8(hh)
+    tick("quant_h")
+    del hh
+    x = gemm_gated(hq, hs, w.fc2, x, gate_mlp, segments)
+    tick("gemm_down_gated")
+    return x
