@@ -241,62 +241,66 @@ __device__ __forceinline__ int kswz(int r, int c) { return r * 128 + ((c ^ ((r ^
 // Vt tile: 128 rows (d) x 256 B, chunk c of row r at c ^ (r & 15)
 __device__ __forceinline__ int vswz(int r, int c) { return r * 256 + ((c ^ (r & 15)) << 4); }
 
-__global__ void __launch_bounds__(256, 1) attn_fwd_kernel(const FwdArgs a) {
+// 8 waves (2 per SIMD, so one wave's softmax overlaps the other's MFMAs), 256 queries per workgroup:
+// wave w owns queries qb*256 + 32*w .. +31, inside 128-query scale block 2*qb + w/4.
+constexpr int FWD_WAVES = 8, FWD_NT = FWD_WAVES * 64, FWD_BQ = FWD_WAVES * 32;
+// lazy rescale: the reference max moves only when a tile max exceeds it by more than 2^8 (P <= 256)
+constexpr float RESCALE_LOG2 = 8.0f;
+
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
+  const v2bf v = {static_cast<__bf16>(a), static_cast<__bf16>(b)};  // v_cvt_pk_bf16_f32, RNE
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+__global__ void __launch_bounds__(FWD_NT, 1) attn_fwd_kernel(const FwdArgs a) {
   __shared__ __attribute__((aligned(16))) int8_t klds[2][BLK * D];
   __shared__ __attribute__((aligned(16))) int8_t vlds[2][D * BLK * 2];
   const int h = blockIdx.y, qb = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, g = lane >> 5;
-  const int64_t q = static_cast<int64_t>(qb) * BLK + wave * 32 + l32;
+  const int64_t q = static_cast<int64_t>(qb) * FWD_BQ + wave * 32 + l32;
 
+  // the Q operands are padded to 128 queries; a workgroup's last 128 may lie past them (then they are
+  // computed on zero codes and never stored)
+  const bool qin = q < a.Sqpad;
   v4i qf[4];
   {
     const int8_t* qp = a.q8 + (static_cast<int64_t>(h) * a.Sqpad + q) * D + g * 16;
 #pragma unroll
-    for (int ds = 0; ds < 4; ++ds) qf[ds] = *reinterpret_cast<const v4i*>(qp + ds * 32);
+    for (int ds = 0; ds < 4; ++ds) qf[ds] = qin ? *reinterpret_cast<const v4i*>(qp + ds * 32) : v4i{0, 0, 0, 0};
   }
-  const float qscale = a.qs[static_cast<int64_t>(h) * (a.Sqpad / BLK) + qb] * a.scale_log2;
+  const float qscale = (qin ? a.qs[static_cast<int64_t>(h) * (a.Sqpad / BLK) + (q >> 7)] : 0.0f) * a.scale_log2;
 
   const int8_t* kbase = a.k8 + static_cast<int64_t>(h) * a.Skpad * D;
   const uint16_t* vbase = a.vt + static_cast<int64_t>(h) * D * a.Skpad;
   const float* ksb = a.ks + static_cast<int64_t>(h) * (a.Skpad / BLK);
-  uint4 sk0, sk1, sk2, sk3, sv0, sv1, sv2, sv3, sv4, sv5, sv6, sv7;
-  // V^T tile chunk id = tid + 256 * i: row d = id / 16 = tid / 16 + 16 * i, 16-byte chunk c = tid % 16
+  // K tile (1024 chunks): chunk id tid + 512 i -> key row id / 8, chunk id % 8
+  // V^T tile (2048 chunks): chunk id tid + 512 i -> d row id / 16 = tid / 16 + 32 i, chunk tid % 16
   const int vd = tid >> 4, vc = tid & 15;
   const uint16_t* vrow = vbase + static_cast<int64_t>(vd) * a.Skpad + vc * 8;
-  const int64_t vstep = 16 * a.Skpad;
+  const int64_t vstep = 32 * a.Skpad;
+  uint4 sk0, sk1, sv0, sv1, sv2, sv3;
 #define RH3_GLOAD(kt)                                                                   \
   do {                                                                                  \
     const int8_t* kp = kbase + static_cast<int64_t>(kt) * BLK * D + tid * 16;           \
     sk0 = *reinterpret_cast<const uint4*>(kp);                                          \
-    sk1 = *reinterpret_cast<const uint4*>(kp + 4096);                                   \
-    sk2 = *reinterpret_cast<const uint4*>(kp + 8192);                                   \
-    sk3 = *reinterpret_cast<const uint4*>(kp + 12288);                                  \
+    sk1 = *reinterpret_cast<const uint4*>(kp + 8192);                                   \
     const uint16_t* vp = vrow + static_cast<int64_t>(kt) * BLK;                         \
     sv0 = *reinterpret_cast<const uint4*>(vp);                                          \
     sv1 = *reinterpret_cast<const uint4*>(vp + vstep);                                  \
     sv2 = *reinterpret_cast<const uint4*>(vp + 2 * vstep);                              \
     sv3 = *reinterpret_cast<const uint4*>(vp + 3 * vstep);                              \
-    sv4 = *reinterpret_cast<const uint4*>(vp + 4 * vstep);                              \
-    sv5 = *reinterpret_cast<const uint4*>(vp + 5 * vstep);                              \
-    sv6 = *reinterpret_cast<const uint4*>(vp + 6 * vstep);                              \
-    sv7 = *reinterpret_cast<const uint4*>(vp + 7 * vstep);                              \
   } while (0)
-  // K tile chunk id = tid + 256 * i: row = id / 8, chunk = id % 8
 #define RH3_SSTORE(st)                                                                  \
   do {                                                                                  \
     *reinterpret_cast<uint4*>(&klds[st][kswz((tid >> 3) + 0, tid & 7)]) = sk0;          \
-    *reinterpret_cast<uint4*>(&klds[st][kswz((tid >> 3) + 32, tid & 7)]) = sk1;         \
-    *reinterpret_cast<uint4*>(&klds[st][kswz((tid >> 3) + 64, tid & 7)]) = sk2;         \
-    *reinterpret_cast<uint4*>(&klds[st][kswz((tid >> 3) + 96, tid & 7)]) = sk3;         \
+    *reinterpret_cast<uint4*>(&klds[st][kswz((tid >> 3) + 64, tid & 7)]) = sk1;         \
     *reinterpret_cast<uint4*>(&vlds[st][vswz(vd + 0, vc)]) = sv0;                       \
-    *reinterpret_cast<uint4*>(&vlds[st][vswz(vd + 16, vc)]) = sv1;                      \
-    *reinterpret_cast<uint4*>(&vlds[st][vswz(vd + 32, vc)]) = sv2;                      \
-    *reinterpret_cast<uint4*>(&vlds[st][vswz(vd + 48, vc)]) = sv3;                      \
-    *reinterpret_cast<uint4*>(&vlds[st][vswz(vd + 64, vc)]) = sv4;                      \
-    *reinterpret_cast<uint4*>(&vlds[st][vswz(vd + 80, vc)]) = sv5;                      \
-    *reinterpret_cast<uint4*>(&vlds[st][vswz(vd + 96, vc)]) = sv6;                      \
-    *reinterpret_cast<uint4*>(&vlds[st][vswz(vd + 112, vc)]) = sv7;                     \
+    *reinterpret_cast<uint4*>(&vlds[st][vswz(vd + 32, vc)]) = sv1;                      \
+    *reinterpret_cast<uint4*>(&vlds[st][vswz(vd + 64, vc)]) = sv2;                      \
+    *reinterpret_cast<uint4*>(&vlds[st][vswz(vd + 96, vc)]) = sv3;                      \
   } while (0)
 
   v16f o[4];
@@ -304,7 +308,8 @@ __global__ void __launch_bounds__(256, 1) attn_fwd_kernel(const FwdArgs a) {
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int r = 0; r < 16; ++r) o[i][r] = 0.0f;
-  float mrow = -INFINITY, lrow = 0.0f;
+  float mref = -INFINITY, lrow = 0.0f;
+  const v2bf ones = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
 
   const int nkt = static_cast<int>(a.Skpad / BLK);
   RH3_GLOAD(0);
@@ -316,6 +321,7 @@ __global__ void __launch_bounds__(256, 1) attn_fwd_kernel(const FwdArgs a) {
     const int8_t* kl = klds[cur];
     const int8_t* vl = vlds[cur];
 
+    // S^T[key][query] = K8 . Q8^T: lane (l32, g) of s[kb] holds query l32 and keys kb*32 + 8*(r/4) + 4*g + r%4
     v16i s[4];
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb)
@@ -330,45 +336,53 @@ __global__ void __launch_bounds__(256, 1) attn_fwd_kernel(const FwdArgs a) {
       }
     }
 
-    // scores in log2 units; keys past Sk (last tile only) are masked
-    const float c = qscale * ksb[kt];
-    float t[4][16];
-    float mx = -INFINITY;
     const int64_t key0 = static_cast<int64_t>(kt) * BLK;
-    const bool tail = key0 + BLK > a.Sk;
+    const bool tail = key0 + BLK > a.Sk;  // only the last tile can hold keys >= Sk
+    if (tail) {
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (key0 + kb * 32 + 8 * (r >> 2) + 4 * g + (r & 3) >= a.Sk) s[kb][r] = INT_MIN;
+    }
+    // the scale c > 0, so the tile's max score is c * (max int32 accumulator)
+    int mi = INT_MIN;
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float x = static_cast<float>(s[kb][r]) * c;
-        if (tail) {
-          const int64_t key = key0 + kb * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-          if (key >= a.Sk) x = -INFINITY;
-        }
-        t[kb][r] = x;
-        mx = fmaxf(mx, x);
-      }
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float mnew = fmaxf(mrow, mx);
-    const float alpha = __builtin_amdgcn_exp2f(mrow - mnew);
-    mrow = mnew;
-    float lsum = 0.0f;
+      for (int r = 0; r < 16; ++r) mi = max(mi, s[kb][r]);
+    mi = max(mi, __shfl_xor(mi, 32, 64));
+    const float c = qscale * ksb[kt];
+    const float mt = static_cast<float>(mi) * c;
+    if (__builtin_amdgcn_ballot_w64(mt > mref + RESCALE_LOG2) != 0) {
+      const float mnew = fmaxf(mref, mt);
+      const float alpha = __builtin_amdgcn_exp2f(mref - mnew);
+      mref = mnew;
+      lrow = lrow * alpha;
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[db][r] = o[db][r] * alpha;
+    }
+    const float nb = -mref;
+
+    // P = 2^(t - mref) in bf16 (P <= 2^8); the row sum adds exactly these bf16 values
     uint32_t pk[4][8];
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
       for (int r = 0; r < 16; r += 2) {
-        const float p0 = round_bf(__builtin_amdgcn_exp2f(t[kb][r] - mnew));
-        const float p1 = round_bf(__builtin_amdgcn_exp2f(t[kb][r + 1] - mnew));
-        lsum = lsum + p0 + p1;
-        pk[kb][r >> 1] = (__float_as_uint(p0) >> 16) | (__float_as_uint(p1) & 0xffff0000u);
+        float p0 = __builtin_amdgcn_exp2f(fmaf(static_cast<float>(s[kb][r]), c, nb));
+        float p1 = __builtin_amdgcn_exp2f(fmaf(static_cast<float>(s[kb][r + 1]), c, nb));
+        if (tail) {
+          if (s[kb][r] == INT_MIN) p0 = 0.0f;
+          if (s[kb][r + 1] == INT_MIN) p1 = 0.0f;
+        }
+        pk[kb][r >> 1] = pk_bf16(p0, p1);
+        lrow = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2bf, pk[kb][r >> 1]), ones, lrow, false);
       }
-    lrow = lrow * alpha + lsum;
-#pragma unroll
-    for (int db = 0; db < 4; ++db)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) o[db][r] = o[db][r] * alpha;
 
+    // O^T[d][query] += V^T . P^T
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
 #pragma unroll
@@ -379,8 +393,7 @@ __global__ void __launch_bounds__(256, 1) attn_fwd_kernel(const FwdArgs a) {
 #pragma unroll
         for (int db = 0; db < 4; ++db) {
           const v4i vw = *reinterpret_cast<const v4i*>(vl + vswz(db * 32 + l32, kb * 4 + m * 2 + g));
-          const v8bf vf = __builtin_bit_cast(v8bf, vw);
-          o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, o[db], 0, 0, 0);
+          o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, vw), pf, o[db], 0, 0, 0);
         }
       }
     }
@@ -400,8 +413,8 @@ __global__ void __launch_bounds__(256, 1) attn_fwd_kernel(const FwdArgs a) {
       for (int rq = 0; rq < 4; ++rq) {
         const int d = db * 32 + 8 * rq + 4 * g;
         uint2 w;
-        w.x = pack_bf2(o[db][4 * rq + 0] * il, o[db][4 * rq + 1] * il);
-        w.y = pack_bf2(o[db][4 * rq + 2] * il, o[db][4 * rq + 3] * il);
+        w.x = pk_bf16(o[db][4 * rq + 0] * il, o[db][4 * rq + 1] * il);
+        w.y = pk_bf16(o[db][4 * rq + 2] * il, o[db][4 * rq + 3] * il);
         *reinterpret_cast<uint2*>(op + d) = w;
       }
   }
@@ -471,7 +484,7 @@ int forward(const Work& w, int64_t Sq, int64_t Sk, int64_t H, float scale, uint1
             int64_t o_sh, hipStream_t st) {
   FwdArgs f{w.q8, w.qs, w.k8, w.ks, w.vt, out, o_ss, o_sh, Sq, Sk, pad(Sq), pad(Sk),
             scale * 1.4426950408889634f};
-  hipLaunchKernelGGL(attn_fwd_kernel, dim3(pad(Sq) / BLK, H), dim3(256), 0, st, f);
+  hipLaunchKernelGGL(attn_fwd_kernel, dim3((Sq + FWD_BQ - 1) / FWD_BQ, H), dim3(FWD_NT), 0, st, f);
   return launch_status("attention forward");
 }
 
