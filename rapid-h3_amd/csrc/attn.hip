@@ -16,6 +16,8 @@
 //   v_mfma_f32_32x32x16_bf16 (D on rows, queries on lanes, so the per-query rescale is per lane).
 //   The row sum l adds the same bf16-rounded P the MFMA consumes (attn_int8.cu:8-10, :652-656).
 //   K and Vt tiles (16 + 32 KiB) are double-buffered in LDS with XOR-swizzled 16-byte chunks.
+#include <type_traits>
+
 #include "rh3_common.hpp"
 
 namespace rh3 {
@@ -312,10 +314,10 @@ __global__ void __launch_bounds__(FWD_NT, 1) attn_fwd_kernel(const FwdArgs a) {
   const v2bf ones = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
 
   const int nkt = static_cast<int>(a.Skpad / BLK);
-  RH3_GLOAD(0);
-  RH3_SSTORE(0);
-  __syncthreads();
-  for (int kt = 0; kt < nkt; ++kt) {
+  // one 128-key tile; TAIL (the last tile when Sk is not a multiple of 128) masks keys >= Sk. The two
+  // instantiations keep the mask out of the per-score code of every other tile.
+  auto tile = [&](const int kt, auto tail_tag) {
+    constexpr bool TAIL = decltype(tail_tag)::value;
     const int cur = kt & 1;
     if (kt + 1 < nkt) RH3_GLOAD(kt + 1);
     const int8_t* kl = klds[cur];
@@ -335,15 +337,14 @@ __global__ void __launch_bounds__(FWD_NT, 1) attn_fwd_kernel(const FwdArgs a) {
         s[kb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf, qf[ds], s[kb], 0, 0, 0);
       }
     }
-
-    const int64_t key0 = static_cast<int64_t>(kt) * BLK;
-    const bool tail = key0 + BLK > a.Sk;  // only the last tile can hold keys >= Sk
-    if (tail) {
+    int nvalid = BLK;  // keys of this tile below Sk
+    if constexpr (TAIL) {
+      nvalid = static_cast<int>(a.Sk - static_cast<int64_t>(kt) * BLK);
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
         for (int r = 0; r < 16; ++r)
-          if (key0 + kb * 32 + 8 * (r >> 2) + 4 * g + (r & 3) >= a.Sk) s[kb][r] = INT_MIN;
+          if (kb * 32 + 8 * (r >> 2) + 4 * g + (r & 3) >= nvalid) s[kb][r] = INT_MIN;
     }
     // the scale c > 0, so the tile's max score is c * (max int32 accumulator)
     int mi = INT_MIN;
@@ -374,9 +375,9 @@ __global__ void __launch_bounds__(FWD_NT, 1) attn_fwd_kernel(const FwdArgs a) {
       for (int r = 0; r < 16; r += 2) {
         float p0 = __builtin_amdgcn_exp2f(fmaf(static_cast<float>(s[kb][r]), c, nb));
         float p1 = __builtin_amdgcn_exp2f(fmaf(static_cast<float>(s[kb][r + 1]), c, nb));
-        if (tail) {
-          if (s[kb][r] == INT_MIN) p0 = 0.0f;
-          if (s[kb][r + 1] == INT_MIN) p1 = 0.0f;
+        if constexpr (TAIL) {
+          if (kb * 32 + 8 * (r >> 2) + 4 * g + (r & 3) >= nvalid) p0 = 0.0f;
+          if (kb * 32 + 8 * (r >> 2) + 4 * g + ((r + 1) & 3) >= nvalid) p1 = 0.0f;
         }
         pk[kb][r >> 1] = pk_bf16(p0, p1);
         lrow = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2bf, pk[kb][r >> 1]), ones, lrow, false);
@@ -399,7 +400,15 @@ __global__ void __launch_bounds__(FWD_NT, 1) attn_fwd_kernel(const FwdArgs a) {
     }
     if (kt + 1 < nkt) RH3_SSTORE(cur ^ 1);
     __syncthreads();
-  }
+  };
+
+  RH3_GLOAD(0);
+  RH3_SSTORE(0);
+  __syncthreads();
+  const bool ragged = a.Sk % BLK != 0;
+  const int nfull = ragged ? nkt - 1 : nkt;
+  for (int kt = 0; kt < nfull; ++kt) tile(kt, std::false_type{});
+  if (ragged) tile(nkt - 1, std::true_type{});
 #undef RH3_GLOAD
 #undef RH3_SSTORE
 
