@@ -7,12 +7,12 @@
 //   EPI_GATED   resid = bf16(fma(bf16(y), gate[n], resid))     (in place)
 //   EPI_ACC     raw int32 accumulators (verification)
 //
-// Schedule: 256x256 output tile per workgroup, 4 waves in a 2x2 grid, 128x128 per wave held in
-// accumulator registers (int8: 4x4 v_mfma_i32_32x32x32_i8 tiles; fp8: v_mfma_f32_32x32x64_f8f6f4).
-// K advances 64 bytes per step through a double-buffered LDS stage (2 x 32 KiB): the next step's
-// global loads are issued before the current step's MFMAs and land in the other buffer after them,
-// one barrier per step. LDS rows are 64 B; 16-byte chunks are XOR-swizzled by row so the
-// ds_read_b128 fragment loads of 16 consecutive rows hit distinct banks.
+// Schedule: 256x256 output tile per workgroup, 8 waves (2 per SIMD, so each hides the other's LDS and
+// barrier latency) in a 2x4 grid, 128x64 per wave held in registers (int8: 2x4 v_mfma_i32_32x32x32_i8
+// tiles; fp8: v_mfma_f32_32x32x64_f8f6f4). K advances 64 bytes per step through a 4-stage LDS ring
+// (4 x 32 KiB) filled by asynchronous global->LDS loads three steps ahead; each step waits only for the
+// loads of the next step, then one barrier. LDS rows are 64 B; 16-byte chunks are XOR-swizzled by row so
+// the ds_read_b128 fragment loads of 16 consecutive rows hit distinct banks.
 //
 // MFMA roles: the weight tile is the A operand (rows = n) and the activation tile the B operand
 // (columns = m), so each lane's accumulator holds one token m and runs of 4 consecutive n — the
@@ -31,8 +31,11 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 
 enum Epi { EPI_PLAIN = 0, EPI_SWIGLU = 1, EPI_GATED = 2, EPI_ACC = 3 };
 
-constexpr int BM = 256, BN = 256, BK = 64, NT = 256;
-constexpr int TILE_BYTES = BM * BK;  // per operand per stage
+constexpr int BM = 256, BN = 256, BK = 64, NT = 512;
+// 8 waves in a 2 (m) x 4 (n) grid, 128 x 64 outputs per wave: 2 waves per SIMD hide each other's LDS and
+// barrier latency
+constexpr int WAVES = NT / 64, WM = 128, WN = 64, TI = WN / 32, TJ = WM / 32;
+constexpr int TILE_BYTES = BM * BK;  // per operand per stage (BM == BN)
 
 struct GemmArgs {
   const int8_t* x;  // [M, K] int8 or e4m3 codes
@@ -98,10 +101,13 @@ struct Mma<true> {  // e4m3: 1 MFMA of k = 64 per step, 32-byte fragments (two 1
 };
 
 template <bool FP8, int EPI>
-__global__ void __launch_bounds__(NT, 1) gemm_kernel(const GemmArgs a) {
+__global__ void __launch_bounds__(NT, 2) gemm_kernel(const GemmArgs a) {
   using MM = Mma<FP8>;
   using acc_t = typename MM::acc_t;
-  __shared__ __attribute__((aligned(16))) int8_t lds[2][2][TILE_BYTES];  // [stage][x|w]
+  // 4-stage ring, each stage its own LDS object {x tile, w tile} (2 x 16 KiB) named statically: the
+  // asynchronous global->LDS loads into one stage then provably do not alias the reads of another
+  __shared__ __attribute__((aligned(16))) int8_t st0[2 * TILE_BYTES], st1[2 * TILE_BYTES], st2[2 * TILE_BYTES],
+      st3[2 * TILE_BYTES];
 
   // XCD-aware tile order: workgroup id b runs on XCD b % 8; give XCD x the contiguous logical range
   const int nb = a.tiles_m * a.tiles_n;
@@ -112,94 +118,101 @@ __global__ void __launch_bounds__(NT, 1) gemm_kernel(const GemmArgs a) {
   const int64_t m0 = static_cast<int64_t>(tm) * BM, n0 = static_cast<int64_t>(tn) * BN;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave >> 2, wn = wave & 3;
   const int l32 = lane & 31, g = lane >> 5;
 
-  // global -> register staging: 4 chunks of 16 B per operand per thread
-  const int8_t* xp[4];
-  const int8_t* wp[4];
-  int lofs[4];
+  // Global -> LDS loads bypass VGPRs (global_load_lds_dwordx4: lane l of a wave writes LDS base + 16*l),
+  // so the XOR swizzle is applied on the global side: stage position p (16-byte units, 1024 per operand)
+  // holds row p / 4, logical chunk (p % 4) ^ f(row) (swz is an involution on the chunk index). Wave w
+  // fills positions (2w + i)*64 + lane, i = 0, 1, of each operand.
+  const int8_t* xp[2];
+  const int8_t* wp[2];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int id = tid + NT * i, r = id >> 2, c = id & 3;
+  for (int i = 0; i < 2; ++i) {
+    const int p = (2 * wave + i) * 64 + lane, r = p >> 2;
+    const int c = (p & 3) ^ (((r >> 1) & 3) ^ ((r >> 3) & 1));
     int64_t mr = m0 + r, nr = n0 + r;
     mr = mr < a.M ? mr : a.M - 1;
     nr = nr < a.N ? nr : a.N - 1;
     xp[i] = a.x + mr * a.ldx + c * 16;
     wp[i] = a.w + nr * a.ldw + c * 16;
-    lofs[i] = swz(r, c);
   }
-  uint4 sx0, sx1, sx2, sx3, sw0, sw1, sw2, sw3;
-#define RH3_GLOAD(k0)                                                   \
-  do {                                                                  \
-    sx0 = *reinterpret_cast<const uint4*>(xp[0] + (k0));                \
-    sx1 = *reinterpret_cast<const uint4*>(xp[1] + (k0));                \
-    sx2 = *reinterpret_cast<const uint4*>(xp[2] + (k0));                \
-    sx3 = *reinterpret_cast<const uint4*>(xp[3] + (k0));                \
-    sw0 = *reinterpret_cast<const uint4*>(wp[0] + (k0));                \
-    sw1 = *reinterpret_cast<const uint4*>(wp[1] + (k0));                \
-    sw2 = *reinterpret_cast<const uint4*>(wp[2] + (k0));                \
-    sw3 = *reinterpret_cast<const uint4*>(wp[3] + (k0));                \
-  } while (0)
-#define RH3_SSTORE(st)                                                  \
-  do {                                                                  \
-    *reinterpret_cast<uint4*>(&lds[st][0][lofs[0]]) = sx0;              \
-    *reinterpret_cast<uint4*>(&lds[st][0][lofs[1]]) = sx1;              \
-    *reinterpret_cast<uint4*>(&lds[st][0][lofs[2]]) = sx2;              \
-    *reinterpret_cast<uint4*>(&lds[st][0][lofs[3]]) = sx3;              \
-    *reinterpret_cast<uint4*>(&lds[st][1][lofs[0]]) = sw0;              \
-    *reinterpret_cast<uint4*>(&lds[st][1][lofs[1]]) = sw1;              \
-    *reinterpret_cast<uint4*>(&lds[st][1][lofs[2]]) = sw2;              \
-    *reinterpret_cast<uint4*>(&lds[st][1][lofs[3]]) = sw3;              \
-  } while (0)
+  const int nk = static_cast<int>(a.K / BK);
+  // loads of k-step kt into a stage (clamped to the last step so every step issues the same four
+  // loads and the vmcnt bookkeeping stays exact; a clamped load lands in a stage nobody reads again)
+  auto gload = [&](int kt, int8_t* stg) __attribute__((always_inline)) {
+    const int64_t k0 = static_cast<int64_t>(min(kt, nk - 1)) * BK;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      __builtin_amdgcn_global_load_lds(xp[i] + k0, stg + (2 * wave + i) * 1024, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(wp[i] + k0, stg + TILE_BYTES + (2 * wave + i) * 1024, 16, 0, 0);
+    }
+  };
 
-  acc_t acc[4][4];
+  acc_t acc[TI][TJ];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < TI; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < TJ; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
 
-  const int nk = static_cast<int>(a.K / BK);
-  RH3_GLOAD(0);
-  RH3_SSTORE(0);
-  __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < nk) RH3_GLOAD(static_cast<int64_t>(kt + 1) * BK);
-    const int8_t* ldx = lds[cur][0];
-    const int8_t* ldw = lds[cur][1];
+  // k-step kt: load step kt+3 into the stage step kt-1 used, compute from this stage, then wait for
+  // step kt+1's loads (the 8 most recent loads, steps kt+2 and kt+3, stay in flight) and barrier
+  auto step = [&](const int kt, const int8_t* cur, int8_t* nxt3) __attribute__((always_inline)) {
+    gload(kt + 3, nxt3);
+    const int8_t* ldx = cur;
+    const int8_t* ldw = cur + TILE_BYTES;
 #pragma unroll
     for (int ks = 0; ks < MM::KSUB; ++ks) {
-      typename MM::frag_t fa[4], fb[4];
+      typename MM::frag_t fa[TI], fb[TJ];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) fa[i] = MM::load(ldw, wn * 128 + i * 32 + l32, ks, g);
+      for (int i = 0; i < TI; ++i) fa[i] = MM::load(ldw, wn * WN + i * 32 + l32, ks, g);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) fb[j] = MM::load(ldx, wm * 128 + j * 32 + l32, ks, g);
+      for (int j = 0; j < TJ; ++j) fb[j] = MM::load(ldx, wm * WM + j * 32 + l32, ks, g);
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < TI; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = MM::mma(fa[i], fb[j], acc[i][j]);
+        for (int j = 0; j < TJ; ++j) acc[i][j] = MM::mma(fa[i], fb[j], acc[i][j]);
     }
-    if (kt + 1 < nk) RH3_SSTORE(cur ^ 1);
-    __syncthreads();
+    // s_waitcnt on gfx9: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14];
+    // vmcnt(8) expcnt(7) lgkmcnt(0) = 8 | 0x70
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0x0078);
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+
+  gload(0, st0);
+  gload(1, st1);
+  gload(2, st2);
+  asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+  __syncthreads();
+  int kt = 0;
+  for (; kt + 4 <= nk; kt += 4) {
+    step(kt + 0, st0, st3);
+    step(kt + 1, st1, st0);
+    step(kt + 2, st2, st1);
+    step(kt + 3, st3, st2);
   }
-#undef RH3_GLOAD
-#undef RH3_SSTORE
+  const int rem = nk - kt;  // steps left: they read stages 0, 1, 2 in order
+  if (rem >= 1) step(kt + 0, st0, st3);
+  if (rem >= 2) step(kt + 1, st1, st0);
+  if (rem >= 3) step(kt + 2, st2, st1);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no global->LDS load outlives the workgroup
 
   // epilogue: acc[i][j] register r holds m = m0 + wm*128 + j*32 + l32,
-  //           n = n0 + wn*128 + i*32 + 8*(r/4) + 4*g + (r%4)
+  //           n = n0 + wn*64 + i*32 + 8*(r/4) + 4*g + (r%4)
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int64_t m = m0 + wm * 128 + j * 32 + l32;
+  for (int j = 0; j < TJ; ++j) {
+    const int64_t m = m0 + wm * WM + j * 32 + l32;
     const bool mok = m < a.M;
     const float xsm = (EPI != EPI_ACC && mok) ? a.xs[m] : 0.0f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < TI; ++i) {
 #pragma unroll
       for (int rq = 0; rq < 4; ++rq) {
-        const int64_t n = n0 + wn * 128 + i * 32 + 8 * rq + 4 * g;
+        const int64_t n = n0 + wn * WN + i * 32 + 8 * rq + 4 * g;
         const bool ok = mok && n < a.N;
         if constexpr (EPI == EPI_ACC) {
           static_assert(!FP8, "raw accumulators are an int8 feature");
