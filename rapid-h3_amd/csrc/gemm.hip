@@ -35,6 +35,10 @@ constexpr int BM = 256, BN = 256, BK = 64, NT = 512;
 // 8 waves in a 2 (m) x 4 (n) grid, 128 x 64 outputs per wave: 2 waves per SIMD hide each other's LDS and
 // barrier latency
 constexpr int WAVES = NT / 64, WM = 128, WN = 64, TI = WN / 32, TJ = WM / 32;
+#ifndef RH3_GEMM_GROUP_M
+#define RH3_GEMM_GROUP_M 1
+#endif
+constexpr int GROUP_M = RH3_GEMM_GROUP_M;
 constexpr int TILE_BYTES = BM * BK;  // per operand per stage (BM == BN)
 
 struct GemmArgs {
@@ -114,7 +118,12 @@ __global__ void __launch_bounds__(NT, 2) gemm_kernel(const GemmArgs a) {
   const int b = blockIdx.x;
   const int xcd = b % 8, slot = b / 8;
   const int lt = xcd * (nb / 8) + min(xcd, nb % 8) + slot;  // XCD x owns logical tiles [prefix(x), prefix(x+1))
-  const int tm = lt / a.tiles_n, tn = lt % a.tiles_n;
+  // grouped order: GROUP_M consecutive M tiles per N column, so the ~32 tiles an XCD runs at once form a
+  // GROUP_M x (32 / GROUP_M) block that shares activation and weight panels in that XCD's L2
+  const int group = lt / (GROUP_M * a.tiles_n), first_m = group * GROUP_M;
+  const int gsz = min(a.tiles_m - first_m, GROUP_M);
+  const int tm = first_m + (lt % (GROUP_M * a.tiles_n)) % gsz;
+  const int tn = (lt % (GROUP_M * a.tiles_n)) / gsz;
   const int64_t m0 = static_cast<int64_t>(tm) * BM, n0 = static_cast<int64_t>(tn) * BN;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -157,30 +166,46 @@ __global__ void __launch_bounds__(NT, 2) gemm_kernel(const GemmArgs a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
 
-  // k-step kt: load step kt+3 into the stage step kt-1 used, compute from this stage, then wait for
-  // step kt+1's loads (the 8 most recent loads, steps kt+2 and kt+3, stay in flight) and barrier
-  auto step = [&](const int kt, const int8_t* cur, int8_t* nxt3) __attribute__((always_inline)) {
-    gload(kt + 3, nxt3);
-    const int8_t* ldx = cur;
-    const int8_t* ldw = cur + TILE_BYTES;
-#pragma unroll
-    for (int ks = 0; ks < MM::KSUB; ++ks) {
-      typename MM::frag_t fa[TI], fb[TJ];
-#pragma unroll
-      for (int i = 0; i < TI; ++i) fa[i] = MM::load(ldw, wn * WN + i * 32 + l32, ks, g);
-#pragma unroll
-      for (int j = 0; j < TJ; ++j) fb[j] = MM::load(ldx, wm * WM + j * 32 + l32, ks, g);
-#pragma unroll
-      for (int i = 0; i < TI; ++i)
-#pragma unroll
-        for (int j = 0; j < TJ; ++j) acc[i][j] = MM::mma(fa[i], fb[j], acc[i][j]);
-    }
-    // s_waitcnt on gfx9: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14];
-    // vmcnt(8) expcnt(7) lgkmcnt(0) = 8 | 0x70
+  // s_waitcnt on gfx9: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14]; 0x0078 is vmcnt(8)
+  // expcnt(7) lgkmcnt(0). The empty asm statements keep the compiler from moving memory accesses across.
+  auto sync_next = [&]() __attribute__((always_inline)) {
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_waitcnt(0x0078);
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
+  };
+  typename MM::frag_t fa0[TI], fb0[TJ], fa1[TI], fb1[TJ];
+  auto load_frags = [&](const int8_t* stg, const int ks, typename MM::frag_t* fa, typename MM::frag_t* fb)
+      __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < TI; ++i) fa[i] = MM::load(stg + TILE_BYTES, wn * WN + i * 32 + l32, ks, g);
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) fb[j] = MM::load(stg, wm * WM + j * 32 + l32, ks, g);
+  };
+  auto mma_all = [&](const typename MM::frag_t* fa, const typename MM::frag_t* fb) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+      for (int j = 0; j < TJ; ++j) acc[i][j] = MM::mma(fa[i], fb[j], acc[i][j]);
+  };
+  // k-step kt, reading stage cur; loads step kt+3 into nxt3 (the stage of step kt-1, whose readers all
+  // passed the previous step's barrier). int8 (two k = 32 halves): the fragments of half 0 were read at
+  // the end of the previous step; read half 1, run half 0's MFMAs, wait for step kt+1's loads (the 8 most
+  // recent loads, steps kt+2 and kt+3, stay in flight) and barrier, then read half 0 of step kt+1 while
+  // half 1's MFMAs run, so the LDS latency after the barrier hides behind the MFMA tail.
+  auto step = [&](const int kt, const int8_t* cur, const int8_t* nxt1, int8_t* nxt3) __attribute__((always_inline)) {
+    gload(kt + 3, nxt3);
+    if constexpr (MM::KSUB == 2) {
+      load_frags(cur, 1, fa1, fb1);
+      mma_all(fa0, fb0);
+      sync_next();
+      load_frags(nxt1, 0, fa0, fb0);
+      mma_all(fa1, fb1);
+    } else {
+      load_frags(cur, 0, fa1, fb1);
+      mma_all(fa1, fb1);
+      sync_next();
+    }
   };
 
   gload(0, st0);
@@ -188,35 +213,33 @@ __global__ void __launch_bounds__(NT, 2) gemm_kernel(const GemmArgs a) {
   gload(2, st2);
   asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
   __syncthreads();
+  if constexpr (MM::KSUB == 2) load_frags(st0, 0, fa0, fb0);
   int kt = 0;
   for (; kt + 4 <= nk; kt += 4) {
-    step(kt + 0, st0, st3);
-    step(kt + 1, st1, st0);
-    step(kt + 2, st2, st1);
-    step(kt + 3, st3, st2);
+    step(kt + 0, st0, st1, st3);
+    step(kt + 1, st1, st2, st0);
+    step(kt + 2, st2, st3, st1);
+    step(kt + 3, st3, st0, st2);
   }
   const int rem = nk - kt;  // steps left: they read stages 0, 1, 2 in order
-  if (rem >= 1) step(kt + 0, st0, st3);
-  if (rem >= 2) step(kt + 1, st1, st0);
-  if (rem >= 3) step(kt + 2, st2, st1);
+  if (rem >= 1) step(kt + 0, st0, st1, st3);
+  if (rem >= 2) step(kt + 1, st1, st2, st0);
+  if (rem >= 3) step(kt + 2, st2, st3, st1);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no global->LDS load outlives the workgroup
 
   // epilogue: acc[i][j] register r holds m = m0 + wm*128 + j*32 + l32,
   //           n = n0 + wn*64 + i*32 + 8*(r/4) + 4*g + (r%4)
+  if constexpr (EPI == EPI_ACC) {
+    static_assert(!FP8, "raw accumulators are an int8 feature");
 #pragma unroll
-  for (int j = 0; j < TJ; ++j) {
-    const int64_t m = m0 + wm * WM + j * 32 + l32;
-    const bool mok = m < a.M;
-    const float xsm = (EPI != EPI_ACC && mok) ? a.xs[m] : 0.0f;
+    for (int j = 0; j < TJ; ++j) {
+      const int64_t m = m0 + wm * WM + j * 32 + l32;
 #pragma unroll
-    for (int i = 0; i < TI; ++i) {
+      for (int i = 0; i < TI; ++i)
 #pragma unroll
-      for (int rq = 0; rq < 4; ++rq) {
-        const int64_t n = n0 + wn * WN + i * 32 + 8 * rq + 4 * g;
-        const bool ok = mok && n < a.N;
-        if constexpr (EPI == EPI_ACC) {
-          static_assert(!FP8, "raw accumulators are an int8 feature");
-          if (ok) {
+        for (int rq = 0; rq < 4; ++rq) {
+          const int64_t n = n0 + wn * WN + i * 32 + 8 * rq + 4 * g;
+          if (m < a.M && n < a.N) {
             int4 v;
             v.x = acc[i][j][4 * rq + 0];
             v.y = acc[i][j][4 * rq + 1];
@@ -224,59 +247,81 @@ __global__ void __launch_bounds__(NT, 2) gemm_kernel(const GemmArgs a) {
             v.w = acc[i][j][4 * rq + 3];
             *reinterpret_cast<int4*>(static_cast<int32_t*>(a.out) + m * a.ldo + n) = v;
           }
-          continue;
         }
-        float y[4];
-        float4 wsn = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (n < a.N) wsn = *reinterpret_cast<const float4*>(a.ws + n);
-        const float wsv[4] = {wsn.x, wsn.y, wsn.z, wsn.w};
+    }
+  } else {
+    // bf16(y) (plain: bf16(y + bias)) goes through LDS so that the global side reads and writes whole
+    // 128-byte row segments: each wave stages its 128 x 64 block (16 KiB, row r at r*128, 16-byte chunk c
+    // at c ^ (r & 7)) in the now idle ring, then lane l handles row 8*it + l/8, columns 8*(l%8)..+7.
+    __syncthreads();  // every wave is done reading the ring
+    int8_t* const stage = (wave >> 1) == 0 ? st0 : (wave >> 1) == 1 ? st1 : (wave >> 1) == 2 ? st2 : st3;
+    int8_t* const ep = stage + (wave & 1) * 16384;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) y[e] = (MM::val(acc[i][j], 4 * rq + e) * xsm) * wsv[e];
-        if constexpr (EPI == EPI_PLAIN) {
-          if (ok) {
-            if (a.bias) {
+    for (int j = 0; j < TJ; ++j) {
+      const int row = j * 32 + l32;
+      const int64_t m = m0 + wm * WM + row;
+      const float xsm = m < a.M ? a.xs[m] : 0.0f;
+#pragma unroll
+      for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int rq = 0; rq < 4; ++rq) {
+          const int col = i * 32 + 8 * rq + 4 * g;
+          const int64_t n = n0 + wn * WN + col;
+          float4 wsn = make_float4(0.f, 0.f, 0.f, 0.f);
+          if (n < a.N) wsn = *reinterpret_cast<const float4*>(a.ws + n);
+          float y[4] = {(MM::val(acc[i][j], 4 * rq + 0) * xsm) * wsn.x, (MM::val(acc[i][j], 4 * rq + 1) * xsm) * wsn.y,
+                        (MM::val(acc[i][j], 4 * rq + 2) * xsm) * wsn.z, (MM::val(acc[i][j], 4 * rq + 3) * xsm) * wsn.w};
+          if constexpr (EPI == EPI_PLAIN) {
+            if (a.bias && n < a.N) {
               const uint2 bb = *reinterpret_cast<const uint2*>(a.bias + n);
               y[0] = y[0] + __uint_as_float(bb.x << 16);
               y[1] = y[1] + __uint_as_float(bb.x & 0xffff0000u);
               y[2] = y[2] + __uint_as_float(bb.y << 16);
               y[3] = y[3] + __uint_as_float(bb.y & 0xffff0000u);
             }
-            uint2 o;
-            o.x = pack_bf2(y[0], y[1]);
-            o.y = pack_bf2(y[2], y[3]);
-            *reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.out) + m * a.ldo + n) = o;
           }
-        } else if constexpr (EPI == EPI_GATED) {
-          if (ok) {
-            uint16_t* rp = static_cast<uint16_t*>(a.out) + m * a.ldo + n;
-            const uint2 rr = *reinterpret_cast<const uint2*>(rp);
-            const uint2 gg = *reinterpret_cast<const uint2*>(a.gate + n);
-            const float rv[4] = {__uint_as_float(rr.x << 16), __uint_as_float(rr.x & 0xffff0000u),
-                                 __uint_as_float(rr.y << 16), __uint_as_float(rr.y & 0xffff0000u)};
-            const float gv[4] = {__uint_as_float(gg.x << 16), __uint_as_float(gg.x & 0xffff0000u),
-                                 __uint_as_float(gg.y << 16), __uint_as_float(gg.y & 0xffff0000u)};
-            float o4[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) o4[e] = fmaf(round_bf(y[e]), gv[e], rv[e]);
-            uint2 o;
-            o.x = pack_bf2(o4[0], o4[1]);
-            o.y = pack_bf2(o4[2], o4[3]);
-            *reinterpret_cast<uint2*>(rp) = o;
-          }
-        } else {  // EPI_SWIGLU: lanes g = 0 hold gate columns 4j..4j+3, lanes g = 1 the matching up columns
-          float other[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) other[e] = __shfl_xor(y[e], 32, 64);
-          if (g == 0 && ok) {
-            float h[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) h[e] = silu_mul(round_bf(y[e]), round_bf(other[e]));
-            uint2 o;
-            o.x = pack_bf2(h[0], h[1]);
-            o.y = pack_bf2(h[2], h[3]);
-            *reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.out) + m * a.ldo + n / 2) = o;
-          }
+          uint2 o;
+          o.x = pack_bf2(y[0], y[1]);
+          o.y = pack_bf2(y[2], y[3]);
+          const int ch = col >> 3;  // 16-byte chunk; this lane's 8 bytes are its half g
+          *reinterpret_cast<uint2*>(ep + row * 128 + ((ch ^ (row & 7)) << 4) + 8 * g) = o;
         }
+    }
+    // each lane reads back what other lanes of its own wave wrote: LDS executes a wave's accesses in
+    // order, and the compiler keeps the reads after the writes (same array)
+    const int ch = lane & 7;
+    const int64_t n = n0 + wn * WN + ch * 8;
+    const bool nok = n < a.N;
+    float gv[8];
+    if constexpr (EPI == EPI_GATED) {
+      if (nok) unpack8(*reinterpret_cast<const uint4*>(a.gate + n), gv);
+    }
+#pragma unroll 4
+    for (int it = 0; it < WM / 8; ++it) {
+      const int row = it * 8 + (lane >> 3);
+      const int64_t m = m0 + wm * WM + row;
+      const uint4 v = *reinterpret_cast<const uint4*>(ep + row * 128 + ((ch ^ (row & 7)) << 4));
+      if (m >= a.M || !nok) continue;
+      if constexpr (EPI == EPI_PLAIN) {
+        *reinterpret_cast<uint4*>(static_cast<uint16_t*>(a.out) + m * a.ldo + n) = v;
+      } else if constexpr (EPI == EPI_GATED) {
+        uint16_t* rp = static_cast<uint16_t*>(a.out) + m * a.ldo + n;
+        float yv[8], rv[8];
+        unpack8(v, yv);
+        unpack8(*reinterpret_cast<const uint4*>(rp), rv);
+        uint4 o;
+        o.x = pack_bf2(fmaf(yv[0], gv[0], rv[0]), fmaf(yv[1], gv[1], rv[1]));
+        o.y = pack_bf2(fmaf(yv[2], gv[2], rv[2]), fmaf(yv[3], gv[3], rv[3]));
+        o.z = pack_bf2(fmaf(yv[4], gv[4], rv[4]), fmaf(yv[5], gv[5], rv[5]));
+        o.w = pack_bf2(fmaf(yv[6], gv[6], rv[6]), fmaf(yv[7], gv[7], rv[7]));
+        *reinterpret_cast<uint4*>(rp) = o;
+      } else {  // EPI_SWIGLU: the 8 columns are one [gate 4j..4j+3 | up 4j..4j+3] group of swiglu_perm
+        float yv[8];
+        unpack8(v, yv);
+        uint2 o;
+        o.x = pack_bf2(silu_mul(yv[0], yv[4]), silu_mul(yv[1], yv[5]));
+        o.y = pack_bf2(silu_mul(yv[2], yv[6]), silu_mul(yv[3], yv[7]));
+        *reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.out) + m * a.ldo + n / 2) = o;
       }
     }
   }
@@ -304,7 +349,7 @@ int check(const char* name, const void* xq, int64_t ldx, const void* wq, int64_t
   RH3_REQUIRE(ldx >= K && ldw >= K && ldx % 16 == 0 && ldw % 16 == 0,
               "%s: operand row strides (%lld, %lld) must be >= K and multiples of 16", name, (long long)ldx,
               (long long)ldw);
-  RH3_REQUIRE(ldo >= out_cols && ldo % 4 == 0, "%s: output row stride %lld invalid (need >= %lld, multiple of 4)",
+  RH3_REQUIRE(ldo >= out_cols && ldo % 8 == 0, "%s: output row stride %lld invalid (need >= %lld, multiple of 8)",
               name, (long long)ldo, (long long)out_cols);
   RH3_REQUIRE(aligned16(xq) && aligned16(wq) && aligned16(out), "%s: operands must be 16-byte aligned", name);
   return RH3_OK;
