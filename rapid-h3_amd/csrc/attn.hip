@@ -243,28 +243,59 @@ __device__ __forceinline__ int kswz(int r, int c) { return r * 128 + ((c ^ ((r ^
 // Vt tile: 128 rows (d) x 256 B, chunk c of row r at c ^ (r & 15)
 __device__ __forceinline__ int vswz(int r, int c) { return r * 256 + ((c ^ (r & 15)) << 4); }
 
-// 8 waves (2 per SIMD, so one wave's softmax overlaps the other's MFMAs), 256 queries per workgroup:
-// wave w owns queries qb*256 + 32*w .. +31, inside 128-query scale block 2*qb + w/4.
-constexpr int FWD_WAVES = 8, FWD_NT = FWD_WAVES * 64, FWD_BQ = FWD_WAVES * 32;
-// lazy rescale: the reference max moves only when a tile max exceeds it by more than 2^8 (P <= 256)
+// 12 waves (3 per SIMD), 32 queries each = 384 queries per workgroup (three 128-query scale blocks);
+// ~168 registers per wave, so a step covers 64 keys. Per wave and step: 8 i8 MFMAs (S^T = K Q^T), 16 bf16
+// MFMAs (O^T += V^T P^T) and ~150 VALU instructions (32 scores: convert, scale, exp2, pack, row sum, max).
+constexpr int FWD_WAVES = 12, FWD_NT = FWD_WAVES * 64, FWD_BQ = FWD_WAVES * 32;
+constexpr int STEP = 64;  // keys per step
+// lazy rescale: the reference max moves only when a step max exceeds it by more than 2^8 (P <= 256)
 constexpr float RESCALE_LOG2 = 8.0f;
 
 typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) const v4i lds_v4i;
 
 __device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
   const v2bf v = {static_cast<__bf16>(a), static_cast<__bf16>(b)};  // v_cvt_pk_bf16_f32, RNE
   return __builtin_bit_cast(uint32_t, v);
 }
 
+// 16-byte LDS read at a byte address (the immediate offset folds into ds_read_b128)
+__device__ __forceinline__ v4i lds_read16(uint32_t addr) {
+  return *reinterpret_cast<lds_v4i*>(static_cast<uintptr_t>(addr));
+}
+
+// max of lane l and lane l ^ 32 (v_permlane32_swap exchanges the wave's halves)
+__device__ __forceinline__ int max_halves(int v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return max(static_cast<int>(r[0]), static_cast<int>(r[1]));
+}
+
+// Global -> LDS copy of 16 bytes per lane: lane l of the wave writes LDS byte offset lds_base + 16*l
+// (M0 holds the wave-uniform base). Issued from inline assembly so that the compiler adds no wait of
+// its own for it: the kernel below accounts for these loads itself (s_waitcnt vmcnt) and issues no
+// other vector-memory loads while they are in flight. gfx9 requires one wait state between writing M0
+// and an LDS DMA that reads it.
+__device__ __forceinline__ void lds_dma16(const void* gptr, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds_base)
+               : "memory", "m0");
+}
+
+// Step j (64 keys) reads K(j) and V^T(j) from ring slot j % 4 and first loads K(j+2), V^T(j+2) into slot
+// (j+2) % 4, last read in step j-2 (every wave has passed the end-of-step barrier of step j-1). A slot
+// holds K: 64 keys x 128 B (chunk c of row r at c ^ ((r ^ (r >> 3)) & 7)), then V^T: 128 d x 64 keys x
+// 2 B (chunk c of row r at c ^ (r & 7)). Steps past Sk are not run; the ragged last step is a separate
+// instantiation, so the full steps carry no key mask.
 __global__ void __launch_bounds__(FWD_NT, 1) attn_fwd_kernel(const FwdArgs a) {
-  __shared__ __attribute__((aligned(16))) int8_t klds[2][BLK * D];
-  __shared__ __attribute__((aligned(16))) int8_t vlds[2][D * BLK * 2];
+  constexpr int KB = STEP * D, VB = D * STEP * 2, SLOT = KB + VB;
+  __shared__ __attribute__((aligned(16))) int8_t ring[4 * SLOT];
+  __shared__ float kscale[4096];  // per-128-key-block K scales of this head (Skpad/128 <= 4096)
   const int h = blockIdx.y, qb = blockIdx.x;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, g = lane >> 5;
   const int64_t q = static_cast<int64_t>(qb) * FWD_BQ + wave * 32 + l32;
 
-  // the Q operands are padded to 128 queries; a workgroup's last 128 may lie past them (then they are
+  // the Q operands are padded to 128 queries; a workgroup's last blocks may lie past them (then they are
   // computed on zero codes and never stored)
   const bool qin = q < a.Sqpad;
   v4i qf[4];
@@ -274,36 +305,67 @@ __global__ void __launch_bounds__(FWD_NT, 1) attn_fwd_kernel(const FwdArgs a) {
     for (int ds = 0; ds < 4; ++ds) qf[ds] = qin ? *reinterpret_cast<const v4i*>(qp + ds * 32) : v4i{0, 0, 0, 0};
   }
   const float qscale = (qin ? a.qs[static_cast<int64_t>(h) * (a.Sqpad / BLK) + (q >> 7)] : 0.0f) * a.scale_log2;
+  const int nkb = static_cast<int>(a.Skpad / BLK);
+  for (int i = tid; i < nkb; i += FWD_NT) kscale[i] = a.ks[static_cast<int64_t>(h) * nkb + i];
 
   const int8_t* kbase = a.k8 + static_cast<int64_t>(h) * a.Skpad * D;
   const uint16_t* vbase = a.vt + static_cast<int64_t>(h) * D * a.Skpad;
-  const float* ksb = a.ks + static_cast<int64_t>(h) * (a.Skpad / BLK);
-  // K tile (1024 chunks): chunk id tid + 512 i -> key row id / 8, chunk id % 8
-  // V^T tile (2048 chunks): chunk id tid + 512 i -> d row id / 16 = tid / 16 + 32 i, chunk tid % 16
-  const int vd = tid >> 4, vc = tid & 15;
-  const uint16_t* vrow = vbase + static_cast<int64_t>(vd) * a.Skpad + vc * 8;
-  const int64_t vstep = 32 * a.Skpad;
-  uint4 sk0, sk1, sv0, sv1, sv2, sv3;
-#define RH3_GLOAD(kt)                                                                   \
-  do {                                                                                  \
-    const int8_t* kp = kbase + static_cast<int64_t>(kt) * BLK * D + tid * 16;           \
-    sk0 = *reinterpret_cast<const uint4*>(kp);                                          \
-    sk1 = *reinterpret_cast<const uint4*>(kp + 8192);                                   \
-    const uint16_t* vp = vrow + static_cast<int64_t>(kt) * BLK;                         \
-    sv0 = *reinterpret_cast<const uint4*>(vp);                                          \
-    sv1 = *reinterpret_cast<const uint4*>(vp + vstep);                                  \
-    sv2 = *reinterpret_cast<const uint4*>(vp + 2 * vstep);                              \
-    sv3 = *reinterpret_cast<const uint4*>(vp + 3 * vstep);                              \
-  } while (0)
-#define RH3_SSTORE(st)                                                                  \
-  do {                                                                                  \
-    *reinterpret_cast<uint4*>(&klds[st][kswz((tid >> 3) + 0, tid & 7)]) = sk0;          \
-    *reinterpret_cast<uint4*>(&klds[st][kswz((tid >> 3) + 64, tid & 7)]) = sk1;         \
-    *reinterpret_cast<uint4*>(&vlds[st][vswz(vd + 0, vc)]) = sv0;                       \
-    *reinterpret_cast<uint4*>(&vlds[st][vswz(vd + 32, vc)]) = sv1;                      \
-    *reinterpret_cast<uint4*>(&vlds[st][vswz(vd + 64, vc)]) = sv2;                      \
-    *reinterpret_cast<uint4*>(&vlds[st][vswz(vd + 96, vc)]) = sv3;                      \
-  } while (0)
+  // Loads go global -> LDS directly (lane l of a wave writes LDS base + 16*l), so the XOR swizzle is
+  // applied on the global side. K slot: 512 chunk positions (64 rows x 8), loaded by waves 0-7 (one
+  // instruction each); V^T slot: 1024 positions (128 rows x 8), waves 0-7 fill positions 64w + lane and
+  // waves 8-11 positions 512 + 64*(2(w-8) + i) + lane. Every wave issues exactly two loads per step.
+  const int8_t* src0;
+  const int8_t* src1;
+  int dst0, dst1;  // byte offsets inside a slot
+  {
+    auto kpos = [&](int p, const int8_t*& src, int& dst) {
+      const int row = p >> 3, pc = p & 7;
+      src = kbase + row * 128 + ((pc ^ ((row ^ (row >> 3)) & 7)) << 4);
+      dst = p * 16;
+    };
+    auto vpos = [&](int p, const int8_t*& src, int& dst) {
+      const int d = p >> 3, pc = p & 7;
+      src = reinterpret_cast<const int8_t*>(vbase + static_cast<int64_t>(d) * a.Skpad + ((pc ^ (d & 7)) << 3));
+      dst = KB + p * 16;
+    };
+    if (wave < 8) {
+      kpos(wave * 64 + lane, src0, dst0);
+      vpos(wave * 64 + lane, src1, dst1);
+    } else {
+      vpos(512 + (2 * (wave - 8)) * 64 + lane, src0, dst0);
+      vpos(512 + (2 * (wave - 8) + 1) * 64 + lane, src1, dst1);
+    }
+  }
+  // per-step advance of the two sources: K rows move 64 keys x 128 B, V^T columns 64 keys x 2 B
+  const int64_t adv0 = wave < 8 ? STEP * D : STEP * 2, adv1 = STEP * 2;
+  // steps that hold keys below Sk; the key side is padded to 128, so nsteps * 64 <= Skpad
+  const int nfull = static_cast<int>(a.Sk / STEP), rem = static_cast<int>(a.Sk % STEP);
+  const int nsteps = nfull + (rem > 0);
+  // wave-uniform LDS bases (lane 0's offsets) of the two copies inside slot 0
+  const uint32_t ring_lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(ring));
+  const uint32_t dbase0 = ring_lds + __builtin_amdgcn_readfirstlane(dst0);
+  const uint32_t dbase1 = ring_lds + __builtin_amdgcn_readfirstlane(dst1);
+  auto load_step = [&](int j) __attribute__((always_inline)) {
+    const uint32_t so = static_cast<uint32_t>(j & 3) * SLOT;
+    j = min(j, nsteps - 1);  // clamped: every step issues the same two loads; the copy lands unread
+    lds_dma16(src0 + adv0 * j, dbase0 + so);
+    lds_dma16(src1 + adv1 * j, dbase1 + so);
+  };
+
+  // Lane parts of the LDS read addresses inside a slot. K fragment (kb, ds): row kb*32 + l32, chunk
+  // 2ds + g, stored at chunk ^ ((row ^ (row >> 3)) & 7) = (2ds ^ 4kb) ^ y with y = (g ^ l32 ^ (l32 >> 3)) & 7,
+  // so the 8 reads use 4 lane offsets koff[(2ds ^ 4kb) / 2] plus the immediate kb * 4096. V^T fragment
+  // (kb, m, db): row db*32 + l32, chunk 4kb + 2m + g at chunk ^ (l32 & 7): 4 lane offsets voff[2kb + m]
+  // plus the immediate KB + db * 4096.
+  uint32_t koff[4], voff[4];
+  {
+    const int y = (g ^ l32 ^ (l32 >> 3)) & 7;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      koff[i] = ring_lds + l32 * 128 + (((2 * i) ^ y) << 4);
+      voff[i] = ring_lds + l32 * 128 + (((2 * i + g) ^ (l32 & 7)) << 4);
+    }
+  }
 
   v16f o[4];
 #pragma unroll
@@ -313,47 +375,43 @@ __global__ void __launch_bounds__(FWD_NT, 1) attn_fwd_kernel(const FwdArgs a) {
   float mref = -INFINITY, lrow = 0.0f;
   const v2bf ones = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
 
-  const int nkt = static_cast<int>(a.Skpad / BLK);
-  // one 128-key tile; TAIL (the last tile when Sk is not a multiple of 128) masks keys >= Sk. The two
-  // instantiations keep the mask out of the per-score code of every other tile.
-  auto tile = [&](const int kt, auto tail_tag) {
-    constexpr bool TAIL = decltype(tail_tag)::value;
-    const int cur = kt & 1;
-    if (kt + 1 < nkt) RH3_GLOAD(kt + 1);
-    const int8_t* kl = klds[cur];
-    const int8_t* vl = vlds[cur];
-
-    // S^T[key][query] = K8 . Q8^T: lane (l32, g) of s[kb] holds query l32 and keys kb*32 + 8*(r/4) + 4*g + r%4
-    v16i s[4];
+  // one step: TAIL steps hold 1..63 keys below Sk
+  auto step = [&](const int j, auto tail) __attribute__((always_inline)) {
+    constexpr bool TAIL = decltype(tail)::value;
+    load_step(j + 2);
+    const uint32_t so = static_cast<uint32_t>(j & 3) * SLOT;
+    uint32_t ka[4], va[4];
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb)
+    for (int i = 0; i < 4; ++i) {
+      ka[i] = koff[i] + so;
+      va[i] = voff[i] + so;
+    }
+    // S^T[key][query] = K8 . Q8^T: lane (l32, g) of s[kb] holds query l32 and step keys
+    // kb*32 + 8*(r/4) + 4*g + r%4
+    v16i s[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int r = 0; r < 16; ++r) s[kb][r] = 0;
 #pragma unroll
     for (int ds = 0; ds < 4; ++ds) {
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb) {
-        const v4i kf = *reinterpret_cast<const v4i*>(kl + kswz(kb * 32 + l32, ds * 2 + g));
+      for (int kb = 0; kb < 2; ++kb) {
+        const v4i kf = lds_read16(ka[ds ^ (2 * kb)] + kb * 4096);
         s[kb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf, qf[ds], s[kb], 0, 0, 0);
       }
     }
-    int nvalid = BLK;  // keys of this tile below Sk
-    if constexpr (TAIL) {
-      nvalid = static_cast<int>(a.Sk - static_cast<int64_t>(kt) * BLK);
-#pragma unroll
-      for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-          if (kb * 32 + 8 * (r >> 2) + 4 * g + (r & 3) >= nvalid) s[kb][r] = INT_MIN;
-    }
-    // the scale c > 0, so the tile's max score is c * (max int32 accumulator)
+    // c > 0, so the step's max score is c * (max int32 accumulator over the valid keys); a tail step
+    // holds key j*64, so every query's max covers at least one key
+    const int nvalid = TAIL ? static_cast<int>(a.Sk - static_cast<int64_t>(j) * STEP) : STEP;
     int mi = INT_MIN;
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb)
+    for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) mi = max(mi, s[kb][r]);
-    mi = max(mi, __shfl_xor(mi, 32, 64));
-    const float c = qscale * ksb[kt];
+      for (int r = 0; r < 16; ++r)
+        if (!TAIL || kb * 32 + 8 * (r >> 2) + 4 * g + (r & 3) < nvalid) mi = max(mi, s[kb][r]);
+    mi = max_halves(mi);
+    const float c = qscale * kscale[j >> 1];
     const float mt = static_cast<float>(mi) * c;
     if (__builtin_amdgcn_ballot_w64(mt > mref + RESCALE_LOG2) != 0) {
       const float mnew = fmaxf(mref, mt);
@@ -366,26 +424,35 @@ __global__ void __launch_bounds__(FWD_NT, 1) attn_fwd_kernel(const FwdArgs a) {
         for (int r = 0; r < 16; ++r) o[db][r] = o[db][r] * alpha;
     }
     const float nb = -mref;
-
-    // P = 2^(t - mref) in bf16 (P <= 2^8); the row sum adds exactly these bf16 values
-    uint32_t pk[4][8];
+    // P = 2^(t - mref) in bf16 (P <= 2^8); keys past Sk get P = 0 (lane mask on the packed words)
+    uint32_t pk[2][8];
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb)
+    for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int r = 0; r < 16; r += 2) {
-        float p0 = __builtin_amdgcn_exp2f(fmaf(static_cast<float>(s[kb][r]), c, nb));
-        float p1 = __builtin_amdgcn_exp2f(fmaf(static_cast<float>(s[kb][r + 1]), c, nb));
-        if constexpr (TAIL) {
-          if (kb * 32 + 8 * (r >> 2) + 4 * g + (r & 3) >= nvalid) p0 = 0.0f;
-          if (kb * 32 + 8 * (r >> 2) + 4 * g + ((r + 1) & 3) >= nvalid) p1 = 0.0f;
-        }
+        const float p0 = __builtin_amdgcn_exp2f(fmaf(static_cast<float>(s[kb][r]), c, nb));
+        const float p1 = __builtin_amdgcn_exp2f(fmaf(static_cast<float>(s[kb][r + 1]), c, nb));
         pk[kb][r >> 1] = pk_bf16(p0, p1);
-        lrow = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2bf, pk[kb][r >> 1]), ones, lrow, false);
       }
-
+    if constexpr (TAIL) {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int w = 0; w < 8; ++w) {
+          const int key = kb * 32 + 8 * (w >> 1) + 4 * g + 2 * (w & 1);  // keys of bf16 halves lo / hi
+          const uint32_t lo = key < nvalid ? 0x0000ffffu : 0u, hi = key + 1 < nvalid ? 0xffff0000u : 0u;
+          pk[kb][w] &= lo | hi;
+        }
+    }
+    // the row sum adds exactly the bf16 values the P.V MFMA consumes
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int w = 0; w < 8; ++w)
+        lrow = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2bf, pk[kb][w]), ones, lrow, false);
     // O^T[d][query] += V^T . P^T
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
+    for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
       for (int m = 0; m < 2; ++m) {
         v4i pw;
@@ -393,24 +460,28 @@ __global__ void __launch_bounds__(FWD_NT, 1) attn_fwd_kernel(const FwdArgs a) {
         const v8bf pf = __builtin_bit_cast(v8bf, pw);
 #pragma unroll
         for (int db = 0; db < 4; ++db) {
-          const v4i vw = *reinterpret_cast<const v4i*>(vl + vswz(db * 32 + l32, kb * 4 + m * 2 + g));
+          const v4i vw = lds_read16(va[2 * kb + m] + KB + db * 4096);
           o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, vw), pf, o[db], 0, 0, 0);
         }
       }
     }
-    if (kt + 1 < nkt) RH3_SSTORE(cur ^ 1);
-    __syncthreads();
+    // the loads issued in step j-1 (slot j+1) have landed: each step issues exactly two per wave
+    // (vmcnt(2) leaves this step's two in flight); the empty asm statements keep the compiler from
+    // moving memory accesses across the barrier
+    asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
   };
 
-  RH3_GLOAD(0);
-  RH3_SSTORE(0);
+  load_step(0);
+  load_step(1);
+  // vmcnt(0) through the builtin, so the compiler also sees the Q loads above as complete and adds no
+  // wait of its own inside the loop (gfx9 s_waitcnt: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8])
+  __builtin_amdgcn_s_waitcnt(0x0f70);
   __syncthreads();
-  const bool ragged = a.Sk % BLK != 0;
-  const int nfull = ragged ? nkt - 1 : nkt;
-  for (int kt = 0; kt < nfull; ++kt) tile(kt, std::false_type{});
-  if (ragged) tile(nkt - 1, std::true_type{});
-#undef RH3_GLOAD
-#undef RH3_SSTORE
+  for (int j = 0; j < nfull; ++j) step(j, std::false_type{});
+  if (rem > 0) step(nfull, std::true_type{});
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no global->LDS load outlives the workgroup
 
   const float lt = lrow + __shfl_xor(lrow, 32, 64);
   const float il = 1.0f / lt;
@@ -460,6 +531,8 @@ int check_qkv(const char* name, const uint16_t* q, int64_t q_ss, int64_t q_sh, c
   RH3_REQUIRE(Sq > 0 && Sk > 0 && H > 0, "%s: sizes must be positive (Sq=%lld Sk=%lld H=%lld)", name, (long long)Sq,
               (long long)Sk, (long long)H);
   RH3_REQUIRE(pad(Sq) / BLK < 65536 * 32768ll && H < 65536, "%s: grid too large", name);
+  RH3_REQUIRE(pad(Sk) / BLK <= 4096, "%s: Sk=%lld exceeds the 524288-key limit of the attention kernel", name,
+              (long long)Sk);
   RH3_REQUIRE(q && k && v, "%s: null q/k/v", name);
   RH3_REQUIRE(aligned16(q) && aligned16(k) && aligned16(v), "%s: q/k/v must be 16-byte aligned", name);
   RH3_REQUIRE(q_ss % 8 == 0 && q_sh % 8 == 0 && k_ss % 8 == 0 && k_sh % 8 == 0 && v_ss % 8 == 0 && v_sh % 8 == 0,
