@@ -139,6 +139,27 @@ def traffic_from_profile():
         return json.load(f).get("bytes_per_launch")
 
 
+def traffic_probe(m):
+    """Workload of the rocprofv3 --pmc passes behind profiles/attn_main_traffic.json: one attention main
+    kernel launch at the bench shape (S = m, H = 24, D = 128; pre-pass outside), then a plain device copy
+    of exactly 2^30 bytes whose FETCH_SIZE / WRITE_SIZE readings calibrate the counters."""
+    import torch
+    from rapid_h3 import attention
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(0)
+    q, k, v = (torch.randn(m, HEADS, D, device=dev, generator=g).to(torch.bfloat16) for _ in range(3))
+    pp = attention.prepass(q, k, v)
+    out = torch.empty(m, HEADS, D, dtype=torch.bfloat16, device=dev)
+    torch.cuda.synchronize()
+    attention.forward(pp, m, out=out)
+    src = torch.ones(2 ** 29, dtype=torch.bfloat16, device=dev)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    print(f"traffic probe: attn_fwd_kernel S={m} H={HEADS} D={D}; copy 1073741824 B", flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -146,11 +167,16 @@ def main():
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--tokens", type=int, default=GRID[0] * GRID[1] * GRID[2])
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="run only the attention kernel + a 1 GiB copy (workload of the --pmc passes)")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {a.gpus} is not supported (no multi-GPU path)",
               file=sys.stderr)
         sys.exit(2)
+    if a.traffic_probe:
+        traffic_probe(a.tokens)
+        return
     import torch
     from rapid_h3.block import PHASES, fused_block
     dev = torch.device("cuda:0")
