@@ -248,6 +248,9 @@ __device__ __forceinline__ int vswz(int r, int c) { return r * 256 + ((c ^ (r & 
 // MFMAs (O^T += V^T P^T) and ~150 VALU instructions (32 scores: convert, scale, exp2, pack, row sum, max).
 constexpr int FWD_WAVES = 12, FWD_NT = FWD_WAVES * 64, FWD_BQ = FWD_WAVES * 32;
 constexpr int STEP = 64;  // keys per step
+#ifndef LAG_MASK
+#define LAG_MASK 2  // bit i set: waves 4i..4i+3 (one per SIMD) run half a step behind
+#endif
 // lazy rescale: the reference max moves only when a step max exceeds it by more than 2^8 (P <= 256)
 constexpr float RESCALE_LOG2 = 8.0f;
 
@@ -375,20 +378,17 @@ __global__ void __launch_bounds__(FWD_NT, 1) attn_fwd_kernel(const FwdArgs a) {
   float mref = -INFINITY, lrow = 0.0f;
   const v2bf ones = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
 
-  // one step: TAIL steps hold 1..63 keys below Sk
-  auto step = [&](const int j, auto tail) __attribute__((always_inline)) {
-    constexpr bool TAIL = decltype(tail)::value;
-    load_step(j + 2);
+  // S^T[key][query] = K8 . Q8^T of step j: lane (l32, g) of s[kb] holds query l32 and step keys
+  // kb*32 + 8*(r/4) + 4*g + r%4
+  v16i s[2];
+  auto qk = [&](const int j) __attribute__((always_inline)) {
     const uint32_t so = static_cast<uint32_t>(j & 3) * SLOT;
-    uint32_t ka[4], va[4];
+    uint32_t ka[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      ka[i] = koff[i] + so;
-      va[i] = voff[i] + so;
-    }
-    // S^T[key][query] = K8 . Q8^T: lane (l32, g) of s[kb] holds query l32 and step keys
-    // kb*32 + 8*(r/4) + 4*g + r%4
-    v16i s[2];
+    for (int i = 0; i < 4; ++i) ka[i] = koff[i] + so;
+#ifdef RH3_SETPRIO
+    __builtin_amdgcn_s_setprio(1);
+#endif
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -401,6 +401,17 @@ __global__ void __launch_bounds__(FWD_NT, 1) attn_fwd_kernel(const FwdArgs a) {
         s[kb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf, qf[ds], s[kb], 0, 0, 0);
       }
     }
+#ifdef RH3_SETPRIO
+    __builtin_amdgcn_s_setprio(0);
+#endif
+  };
+  // online softmax of step j's scores and O^T += V^T(j) . P^T; TAIL steps hold 1..63 keys below Sk
+  auto softmax_pv = [&](const int j, auto tail) __attribute__((always_inline)) {
+    constexpr bool TAIL = decltype(tail)::value;
+    const uint32_t so = static_cast<uint32_t>(j & 3) * SLOT;
+    uint32_t va[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) va[i] = voff[i] + so;
     // c > 0, so the step's max score is c * (max int32 accumulator over the valid keys); a tail step
     // holds key j*64, so every query's max covers at least one key
     const int nvalid = TAIL ? static_cast<int>(a.Sk - static_cast<int64_t>(j) * STEP) : STEP;
@@ -451,6 +462,9 @@ __global__ void __launch_bounds__(FWD_NT, 1) attn_fwd_kernel(const FwdArgs a) {
       for (int w = 0; w < 8; ++w)
         lrow = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2bf, pk[kb][w]), ones, lrow, false);
     // O^T[d][query] += V^T . P^T
+#ifdef RH3_SETPRIO
+    __builtin_amdgcn_s_setprio(1);
+#endif
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
@@ -465,12 +479,32 @@ __global__ void __launch_bounds__(FWD_NT, 1) attn_fwd_kernel(const FwdArgs a) {
         }
       }
     }
-    // the loads issued in step j-1 (slot j+1) have landed: each step issues exactly two per wave
-    // (vmcnt(2) leaves this step's two in flight); the empty asm statements keep the compiler from
-    // moving memory accesses across the barrier
+#ifdef RH3_SETPRIO
+    __builtin_amdgcn_s_setprio(0);
+#endif
+  };
+
+  // Barrier B_j ends the use of ring slot j. Every wave runs qk(0), softmax_pv(0), qk(1), ...; leading
+  // waves reach B_j after softmax_pv(j), lagging waves after qk(j), so between B_(j-1) and B_j a lagging
+  // wave runs softmax_pv(j-1) (VALU, then MFMA) while a leading wave runs qk(j) (MFMA, then VALU). Each
+  // wave issues the two loads of step j+2 right after B_(j-1), into slot (j+2) % 4, whose last reader
+  // (softmax_pv(j-2) of a lagging wave) ran before B_(j-1); before B_j it waits for its loads of step
+  // j+1 (vmcnt(2) leaves the two issued after B_(j-1) in flight), so slot j+1 is complete past B_j.
+  const bool lag = (LAG_MASK >> (wave >> 2)) & 1;
+  auto barrier = [&]() __attribute__((always_inline)) {
     asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
+  };
+  auto step = [&](const int j, auto tail) __attribute__((always_inline)) {
+    if (!lag) load_step(j + 2);
+    qk(j);
+    if (lag) {
+      barrier();
+      load_step(j + 3);
+    }
+    softmax_pv(j, tail);
+    if (!lag) barrier();
   };
 
   load_step(0);
@@ -479,6 +513,7 @@ __global__ void __launch_bounds__(FWD_NT, 1) attn_fwd_kernel(const FwdArgs a) {
   // wait of its own inside the loop (gfx9 s_waitcnt: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8])
   __builtin_amdgcn_s_waitcnt(0x0f70);
   __syncthreads();
+  if (lag) load_step(2);
   for (int j = 0; j < nfull; ++j) step(j, std::false_type{});
   if (rem > 0) step(nfull, std::true_type{});
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no global->LDS load outlives the workgroup
