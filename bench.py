@@ -88,8 +88,8 @@ def setup(m, device):
 
 def cpu_baseline(m):
     """The CPU oracle (numpy port of the reference's PyTorch path) on a bounded sample of the same
-    block: every quantizer and GEMM at 2,048 of the M tokens, attention for 128 query rows x all S
-    keys x 1 head, each extrapolated linearly to the full block."""
+    block: every quantizer and GEMM at 16,384 of the M tokens, attention for 2,048 query rows x all S
+    keys x 1 head (about 10 s of CPU work together), each extrapolated linearly to the full block."""
     import numpy as np
     from oracle import attn as oa
     from oracle import gemm as og
@@ -101,7 +101,7 @@ def cpu_baseline(m):
     except Exception:  # noqa: BLE001
         cores = os.cpu_count()
     rng = np.random.default_rng(0)
-    ms = 2048
+    ms = 16384
     t_gemm = 0.0
     x = f32_to_bf16(rng.standard_normal((ms, HIDDEN)).astype(np.float32))
     for n, k in ((3 * HIDDEN, HIDDEN), (HIDDEN, HIDDEN), (2 * FFN, HIDDEN), (HIDDEN, FFN)):
@@ -111,7 +111,7 @@ def cpu_baseline(m):
         xq, xs = oq.quantize_rows(a)
         og.int8_gemm(xq, xs, wq, ws)
         t_gemm += time.perf_counter() - t0
-    rows, s = 128, m
+    rows, s = 2048, m
     q = f32_to_bf16(rng.standard_normal((s, 1, D)).astype(np.float32))
     k = f32_to_bf16(rng.standard_normal((s, 1, D)).astype(np.float32))
     v = f32_to_bf16(rng.standard_normal((s, 1, D)).astype(np.float32))
