@@ -72,6 +72,43 @@ int rh3_quant_swiglu_i8(const uint16_t* x, int64_t ldx, int64_t M, int64_t F,
                         int8_t* q, int64_t ldq, float* s, hipStream_t stream);
 
 /* ---------------------------------------------------------------------------------------------
+ * ConvRot (int8_rot) quantizers: the prologue row is rotated by blockdiag(H256) (H256 = normalized 4th
+ * Kronecker power of the 4x4 regular Hadamard) before the per-token int8 quantization. Per 256-group:
+ * bf16(v) in four 64-chunks, z_k = fp32(exact X_k H64^T), the fixed-order fp32 H4/2 combine of the
+ * chunks, s = max(amax/127, 1e-12), q = rint(clamp(y * (1/s))). K % 256 == 0, K <= 16384.
+ * ------------------------------------------------------------------------------------------- */
+
+/* replaces triton_fp8.rot_quant_rows_i8 (triton_fp8.py:424-427), KIND 0 of _rot_quant_wide_kernel */
+int rh3_rot_quant_rows_i8(const uint16_t* x, int64_t ldx, int64_t M, int64_t K,
+                          int8_t* q, int64_t ldq, float* s, hipStream_t stream);
+
+/* replaces triton_fp8.swiglu_rot_quant_rows_i8 (triton_fp8.py:437-439): x [M, 2F] = [gate | up] */
+int rh3_swiglu_rot_quant_rows_i8(const uint16_t* x, int64_t ldx, int64_t M, int64_t F,
+                                 int8_t* q, int64_t ldq, float* s, hipStream_t stream);
+
+/* replaces triton_fp8.norm_mod_rot_quant_rows_i8 (triton_fp8.py:442-446): RMSNorm + modulation
+ * prologue as rh3_quant_norm_mod_i8, then the rotation */
+int rh3_norm_mod_rot_quant_i8(const uint16_t* x, int64_t ldx, int64_t M, int64_t K,
+                              const uint16_t* weight, float eps, const int32_t* idx,
+                              const void* shift, const void* scale, int tab_dtype, int64_t ld_tab,
+                              int8_t* q, int64_t ldq, float* s, hipStream_t stream);
+
+/* replaces triton_fp8.rot_quant_heads_i8 (triton_fp8.py:429-434): head-major o [H, M, 128] gathered
+ * per token as in rh3_quant_heads_i8, then rotated */
+int rh3_rot_quant_heads_i8(const uint16_t* o, int64_t H, int64_t M, int64_t ld_head, int64_t ld_row,
+                           int8_t* q, int64_t ldq, float* s, hipStream_t stream);
+
+/* replaces triton_fp8.convrot (triton_fp8.py:86-90): y = x @ blockdiag(H256)^T as the fp32 rounding of
+ * the exact product; x bf16 (RH3_DTYPE_BF16) or fp32 (RH3_DTYPE_F32) rows, y fp32 */
+int rh3_convrot_f32(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t K,
+                    float* y, int64_t ldy, hipStream_t stream);
+
+/* replaces kernels.quantize_weight(w, "int8_rot") (kernels.py:62-72): convrot(w) (exact, rounded to
+ * fp32), then per-row s = max(amax/127, 1e-12), q = round(w_rot / s); w [N, K] bf16 or fp32 */
+int rh3_quant_weight_rot_i8(const void* w, int w_dtype, int64_t ldw, int64_t N, int64_t K,
+                            int8_t* q, int64_t ldq, float* s, hipStream_t stream);
+
+/* ---------------------------------------------------------------------------------------------
  * Row-wise W8A8 GEMMs on int8 MFMA: acc[m,n] = sum_k xq[m,k] * wq[n,k] (int32, exact),
  * y = (fp32(acc) * xs[m]) * ws[n]. xq [M, K] int8 (row stride ldx), wq [N, K] int8 (row stride ldw),
  * xs [M], ws [N] fp32. K % 64 == 0, N % 8 == 0, strides % 16 == 0, 16-byte aligned rows.

@@ -20,7 +20,7 @@ are then added by a butterfly over lane distances 32, 16, 8, 4, 2, 1.
 """
 import numpy as np
 
-from .numerics import F32, bf16_to_f32, f32_to_fp8_e4m3
+from .numerics import F32, bf16_to_f32, f32_to_bf16, f32_to_fp8_e4m3
 
 I8_MAX = F32(127.0)
 FP8_MAX = F32(448.0)
@@ -139,8 +139,96 @@ def regular_hadamard(n):
     return h / np.sqrt(n)
 
 
+# ---------------------------------------------------------------- ConvRot (int8_rot)
+# The regular H4 = J - 2P (P the anti-identity): H4 x = sum(x) - 2 reverse(x). H64 = H4 (x) H4 (x) H4 over
+# the index i = 16a + 4b + c of a 64-chunk, applied as three radix-4 stages (c, then b, then a), each
+# t = ((x0 + x1) + x2) + x3, y_j = t - 2 x_(3-j), in float64. With bf16 / fp32 inputs every product is
+# exact and, for values within 2^38 of each other, so is every stage, which makes the result the exact
+# dot product (pinned against rational arithmetic in tests/test_oracle.py); the stage order is the HIP
+# kernel's (rapid-h3_amd/csrc/rot.hip), so both sides agree even where float64 would round.
+
+def _h4_stage(d, s):
+    """One radix-4 stage over indices (i, i+s, i+2s, i+3s) of the last axis (length 64), float64."""
+    v = d.reshape(d.shape[:-1] + (64 // (4 * s), 4, s))
+    x0, x1, x2, x3 = v[..., 0, :], v[..., 1, :], v[..., 2, :], v[..., 3, :]
+    t = ((x0 + x1) + x2) + x3
+    return np.stack([t - 2.0 * x3, t - 2.0 * x2, t - 2.0 * x1, t - 2.0 * x0], axis=-2).reshape(d.shape)
+
+
+def h64_unnormalized(x):
+    """(8 * H64) @ x over the last axis (length 64) in float64 staged butterflies."""
+    d = np.asarray(x, dtype=np.float64)
+    for s in (1, 4, 16):
+        d = _h4_stage(d, s)
+    return d
+
+
+def rot_rows(v):
+    """The activation rotation of triton_fp8._rot256 / _rot_wide (triton_fp8.py:102-116, :218-233) on the
+    prologue values v [M, K] fp32: per 256-group, X_k = bf16(v) chunks, z_k = fp32(X_k H64^T) (the exact
+    products rounded once), then y0 = ((z0 + z1) + z2 - z3) * 0.5, y1 = ((z0 + z1) - z2 + z3) * 0.5,
+    y2 = ((z0 - z1) + z2 + z3) * 0.5, y3 = ((z1 + z2) + z3 - z0) * 0.5 in fp32. Returns y [M, K] fp32."""
+    v = np.asarray(v, dtype=F32)
+    m, k = v.shape
+    assert k % 256 == 0, "ConvRot needs K % 256 == 0"
+    xb = bf16_to_f32(f32_to_bf16(v)).reshape(m, k // 256, 4, 64)
+    z = (h64_unnormalized(xb) * 0.125).astype(F32)
+    z0, z1, z2, z3 = z[:, :, 0], z[:, :, 1], z[:, :, 2], z[:, :, 3]
+    h = F32(0.5)
+    y = np.stack([(((z0 + z1) + z2) - z3) * h, (((z0 + z1) - z2) + z3) * h,
+                  (((z0 - z1) + z2) + z3) * h, (((z1 + z2) + z3) - z0) * h], axis=2)
+    return y.astype(F32).reshape(m, k)
+
+
+def rot_quantize(v):
+    """Per-row INT8 of rot_rows(v) as the Triton rotation kernels quantize (triton_fp8.py:96-99, :341-351):
+    s = max(amax / 127, 1e-12), q = rint(clamp(y * (1 / s), -127, 127)). -> (q [M, K] int8, s [M, 1])."""
+    y = rot_rows(v)
+    amax = np.abs(y).max(axis=1, keepdims=True)
+    s = np.maximum(amax / I8_MAX, EPS_SCALE).astype(F32)
+    inv = (F32(1.0) / s).astype(F32)
+    q = np.rint(np.clip((y * inv).astype(F32), -127.0, 127.0)).astype(np.int8)
+    return q, s
+
+
+def rot_quant_rows_i8(x):
+    """triton_fp8.rot_quant_rows_i8 (triton_fp8.py:424-427): x [M, K] bf16 bits."""
+    return rot_quantize(_as_f32(x))
+
+
+def norm_mod_rot_quant_rows_i8(x, weight, eps, idx, shift, scale):
+    """triton_fp8.norm_mod_rot_quant_rows_i8 (triton_fp8.py:442-446)."""
+    return rot_quantize(norm_mod(x, weight, eps, idx, shift, scale))
+
+
+def rot_quant_heads_i8(o):
+    """triton_fp8.rot_quant_heads_i8 (triton_fp8.py:429-434): o [H, M, 128] head-major."""
+    return rot_quantize(_as_f32(heads_to_rows(o)))
+
+
+def swiglu_rot_quant_rows_i8(x):
+    """triton_fp8.swiglu_rot_quant_rows_i8 (triton_fp8.py:437-439): x [M, 2F] = [gate | up]."""
+    v = _as_f32(x)
+    f = v.shape[1] // 2
+    return rot_quantize(silu_mul(v[:, :f], v[:, f:]))
+
+
 def convrot(x, group=256):
-    """x @ blockdiag(H_group)^T (triton_fp8.py:86-90), computed in float64 and rounded once to fp32."""
+    """x @ blockdiag(H256)^T (triton_fp8.py:86-90) as the exact product rounded once to fp32: H256 =
+    (H4 (x) H64) / 16, the H64 stages of h64_unnormalized then the chunk stage t = ((d0 + d1) + d2) + d3,
+    y_k = t - 2 d_(3-k), all float64 (the HIP kernel's order)."""
+    assert group == 256
+    v = _as_f32(x)
+    m, k = v.shape
+    d = h64_unnormalized(v.reshape(m, k // 256, 4, 64))
+    d0, d1, d2, d3 = d[:, :, 0], d[:, :, 1], d[:, :, 2], d[:, :, 3]
+    t = ((d0 + d1) + d2) + d3
+    y = np.stack([t - 2.0 * d3, t - 2.0 * d2, t - 2.0 * d1, t - 2.0 * d0], axis=2) * 0.0625
+    return y.astype(F32).reshape(m, k)
+
+
+def convrot_matmul(x, group=256):
+    """The closed form x @ blockdiag(H)^T in float64 (BLAS order), rounded once to fp32 (a checker)."""
     v = _as_f32(x).astype(np.float64)
     m, k = v.shape
     h = regular_hadamard(group)

@@ -24,6 +24,12 @@ SIGNATURES = {
     "rh3_quant_norm_mod_i8": ([_P, _I, _I, _I, _P, _F, _P, _P, _P, _C, _I, _P, _I, _P, _P], _C),
     "rh3_quant_heads_i8": ([_P, _I, _I, _I, _I, _P, _I, _P, _P], _C),
     "rh3_quant_swiglu_i8": ([_P, _I, _I, _I, _P, _I, _P, _P], _C),
+    "rh3_rot_quant_rows_i8": ([_P, _I, _I, _I, _P, _I, _P, _P], _C),
+    "rh3_swiglu_rot_quant_rows_i8": ([_P, _I, _I, _I, _P, _I, _P, _P], _C),
+    "rh3_norm_mod_rot_quant_i8": ([_P, _I, _I, _I, _P, _F, _P, _P, _P, _C, _I, _P, _I, _P, _P], _C),
+    "rh3_rot_quant_heads_i8": ([_P, _I, _I, _I, _I, _P, _I, _P, _P], _C),
+    "rh3_convrot_f32": ([_P, _C, _I, _I, _I, _P, _I, _P], _C),
+    "rh3_quant_weight_rot_i8": ([_P, _C, _I, _I, _I, _P, _I, _P, _P], _C),
     "rh3_gemm_i8": ([_P, _I, _P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _P], _C),
     "rh3_gemm_i8_swiglu": ([_P, _I, _P, _P, _I, _P, _P, _I, _I, _I, _I, _P], _C),
     "rh3_gemm_i8_gated": ([_P, _I, _P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _P], _C),

@@ -8,7 +8,9 @@ Differences from the reference, all on purpose:
     PyTorch semantics for int8 (exact int32 accumulators, the same (acc * xs) * ws rounding);
   * there is no silent fallback: if librh3 is missing, calls raise (the reference prints and drops to
     torch, kernels.py:88-98);
-  * int8_rot (ConvRot) and the nvfp4 verification modes are not built for gfx950 yet and raise.
+  * int8_rot weights are rotated exactly (float64 butterflies, rounded once to fp32) instead of by a
+    torch fp32 matmul of unspecified order;
+  * the nvfp4 verification modes are not built for gfx950 and raise.
 """
 from dataclasses import dataclass
 
@@ -40,8 +42,11 @@ def quantize_weight(w, mode):
     """kernels.quantize_weight (kernels.py:52-72) for bf16 weights [N, K]."""
     if mode == "int8_fast":
         mode = "int8_rowwise"
-    if mode in ("int8_rot", "nvfp4_fake", "nvfp4_rot_fake"):
-        raise NotImplementedError(f"quantize_weight: mode {mode} is not built for gfx950 yet")
+    if mode in ("nvfp4_fake", "nvfp4_rot_fake"):
+        raise NotImplementedError(f"quantize_weight: mode {mode} is not built for gfx950")
+    if mode == "int8_rot":
+        q, s = _quant.quantize_weight_rot(w)
+        return QWeight(q, s.t().contiguous())
     if w.dtype != torch.bfloat16:
         raise TypeError("quantize_weight: bf16 weights only (the checkpoint dtype of the DiT linears)")
     if mode == "fp8_tensor":
@@ -52,6 +57,14 @@ def quantize_weight(w, mode):
     if mode == "int8_rowwise":
         return _row_quant(w, fp8=False)
     raise ValueError(mode)
+
+
+def adopt_convrot(qdata, scale, group=256, transposed=False):
+    """QWeight of an already-quantized Comfy int8_convrot weight (H256, per-row scale), taken as is, the
+    check of __init__.py:107-114: int8 [N, K] codes, group 256, not transposed; scale -> [1, N] fp32."""
+    if group != _tq.ROT_GROUP or transposed or qdata.dtype != torch.int8 or qdata.ndim != 2:
+        raise ValueError("adopt_convrot: needs int8 [N, K] codes rotated with group 256, not transposed")
+    return QWeight(qdata.contiguous(), scale.float().reshape(1, -1).contiguous())
 
 
 def quantize_rows(x, mode):
@@ -70,11 +83,14 @@ def gemm_config(k, n):
 
 def linear(x, qw, mode):
     """y = x @ W^T for x [M, K] bf16 and a QWeight of W [N, K]; returns x.dtype (kernels.py:107-137)."""
-    if mode in ("int8_rot", "nvfp4_fake", "nvfp4_rot_fake"):
-        raise NotImplementedError(f"linear: mode {mode} is not built for gfx950 yet")
+    if mode in ("nvfp4_fake", "nvfp4_rot_fake"):
+        raise NotImplementedError(f"linear: mode {mode} is not built for gfx950")
     if x.dtype != torch.bfloat16:
         raise TypeError("linear: bf16 activations only")
     x = x.contiguous()
+    if mode == "int8_rot":
+        xq, xs = _quant.rot_quant_rows_i8(x)
+        return _gemm.int8_gemm(xq, xs, qw.q, qw.scale, config=gemm_config(x.shape[1], qw.q.shape[0]))
     if mode in ("int8_rowwise", "int8_fast"):
         xq, xs = _quant.quant_rows_i8(x)
         return _gemm.int8_gemm(xq, xs, qw.q, qw.scale, config=gemm_config(x.shape[1], qw.q.shape[0]))

@@ -96,3 +96,113 @@ def swiglu_quant_rows_i8(x):
     nat.call("rh3_quant_swiglu_i8", nat.ptr(x), x.stride(0), m, f, nat.ptr(q), q.stride(0), nat.ptr(s),
              nat.stream(x.device))
     return q, s
+
+
+# ---------------------------------------------------------------- ConvRot (int8_rot) quantizers
+# Same prologues as above, then x @ blockdiag(H256)^T before the per-row INT8 (librh3 rh3_*rot*):
+# per 256-group bf16(v) in four 64-chunks, z_k = fp32(exact X_k H64^T), the reference's fp32 H4/2
+# combine of the chunks, s = max(amax / 127, 1e-12), q = rint(clamp(y * (1 / s))) (triton_fp8.py:102-116,
+# :277-351). K must be a multiple of 256 and at most 16384.
+
+def _check_rot_width(k, name):
+    if k % 256 != 0:
+        raise AssertionError(f"{name}: K={k} must be a multiple of the rotation group 256")
+
+
+def rot_quant_rows_i8(x):
+    """INT8 of x [M, K] bf16 @ blockdiag(H256)^T (triton_fp8.rot_quant_rows_i8)."""
+    _check_rows(x, "rot_quant_rows_i8")
+    m, k = x.shape
+    _check_rot_width(k, "rot_quant_rows_i8")
+    q, s = _out(x, m, k)
+    nat.call("rh3_rot_quant_rows_i8", nat.ptr(x), x.stride(0), m, k, nat.ptr(q), q.stride(0), nat.ptr(s),
+             nat.stream(x.device))
+    return q, s
+
+
+def swiglu_rot_quant_rows_i8(x):
+    """x [M, 2F] (gate | up) -> INT8 of rot(silu(gate) * up) (triton_fp8.swiglu_rot_quant_rows_i8)."""
+    _check_rows(x, "swiglu_rot_quant_rows_i8")
+    m, k2 = x.shape
+    f = k2 // 2
+    _check_rot_width(f, "swiglu_rot_quant_rows_i8")
+    q, s = _out(x, m, f)
+    nat.call("rh3_swiglu_rot_quant_rows_i8", nat.ptr(x), x.stride(0), m, f, nat.ptr(q), q.stride(0), nat.ptr(s),
+             nat.stream(x.device))
+    return q, s
+
+
+def norm_mod_rot_quant_rows_i8(x, weight, eps, idx, shift, scale):
+    """INT8 of rot(rms_norm(x) * w * (1 + scale[idx]) + shift[idx]) (triton_fp8.norm_mod_rot_quant_rows_i8);
+    arguments as norm_mod_quant_rows_i8."""
+    _check_rows(x, "norm_mod_rot_quant_rows_i8")
+    m, k = x.shape
+    _check_rot_width(k, "norm_mod_rot_quant_rows_i8")
+    if shift.stride(1) != 1 or scale.stride(1) != 1 or shift.stride(0) != scale.stride(0):
+        raise AssertionError("norm_mod_rot_quant_rows_i8: shift/scale need unit column stride and a shared row stride")
+    if shift.dtype != scale.dtype or shift.dtype not in (torch.float32, torch.bfloat16):
+        raise TypeError("norm_mod_rot_quant_rows_i8: shift/scale must both be fp32 or both bf16")
+    if idx.dtype != torch.int32 or idx.numel() != m:
+        raise TypeError("norm_mod_rot_quant_rows_i8: idx must be int32 [M]")
+    if weight is not None:
+        weight = weight.to(torch.bfloat16).contiguous()
+        if weight.numel() != k:
+            raise ValueError("norm_mod_rot_quant_rows_i8: weight must have K elements")
+    idx = idx.contiguous()
+    q, s = _out(x, m, k)
+    dt = nat.RH3_DTYPE_F32 if shift.dtype == torch.float32 else nat.RH3_DTYPE_BF16
+    nat.call("rh3_norm_mod_rot_quant_i8", nat.ptr(x), x.stride(0), m, k, nat.ptr(weight), float(eps), nat.ptr(idx),
+             nat.ptr(shift), nat.ptr(scale), dt, shift.stride(0), nat.ptr(q), q.stride(0), nat.ptr(s),
+             nat.stream(x.device))
+    return q, s
+
+
+def rot_quant_heads_i8(o):
+    """INT8 of rot(o.transpose(0, 1).reshape(M, H * 128)) for a head-major o [H, M, 128]
+    (triton_fp8.rot_quant_heads_i8)."""
+    h, m, d = o.shape
+    if d != 128 or o.stride(2) != 1:
+        raise AssertionError("rot_quant_heads_i8: o must be [H, M, 128] with contiguous last dim")
+    if o.dtype != torch.bfloat16 or not o.is_cuda:
+        raise TypeError("rot_quant_heads_i8: o must be bf16 on a GPU")
+    _check_rot_width(h * d, "rot_quant_heads_i8")
+    q, s = _out(o, m, h * d)
+    nat.call("rh3_rot_quant_heads_i8", nat.ptr(o), h, m, o.stride(0), o.stride(1), nat.ptr(q), q.stride(0),
+             nat.ptr(s), nat.stream(o.device))
+    return q, s
+
+
+def _dtype_code(t, name):
+    if t.dtype == torch.bfloat16:
+        return nat.RH3_DTYPE_BF16
+    if t.dtype == torch.float32:
+        return nat.RH3_DTYPE_F32
+    raise TypeError(f"{name}: bf16 or fp32 input, got {t.dtype}")
+
+
+def convrot_f32(x):
+    """x [M, K] (bf16 or fp32, GPU) @ blockdiag(H256)^T as fp32, the exact product rounded once."""
+    if x.ndim != 2 or x.stride(1) != 1 or not x.is_cuda:
+        raise AssertionError("convrot: x must be a 2-D GPU tensor with a contiguous last dim (no CPU path)")
+    m, k = x.shape
+    _check_rot_width(k, "convrot")
+    dt = _dtype_code(x, "convrot")
+    if x.data_ptr() % 16 or x.stride(0) % 8:
+        x = x.contiguous()
+    y = torch.empty((m, k), device=x.device, dtype=torch.float32)
+    nat.call("rh3_convrot_f32", nat.ptr(x), dt, x.stride(0), m, k, nat.ptr(y), y.stride(0), nat.stream(x.device))
+    return y
+
+
+def quantize_weight_rot(w):
+    """kernels.quantize_weight(w, "int8_rot"): per-row INT8 of convrot(w) -> (q [N, K] int8, s [N, 1] fp32)."""
+    if w.ndim != 2 or not w.is_cuda:
+        raise AssertionError("quantize_weight_rot: w must be a 2-D GPU tensor")
+    w = w.contiguous()
+    n, k = w.shape
+    _check_rot_width(k, "quantize_weight_rot")
+    dt = _dtype_code(w, "quantize_weight_rot")
+    q, s = _out(w, n, k)
+    nat.call("rh3_quant_weight_rot_i8", nat.ptr(w), dt, w.stride(0), n, k, nat.ptr(q), q.stride(0), nat.ptr(s),
+             nat.stream(w.device))
+    return q, s

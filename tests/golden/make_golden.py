@@ -1,6 +1,6 @@
 """Write the golden fixtures in tests/golden/*.npz: seeded small inputs and the oracle's outputs.
 
-    python tests/golden/make_golden.py
+    python tests/golden/make_golden.py [rot]       # all files, or only rot.npz
 
 Inputs come from numpy's PCG64 (seeded), so they are the same on every machine; expected outputs
 come from the CPU oracle (oracle/), which tests/test_oracle.py pins independently against torch's
@@ -117,17 +117,64 @@ def attn_case(rng):
                         ck8=ck8, cks=cks, ckmean=ckm, cout=cout)
 
 
-def main():
-    rng = np.random.default_rng(0)
-    quant_case(rng)
-    norm_mod_case(rng)
-    heads_case(rng)
-    gemm_case(rng)
-    attn_case(rng)
+def rot_case(rng):
+    """ConvRot (int8_rot) quantizers: K = 3072 (one pass of 64-column chunks), 5376 and 14336 (the H3
+    widths, two and four passes), all four prologues, the weight quantizer and convrot."""
+    x = outlier_acts(rng, 37, 3072)
+    x[2] = 0.0                                    # all-zero row -> s = 1e-12, q = 0
+    x[4] = 0.0
+    x[4, 300] = 1.0                               # one-hot: y = column 300 of blockdiag(H256), |y| = 1/16
+    xb = bf16(x)
+    q, s = oq.rot_quant_rows_i8(xb)
+    x2 = bf16(outlier_acts(rng, 7, 5376))
+    q2, s2 = oq.rot_quant_rows_i8(x2)
+    x3 = bf16(outlier_acts(rng, 3, 14336))
+    q3, s3 = oq.rot_quant_rows_i8(x3)
+    m, k, r = 23, 3072, 3
+    xn = bf16(outlier_acts(rng, m, k) * 3.0 + 0.5)
+    w = bf16(1.0 + 0.3 * rng.standard_normal(k))
+    idx = rng.integers(0, r, size=m).astype(np.int32)
+    shift = (0.1 * rng.standard_normal((r, k))).astype(np.float32)
+    scale = (0.2 * rng.standard_normal((r, k))).astype(np.float32)
+    qn, sn = oq.norm_mod_rot_quant_rows_i8(xn, w, 1e-6, idx, shift, scale)
+    shb, scb = bf16(shift), bf16(scale)
+    qnb, snb = oq.norm_mod_rot_quant_rows_i8(xn, w, 1e-6, idx, shb, scb)
+    o = bf16(rng.standard_normal((24, 19, 128)) * np.exp(0.5 * rng.standard_normal((24, 1, 128))))
+    qh, sh = oq.rot_quant_heads_i8(o)
+    g = bf16(2.0 * rng.standard_normal((17, 2 * 1536)))
+    qg, sg = oq.swiglu_rot_quant_rows_i8(g)
+    wt = bf16(0.02 * rng.standard_normal((40, 768)))
+    wt[3] = 0.0
+    wq, ws = oq.quantize_weight(wt, "int8_rot")
+    wf = (0.02 * rng.standard_normal((12, 1280))).astype(np.float32)
+    wfq, wfs = oq.quantize_weight(wf, "int8_rot")
+    cx = bf16(rng.standard_normal((6, 1024)))
+    cy = oq.convrot(cx)
+    np.savez_compressed(os.path.join(HERE, "rot.npz"), x=xb, q=q, s=s, x2=x2, q2=q2, s2=s2, x3=x3, q3=q3, s3=s3,
+                        xn=xn, w=w, idx=idx, shift=shift, scale=scale, qn=qn, sn=sn, shift_bf=shb, scale_bf=scb,
+                        qnb=qnb, snb=snb, eps=np.float32(1e-6), o=o, qh=qh, sh=sh, g=g, qg=qg, sg=sg,
+                        wt=wt, wq=wq, ws=ws, wf=wf, wfq=wfq, wfs=wfs, cx=cx, cy=cy)
+
+
+CASES = ("quant", "norm_mod", "heads", "gemm", "attn", "rot")
+
+
+def main(which=CASES):
+    """Each group draws from its own fixed stream: the first five share seed 0 in this order, rot uses
+    seed 1, so regenerating one file leaves the others' inputs unchanged."""
+    if set(which) & set(CASES[:5]):
+        rng = np.random.default_rng(0)
+        quant_case(rng)
+        norm_mod_case(rng)
+        heads_case(rng)
+        gemm_case(rng)
+        attn_case(rng)
+    if "rot" in which:
+        rot_case(np.random.default_rng(1))
     for f in sorted(os.listdir(HERE)):
         if f.endswith(".npz"):
             print(f, os.path.getsize(os.path.join(HERE, f)))
 
 
 if __name__ == "__main__":
-    main()
+    main(sys.argv[1:] or CASES)

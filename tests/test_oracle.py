@@ -199,6 +199,96 @@ def test_convrot_orthonormal():
                        rtol=1e-5)
 
 
+def _bf16_wide(rng, shape, lo=-20, hi=20):
+    """bf16-representable values with exponents spread over 2^lo .. 2^hi (random signs)."""
+    m = rng.integers(128, 256, size=shape).astype(np.float64) / 128.0
+    e = rng.integers(lo, hi, size=shape)
+    sg = rng.choice([-1.0, 1.0], size=shape)
+    return (sg * m * np.exp2(e)).astype(np.float32)
+
+
+def test_h64_is_the_exact_dot_product():
+    """The staged float64 H64 equals the exact rational dot products with H64 (brute force in
+    fractions.Fraction), for bf16 inputs spread over 2^40 of magnitude."""
+    from fractions import Fraction
+    rng = np.random.default_rng(11)
+    x = _bf16_wide(rng, (6, 64))
+    h = np.rint(oq.regular_hadamard(64) * 8).astype(np.int64)          # +-1 entries
+    got = oq.h64_unnormalized(x)
+    for r in range(x.shape[0]):
+        xf = [Fraction(float(v)) for v in x[r]]
+        for j in range(64):
+            exact = sum((int(h[j, i]) * xf[i] for i in range(64)), Fraction(0))
+            assert Fraction(float(got[r, j])) == exact
+
+
+def test_rot_rows_bruteforce_and_closed_form():
+    """rot_rows against (a) a scalar restatement of triton_fp8._rot256 from its parts -- bf16 rounding,
+    z_k = fp32(exact dot with H64/8), the fp32 combine in the order of triton_fp8.py:109-113 -- built from
+    Fraction sums and np.float32 scalar arithmetic, and (b) the float64 closed form bf16(v) @ blockdiag(H256)^T
+    within fp32 rounding."""
+    from fractions import Fraction
+    rng = np.random.default_rng(12)
+    v = (rng.standard_normal((3, 512)) * np.exp(rng.standard_normal((1, 512)))).astype(np.float32)
+    y = oq.rot_rows(v)
+    xb = bf16_to_f32(f32_to_bf16(v))
+    h = np.rint(oq.regular_hadamard(64) * 8).astype(np.int64)
+    f = np.float32
+    for r in range(3):
+        for g in range(2):
+            z = np.zeros((4, 64), np.float32)
+            for k in range(4):
+                xs = [Fraction(float(t)) for t in xb[r, 256 * g + 64 * k: 256 * g + 64 * (k + 1)]]
+                for j in range(64):
+                    z[k, j] = f(float(sum((int(h[j, i]) * xs[i] for i in range(64)), Fraction(0)) / 8))
+            for j in range(64):
+                z0, z1, z2, z3 = (f(z[k, j]) for k in range(4))
+                ref = [(((z0 + z1) + z2) - z3) * f(0.5), (((z0 + z1) - z2) + z3) * f(0.5),
+                       (((z0 - z1) + z2) + z3) * f(0.5), (((z1 + z2) + z3) - z0) * f(0.5)]
+                for k in range(4):
+                    assert y[r, 256 * g + 64 * k + j] == ref[k]
+    exact = xb.astype(np.float64).reshape(-1, 256) @ oq.regular_hadamard(256).T
+    err = np.abs(y.reshape(-1, 256) - exact)
+    assert (err <= 4 * 2.0 ** -24 * np.abs(exact).max(axis=1, keepdims=True)).all()
+
+
+def test_rot_quant_known_answers():
+    """Zero row -> s = 1e-12, q = 0; one-hot e_j -> y = column j of blockdiag(H256), all |y| = 1/16, codes
+    +-127 with the column's signs; codes use the Triton form rint(clamp(y * (1/s))) (triton_fp8.py:96-99)."""
+    x = np.zeros((2, 512), np.float32)
+    x[1, 256 + 77] = 3.0
+    q, s = oq.rot_quantize(x)
+    assert s[0, 0] == np.float32(1e-12) and not q[0].any()
+    col = np.sign(oq.regular_hadamard(256)[:, 77])
+    assert np.array_equal(q[1, 256:], (127 * col).astype(np.int8)) and not q[1, :256].any()
+    assert s[1, 0] == np.float32(np.float32(3.0 / 16) / np.float32(127))
+    # invariants on random rows: |q| <= 127, the row max code is 127, s * 127 == amax(|y|) to fp32
+    rng = np.random.default_rng(13)
+    v = (rng.standard_normal((5, 1024)) * 4).astype(np.float32)
+    q, s = oq.rot_quantize(v)
+    y = oq.rot_rows(v)
+    assert (np.abs(q.astype(np.int32)).max(axis=1) == 127).all()
+    assert np.array_equal(s[:, 0], np.maximum(np.abs(y).max(axis=1) / np.float32(127), np.float32(1e-12)))
+    assert (np.abs(y - q * s) <= s * 0.5000001).all()
+
+
+def test_convrot_exact_and_weight_rot():
+    """convrot (staged, exact, rounded once) equals the float64 matmul closed form for bf16 and fp32 inputs,
+    and quantize_weight(int8_rot) is quantize_rows of it with the IEEE quotient (kernels.py:62-71)."""
+    rng = np.random.default_rng(14)
+    wb = f32_to_bf16(_bf16_wide(rng, (7, 768), -12, 4))
+    assert np.array_equal(oq.convrot(wb), oq.convrot_matmul(wb))
+    wf = (0.02 * rng.standard_normal((5, 512))).astype(np.float32)
+    assert np.array_equal(oq.convrot(wf), oq.convrot_matmul(wf))
+    q, s = oq.quantize_weight(wb, "int8_rot")
+    q2, s2 = oq.quantize_rows(oq.convrot_matmul(wb), "int8_rowwise")
+    assert np.array_equal(q, q2) and np.array_equal(s, s2.T)
+    t = torch.from_numpy(oq.convrot(wb))
+    st = (t.abs().amax(dim=1, keepdim=True) / 127.0).clamp_min(1e-12)
+    qt = (t / st).round().clamp(-127, 127).to(torch.int8)             # kernels.py:69-71 in torch
+    assert np.array_equal(q, qt.numpy())
+
+
 # ----------------------------------------------------------------------------- GEMM
 def test_int8_acc_matches_int_mm_and_bruteforce():
     rng = np.random.default_rng(8)
@@ -355,3 +445,9 @@ def test_golden_fixtures_regenerate(golden):
     h = golden("heads_swiglu")
     q, s = oq.heads_quant_rows_i8(h["o"])
     assert np.array_equal(q, h["q"]) and np.array_equal(s, h["s"])
+    r = golden("rot")
+    q, s = oq.rot_quant_rows_i8(r["x"])
+    assert np.array_equal(q, r["q"]) and np.array_equal(s, r["s"])
+    q, s = oq.norm_mod_rot_quant_rows_i8(r["xn"], r["w"], float(r["eps"]), r["idx"], r["shift"], r["scale"])
+    assert np.array_equal(q, r["qn"]) and np.array_equal(s, r["sn"])
+    assert np.array_equal(oq.convrot(r["cx"]), r["cy"])
