@@ -1,16 +1,18 @@
 """The fused INT8 DiT block chain on the HIP kernels: the call sequence of the reference's
-_fused_block (/root/reference/custom_nodes/rapid_h3/__init__.py:207-321) for the int8_rowwise recipe,
-plus _row_index (:189-200) and the per-segment gated residual (:242-251).
+_fused_block (/root/reference/custom_nodes/rapid_h3/__init__.py:207-321), plus _row_index (:189-200)
+and the per-segment gated residual (:242-251). Two recipes: int8_rot (the reference's, every quantizer
+with the ConvRot H256 rotation and weights quantized with quantize_weight(w, "int8_rot")) and
+int8_rowwise (the same chain without rotation, the configuration the benchmark names).
 
     x [S, hidden] bf16 residual stream (updated in place and returned)
-    RMSNorm + modulation -> INT8 (one pass)        rh3_quant_norm_mod_i8
+    RMSNorm + modulation -> INT8 (one pass)        rh3_quant_norm_mod_i8      / rh3_norm_mod_rot_quant_i8
     QKV GEMM                                       rh3_gemm_i8
-    q/k RMSNorm + RoPE + INT8 attention            rh3_int8_attention_rr (head-major output)
-    head-major gather -> INT8                      rh3_quant_heads_i8
+    q/k RMSNorm + RoPE + INT8 attention            rh3_attention_prepass + rh3_attention_forward (head-major out)
+    head-major gather -> INT8                      rh3_quant_heads_i8         / rh3_rot_quant_heads_i8
     out-proj GEMM + gated residual, per segment    rh3_gemm_i8_gated
-    RMSNorm + modulation -> INT8                   rh3_quant_norm_mod_i8
+    RMSNorm + modulation -> INT8                   rh3_quant_norm_mod_i8      / rh3_norm_mod_rot_quant_i8
     FFN-up GEMM + SwiGLU epilogue                  rh3_gemm_i8_swiglu
-    INT8 of h                                      rh3_quant_rows_i8
+    INT8 of h                                      rh3_quant_rows_i8          / rh3_rot_quant_rows_i8
     FFN-down GEMM + gated residual, per segment    rh3_gemm_i8_gated
 
 ComfyUI objects (the block module, adaln_proj, model management) are outside this build: the caller
@@ -44,6 +46,7 @@ class BlockWeights:
     heads: int
     eps: float = 1e-6
     qk_eps: float = 1e-6
+    recipe: str = "int8_rowwise"      # or "int8_rot": the weights above must be quantized the same way
 
 
 def row_index(segments, s, device):
@@ -69,20 +72,33 @@ PHASES = ("quant_norm1", "gemm_qkv", "attn_prepass", "attn_main", "quant_heads",
           "gemm_up_swiglu", "quant_h", "gemm_down_gated")
 
 
-def fused_block(x, w: BlockWeights, mod, segments, rope_tab, idx=None, mark=None):
+_QUANTIZERS = {
+    "int8_rowwise": (_quant.norm_mod_quant_rows_i8, _quant.heads_quant_rows_i8, _quant.quant_rows_i8),
+    "int8_rot": (_quant.norm_mod_rot_quant_rows_i8, _quant.rot_quant_heads_i8, _quant.rot_quant_rows_i8),
+}
+
+
+def fused_block(x, w: BlockWeights, mod, segments, rope_tab, idx=None, mark=None, trace=None):
     """One DiT block forward on x [S, hidden] bf16 (modified in place). mod = (shift_msa, scale_msa,
     gate_msa, shift_mlp, scale_mlp, gate_mlp), each [R, hidden]; rope_tab [1, S, 1, rot/2, 2, 2] bf16.
     mark: optional callable, called with each name of PHASES after that phase is enqueued (a timer
-    records a stream event there); the kernels and their order are the same with or without it."""
+    records a stream event there); the kernels and their order are the same with or without it.
+    trace: optional dict that receives every intermediate (a checker's view of each stage)."""
     shift_msa, scale_msa, gate_msa, shift_mlp, scale_mlp, gate_mlp = mod
     tick = mark or (lambda name: None)
+    keep = trace.__setitem__ if trace is not None else (lambda k, v: None)
+    if w.recipe not in _QUANTIZERS:
+        raise ValueError(f"fused_block: recipe {w.recipe!r} (int8_rowwise or int8_rot)")
+    norm_mod_q, heads_q, rows_q = _QUANTIZERS[w.recipe]
     s = x.shape[0]
     h = w.heads
     if idx is None:
         idx = row_index(segments, s, x.device)
-    xq, xs = _quant.norm_mod_quant_rows_i8(x, w.norm1_w, w.eps, idx, shift_msa, scale_msa)
+    xq, xs = norm_mod_q(x, w.norm1_w, w.eps, idx, shift_msa, scale_msa)
+    keep("xq1", xq), keep("xs1", xs)
     tick("quant_norm1")
     qkv = _gemm.int8_gemm(xq, xs, w.qkv.q, w.qkv.scale)
+    keep("qkv", qkv)
     tick("gemm_qkv")
     q, k, v = (t.view(s, h, D) for t in qkv.split(h * D, dim=-1))
     o = torch.empty(1, h, s, D, dtype=x.dtype, device=x.device)
@@ -90,18 +106,25 @@ def fused_block(x, w: BlockWeights, mod, segments, rope_tab, idx=None, mark=None
     pp = _attn.prepass(q, k, v, rope_tab, w.q_norm_w, w.k_norm_w, w.qk_eps)
     tick("attn_prepass")
     _attn.forward(pp, s, out=o[0].transpose(0, 1))
+    keep("o", o)
     tick("attn_main")
     del qkv, pp
-    oq, os_ = _quant.heads_quant_rows_i8(o[0])
+    oq, os_ = heads_q(o[0])
+    keep("oq", oq), keep("os", os_)
     tick("quant_heads")
     del o
     x = gemm_gated(oq, os_, w.out, x, gate_msa, segments)
+    if trace is not None:
+        keep("x_attn", x.clone())
     tick("gemm_out_gated")
-    xq, xs = _quant.norm_mod_quant_rows_i8(x, w.norm2_w, w.eps, idx, shift_mlp, scale_mlp)
+    xq, xs = norm_mod_q(x, w.norm2_w, w.eps, idx, shift_mlp, scale_mlp)
+    keep("xq2", xq), keep("xs2", xs)
     tick("quant_norm2")
     hh = _gemm.int8_gemm_swiglu(xq, xs, w.fc1_perm.q, w.fc1_perm.scale)
+    keep("h", hh)
     tick("gemm_up_swiglu")
-    hq, hs = _quant.quant_rows_i8(hh)
+    hq, hs = rows_q(hh)
+    keep("hq", hq), keep("hs", hs)
     tick("quant_h")
     del hh
     x = gemm_gated(hq, hs, w.fc2, x, gate_mlp, segments)
