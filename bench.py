@@ -9,7 +9,7 @@ value = algorithmic int8-MFMA work of the block (4 GEMMs 2*M*N*K + attention 4*S
 TOPS, inputs and weights resident in HBM before the timed region. Synthetic data: activations N(0,1)
 with 1 % of channels x20, weights N(0, 0.02) random init, modulation and norm weights random.
 
-    python bench.py [--gpus 1] [--steps 3] [--warmup 1] [--tokens 145152] [--no-cpu]
+    python bench.py [--gpus 1] [--steps 3] [--warmup 1] [--tokens 145152] [--no-cpu] [--recipe int8_rot]
 """
 import argparse
 import json
@@ -55,7 +55,7 @@ def quant_bytes(m):
     return {n: m * k * 2 + m * k + 4 * m for n, k in k_in.items()}
 
 
-def setup(m, device):
+def setup(m, device, recipe="int8_rowwise"):
     import torch
     from rapid_h3 import gemm, kernels
     from rapid_h3.block import BlockWeights
@@ -70,7 +70,7 @@ def setup(m, device):
     qw = {}
     for name, n, k in (("qkv", 3 * HIDDEN, HIDDEN), ("out", HIDDEN, HIDDEN), ("fc1", 2 * FFN, HIDDEN),
                        ("fc2", HIDDEN, FFN)):
-        qw[name] = kernels.quantize_weight(randn(n, k, std=0.02).to(torch.bfloat16), "int8_rowwise")
+        qw[name] = kernels.quantize_weight(randn(n, k, std=0.02).to(torch.bfloat16), recipe)
     perm = gemm.swiglu_perm(2 * FFN, device)
     fc1 = kernels.QWeight(qw["fc1"].q[perm].contiguous(), qw["fc1"].scale[:, perm].contiguous())
 
@@ -78,7 +78,7 @@ def setup(m, device):
         return (1 + 0.3 * randn(n)).to(torch.bfloat16)
 
     w = BlockWeights(qkv=qw["qkv"], out=qw["out"], fc1_perm=fc1, fc2=qw["fc2"], norm1_w=nw(HIDDEN),
-                     norm2_w=nw(HIDDEN), q_norm_w=nw(D), k_norm_w=nw(D), heads=HEADS)
+                     norm2_w=nw(HIDDEN), q_norm_w=nw(D), k_norm_w=nw(D), heads=HEADS, recipe=recipe)
     mod = tuple(randn(1, HIDDEN, std=0.1) for _ in range(6))
     segments = [(0, m, 0)]
     tab = rope_table(m, device)
@@ -167,6 +167,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--tokens", type=int, default=GRID[0] * GRID[1] * GRID[2])
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--recipe", default="int8_rowwise", choices=("int8_rowwise", "int8_rot"),
+                    help="int8_rowwise (the configuration the metric names) or the reference's int8_rot")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="run only the attention kernel + a 1 GiB copy (workload of the --pmc passes)")
     a = ap.parse_args()
@@ -181,7 +183,7 @@ def main():
     from rapid_h3.block import PHASES, fused_block
     dev = torch.device("cuda:0")
     m = a.tokens
-    x, w, mod, segments, tab = setup(m, dev)
+    x, w, mod, segments, tab = setup(m, dev, a.recipe)
 
     for _ in range(a.warmup):
         fused_block(x, w, mod, segments, tab)
@@ -243,7 +245,7 @@ def main():
         "vs_baseline": None, "dtype": "int8", "data": "synthetic",
         "config": {"workload": "full-size DiT block: fused quantizers + 4 W8A8 GEMMs (C2) + INT8 attention (C4)",
                    "tokens": m, "hidden": HIDDEN, "heads": HEADS, "head_dim": D, "ffn": FFN,
-                   "recipe": "int8_rowwise, per-128-block Q/K, K smoothing, bf16 P.V", "parallelism": "none"},
+                   "recipe": f"{a.recipe}, per-128-block Q/K, K smoothing, bf16 P.V", "parallelism": "none"},
         "ms_per_block": round(ms_step, 3),
         "gemm_tops": round(sum(gemms.values()) / (gemm_ms * 1e-3) / 1e12, 1),
         "gemm_frac_int8_peak": round(sum(gemms.values()) / (gemm_ms * 1e-3) / 1e12 / PEAK_INT8_TOPS, 4),

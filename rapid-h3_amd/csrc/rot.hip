@@ -49,6 +49,12 @@ template <> __device__ __forceinline__ float tab_at<uint16_t>(const void* p, int
   return bf2f(static_cast<const uint16_t*>(p)[i]);
 }
 
+typedef __bf16 v2bf_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pk_bf16_hw(float a, float b) {
+  const v2bf_t v = {static_cast<__bf16>(a), static_cast<__bf16>(b)};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
 __device__ __forceinline__ float silu_mul_f(float g, float u) {
   const float sig = 1.0f / (1.0f + __expf(-g));
   return (g * sig) * u;
@@ -63,10 +69,11 @@ __device__ __forceinline__ void h4_stage(double (&d)[64]) {
     const int i = (g / S) * 4 * S + (g % S);
     const double x0 = d[i], x1 = d[i + S], x2 = d[i + 2 * S], x3 = d[i + 3 * S];
     const double t = ((x0 + x1) + x2) + x3;
-    d[i] = t - 2.0 * x3;
-    d[i + S] = t - 2.0 * x2;
-    d[i + 2 * S] = t - 2.0 * x1;
-    d[i + 3 * S] = t - 2.0 * x0;
+    // fma(-2, x, t) rounds t - 2x once, like the subtraction (2x is exact)
+    d[i] = fma(-2.0, x3, t);
+    d[i + S] = fma(-2.0, x2, t);
+    d[i + 2 * S] = fma(-2.0, x1, t);
+    d[i + 3 * S] = fma(-2.0, x0, t);
   }
 }
 
@@ -76,21 +83,37 @@ __device__ __forceinline__ void h64(double (&d)[64]) {
   h4_stage<16>(d);
 }
 
-// lane q of every quad receives lane CTRL[2q+1:2q] of the quad (DPP quad_perm)
+// lane q of every quad receives lane CTRL[2q+1:2q] of the quad (DPP quad_perm; every source lane is inside
+// the quad, so bound_ctrl never applies)
 template <int CTRL>
 __device__ __forceinline__ float quad_f(float v) {
-  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, true));
 }
 template <int CTRL>
 __device__ __forceinline__ double quad_d(double v) {
   const uint64_t u = __double_as_longlong(v);
-  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(u & 0xffffffffu), CTRL, 0xf, 0xf, false));
-  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(u >> 32), CTRL, 0xf, 0xf, false));
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(u & 0xffffffffu), CTRL, 0xf, 0xf, true));
+  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(u >> 32), CTRL, 0xf, 0xf, true));
   return __longlong_as_double(static_cast<long long>((static_cast<uint64_t>(hi) << 32) | lo));
 }
 
+// 8 consecutive modulation-table values at element i (VEC: 16-byte loads, the caller checked alignment)
+template <typename TabT, bool VEC>
+__device__ __forceinline__ void tab8(const void* p, int64_t i, float* t) {
+  if (VEC && sizeof(TabT) == 4) {
+    const float4* q = reinterpret_cast<const float4*>(static_cast<const float*>(p) + i);
+    const float4 u0 = q[0], u1 = q[1];
+    t[0] = u0.x; t[1] = u0.y; t[2] = u0.z; t[3] = u0.w; t[4] = u1.x; t[5] = u1.y; t[6] = u1.z; t[7] = u1.w;
+  } else if (VEC) {
+    unpack8(*reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p) + i), t);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) t[e] = tab_at<TabT>(p, i + e);
+  }
+}
+
 // prologue values of the 8 columns c..c+7 of row m
-template <int KIND, typename TabT>
+template <int KIND, typename TabT, bool VEC>
 __device__ __forceinline__ void prologue8(const RotArgs& a, int64_t m, int64_t c, float rstd, int64_t trow, float* v) {
   if (KIND == ROT_HEADS) {
     unpack8(*reinterpret_cast<const uint4*>(a.x + (c >> 7) * a.ld_head + m * a.ldx + (c & 127)), v);
@@ -104,20 +127,22 @@ __device__ __forceinline__ void prologue8(const RotArgs& a, int64_t m, int64_t c
   } else {
     unpack8(*reinterpret_cast<const uint4*>(a.x + m * a.ldx + c), v);
     if (KIND == ROT_NORMMOD) {
-      float wv[8];
+      float wv[8], sc[8], sh[8];
       if (a.w) unpack8(*reinterpret_cast<const uint4*>(a.w + c), wv);
+      tab8<TabT, VEC>(a.scale, trow + c, sc);
+      tab8<TabT, VEC>(a.shift, trow + c, sh);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         float y = v[e] * rstd;
         if (a.w) y = y * wv[e];
-        v[e] = y * (1.0f + tab_at<TabT>(a.scale, trow + c + e)) + tab_at<TabT>(a.shift, trow + c + e);
+        v[e] = y * (1.0f + sc[e]) + sh[e];
       }
     }
   }
 }
 
 // y = the rotated values of chunk ch (zeros for a lane past the row: its whole quad is past it)
-template <int KIND, typename TabT>
+template <int KIND, typename TabT, bool VEC>
 __device__ __forceinline__ void rot_act_chunk(const RotArgs& a, int64_t m, int64_t ch, bool valid, float rstd,
                                               int64_t trow, float sb, float sc, float sd, float (&y)[64]) {
   double d[64];
@@ -125,9 +150,13 @@ __device__ __forceinline__ void rot_act_chunk(const RotArgs& a, int64_t m, int64
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
       float v[8];
-      prologue8<KIND, TabT>(a, m, ch * 64 + 8 * t, rstd, trow, v);
+      prologue8<KIND, TabT, VEC>(a, m, ch * 64 + 8 * t, rstd, trow, v);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) d[8 * t + e] = static_cast<double>(round_bf(v[e]));
+      for (int e = 0; e < 8; e += 2) {  // bf16 round to nearest even (v_cvt_pk_bf16_f32), back to fp32 exactly
+        const uint32_t pk = pk_bf16_hw(v[e], v[e + 1]);
+        d[8 * t + e] = static_cast<double>(__uint_as_float(pk << 16));
+        d[8 * t + e + 1] = static_cast<double>(__uint_as_float(pk & 0xffff0000u));
+      }
     }
   } else {
 #pragma unroll
@@ -164,24 +193,35 @@ __device__ __forceinline__ void store64(int8_t* q, const float (&y)[64], float i
 }
 
 // NP = passes of 64 chunks (K <= 4096 * NP). With one pass the rotated values stay in registers between
-// the absmax and the quantization; with more, each pass is computed twice (the row is re-read from L2).
-template <int KIND, typename TabT, int NP>
-__global__ void __launch_bounds__(256) rot_quant_kernel(const RotArgs a) {
-  const int lane = threadIdx.x & 63;
-  const int64_t m = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  if (m >= a.M) return;  // whole wavefront: DPP partners never leave
+// the absmax and the quantization; with more, the values of passes 0..NP-2 wait in LDS (64 floats per
+// lane, lane-interleaved float4s, a private region per wave) until the row scale is known.
+template <int NP> constexpr int rot_waves() { return NP <= 2 ? 4 : 2; }
+
+template <int KIND, typename TabT, int NP, bool VEC>
+__global__ void __launch_bounds__(64 * rot_waves<NP>()) rot_quant_kernel(const RotArgs a) {
+  constexpr int W = rot_waves<NP>();
+  __shared__ float4 stash[NP > 1 ? W * (NP - 1) * 16 * 64 : 1];  // [wave][pass][i / 4][lane]
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t m = static_cast<int64_t>(blockIdx.x) * W + wave;
+  if (m >= a.M) return;  // whole wavefront: DPP partners never leave; no workgroup barrier below
   const int q4 = lane & 3;
   const float sb = q4 == 2 ? -1.0f : 1.0f, sc = q4 == 1 ? -1.0f : 1.0f, sd = (q4 == 0 || q4 == 3) ? -1.0f : 1.0f;
   float rstd = 0.0f;
   int64_t trow = 0;
   if (KIND == ROT_NORMMOD) {
-    // sum of squares in the order of quant.hip (lane chunks 512 j + 8 l, (j, e) sequential, butterfly)
-    float ss = 0.0f;
-    const int64_t nch = (a.K + 511) / 512;
-    for (int64_t j = 0; j < nch; ++j) {
+    // sum of squares in the order of quant.hip (lane chunks 512 j + 8 l, (j, e) sequential, butterfly);
+    // all of the row's loads are issued before the first product (K <= 4096 * NP, so j < 8 * NP)
+    uint4 r[8 * NP];
+#pragma unroll
+    for (int j = 0; j < 8 * NP; ++j) {
       const int64_t c = 512 * j + 8 * lane;
-      float v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-      if (c < a.K) unpack8(*reinterpret_cast<const uint4*>(a.x + m * a.ldx + c), v);
+      r[j] = c < a.K ? *reinterpret_cast<const uint4*>(a.x + m * a.ldx + c) : make_uint4(0, 0, 0, 0);
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8 * NP; ++j) {
+      float v[8];
+      unpack8(r[j], v);
 #pragma unroll
       for (int e = 0; e < 8; ++e) ss = ss + v[e] * v[e];
     }
@@ -190,30 +230,35 @@ __global__ void __launch_bounds__(256) rot_quant_kernel(const RotArgs a) {
     trow = static_cast<int64_t>(a.idx[m]) * a.ld_tab;
   }
   const int64_t nchunks = a.K / 64;
+  float4* my = stash + wave * (NP - 1) * 16 * 64 + lane;
   float y[64];
   float amax = 0.0f;
 #pragma unroll
   for (int p = 0; p < NP; ++p) {
     const int64_t ch = 64 * p + lane;
-    rot_act_chunk<KIND, TabT>(a, m, ch, ch < nchunks, rstd, trow, sb, sc, sd, y);
+    rot_act_chunk<KIND, TabT, VEC>(a, m, ch, ch < nchunks, rstd, trow, sb, sc, sd, y);
 #pragma unroll
     for (int i = 0; i < 64; ++i) amax = fmaxf(amax, fabsf(y[i]));
-    __builtin_amdgcn_sched_barrier(0);  // passes do not overlap: one chunk's 64 doubles live at a time
+    if (p < NP - 1) {
+#pragma unroll
+      for (int t = 0; t < 16; ++t) my[(p * 16 + t) * 64] = make_float4(y[4 * t], y[4 * t + 1], y[4 * t + 2], y[4 * t + 3]);
+    }
   }
   amax = wave_max(amax);
   const float s = fmaxf(amax / 127.0f, 1e-12f);
   const float inv = 1.0f / s;
   if (lane == 0) a.s[m] = s;
-  if (NP == 1) {
-    if (lane < nchunks) store64(a.q + m * a.ldq + 64 * lane, y, inv);
-  } else {
+  const int64_t last = 64 * (NP - 1) + lane;
+  if (last < nchunks) store64(a.q + m * a.ldq + 64 * last, y, inv);
 #pragma unroll
-    for (int p = 0; p < NP; ++p) {
-      const int64_t ch = 64 * p + lane;
-      rot_act_chunk<KIND, TabT>(a, m, ch, ch < nchunks, rstd, trow, sb, sc, sd, y);
-      if (ch < nchunks) store64(a.q + m * a.ldq + 64 * ch, y, inv);
-      __builtin_amdgcn_sched_barrier(0);
+  for (int p = 0; p < NP - 1; ++p) {
+    const int64_t ch = 64 * p + lane;
+#pragma unroll
+    for (int t = 0; t < 16; ++t) {
+      const float4 u = my[(p * 16 + t) * 64];
+      y[4 * t] = u.x; y[4 * t + 1] = u.y; y[4 * t + 2] = u.z; y[4 * t + 3] = u.w;
     }
+    if (ch < nchunks) store64(a.q + m * a.ldq + 64 * ch, y, inv);
   }
 }
 
@@ -328,13 +373,28 @@ __global__ void __launch_bounds__(256) rot_exact_kernel(const ExactArgs a) {
   }
 }
 
+template <int KIND, typename TabT, bool VEC>
+void launch_act_np(const RotArgs& a, hipStream_t st) {
+  if (a.K <= 4096) {
+    hipLaunchKernelGGL((rot_quant_kernel<KIND, TabT, 1, VEC>), dim3(static_cast<unsigned>((a.M + 3) / 4)), dim3(256), 0,
+                       st, a);
+  } else if (a.K <= 8192) {
+    hipLaunchKernelGGL((rot_quant_kernel<KIND, TabT, 2, VEC>), dim3(static_cast<unsigned>((a.M + 3) / 4)), dim3(256), 0,
+                       st, a);
+  } else {
+    hipLaunchKernelGGL((rot_quant_kernel<KIND, TabT, 4, VEC>), dim3(static_cast<unsigned>((a.M + 1) / 2)), dim3(128), 0,
+                       st, a);
+  }
+}
+
 template <int KIND, typename TabT>
 int launch_act(const RotArgs& a, hipStream_t st, const char* name) {
   if (a.M == 0) return RH3_OK;
-  const dim3 grid(static_cast<unsigned>((a.M + 3) / 4)), block(256);
-  if (a.K <= 4096) hipLaunchKernelGGL((rot_quant_kernel<KIND, TabT, 1>), grid, block, 0, st, a);
-  else if (a.K <= 8192) hipLaunchKernelGGL((rot_quant_kernel<KIND, TabT, 2>), grid, block, 0, st, a);
-  else hipLaunchKernelGGL((rot_quant_kernel<KIND, TabT, 4>), grid, block, 0, st, a);
+  // 16-byte modulation-table loads when every row start is 16-byte aligned
+  const bool vec = KIND != ROT_NORMMOD ||
+                   (aligned16(a.shift) && aligned16(a.scale) && (a.ld_tab * static_cast<int64_t>(sizeof(TabT))) % 16 == 0);
+  if (vec) launch_act_np<KIND, TabT, true>(a, st);
+  else launch_act_np<KIND, TabT, false>(a, st);
   return launch_status(name);
 }
 
