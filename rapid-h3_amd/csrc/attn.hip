@@ -276,11 +276,16 @@ __device__ __forceinline__ int max_halves(int v) {
 // Global -> LDS copy of 16 bytes per lane: lane l of the wave writes LDS byte offset lds_base + 16*l
 // (M0 holds the wave-uniform base). Issued from inline assembly so that the compiler adds no wait of
 // its own for it: the kernel below accounts for these loads itself (s_waitcnt vmcnt) and issues no
-// other vector-memory loads while they are in flight. gfx9 requires one wait state between writing M0
-// and an LDS DMA that reads it.
+// other vector-memory loads while they are in flight. M0 is a reserved register, so the statement
+// restores the value it found; gfx9 requires one wait state between writing M0 and an LDS DMA that
+// reads it.
 __device__ __forceinline__ void lds_dma16(const void* gptr, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds_base)
-               : "memory", "m0");
+  uint32_t saved;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off\n\t"
+               "s_nop 0\n\ts_mov_b32 m0, %0"
+               : "=&s"(saved)
+               : "v"(gptr), "s"(lds_base)
+               : "memory");
 }
 
 // Step j (64 keys) reads K(j) and V^T(j) from ring slot j % 4 and first loads K(j+2), V^T(j+2) into slot

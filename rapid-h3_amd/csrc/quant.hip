@@ -44,6 +44,21 @@ template <> __device__ __forceinline__ float tab_load<uint16_t>(const void* p, i
   return bf2f(static_cast<const uint16_t*>(p)[i]);
 }
 
+// 8 consecutive table values at element i (VEC: 16-byte loads; the launcher checked the alignment)
+template <typename TabT, bool VEC>
+__device__ __forceinline__ void tab_load8(const void* p, int64_t i, float* t) {
+  if (VEC && sizeof(TabT) == 4) {
+    const float4* q = reinterpret_cast<const float4*>(static_cast<const float*>(p) + i);
+    const float4 u0 = q[0], u1 = q[1];
+    t[0] = u0.x; t[1] = u0.y; t[2] = u0.z; t[3] = u0.w; t[4] = u1.x; t[5] = u1.y; t[6] = u1.z; t[7] = u1.w;
+  } else if (VEC) {
+    unpack8(*reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p) + i), t);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) t[e] = tab_load<TabT>(p, i + e);
+  }
+}
+
 __device__ __forceinline__ float silu_mul(float g, float u) {
   const float sig = 1.0f / (1.0f + __expf(-g));
   return (g * sig) * u;
@@ -81,28 +96,47 @@ __device__ __forceinline__ void load_chunk(const QuantArgs& a, int64_t m, int64_
   }
 }
 
-// NCH = 512-column chunks held in registers per lane (row width <= 512 * NCH)
-template <int NCH, int KIND, bool FP8, typename TabT>
+// NCH = 512-column chunks held in registers per lane (row width <= 512 * NCH). PLAIN and HEADS keep the
+// raw bf16 words (4 VGPRs per 8 columns) and unpack them again for the quantization; the prologue kinds
+// keep fp32 values.
+template <int NCH, int KIND, bool FP8, typename TabT, bool VEC>
 __global__ void __launch_bounds__(256) quant_rows_kernel(const QuantArgs a) {
+  constexpr bool RAW = KIND == KIND_PLAIN || KIND == KIND_HEADS;
   const int lane = threadIdx.x & 63;
   const int64_t m = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (m >= a.M) return;
-  float v[NCH][8];
+  uint4 raw[RAW ? NCH : 1];
+  float v[RAW ? 1 : NCH][8];
 #pragma unroll
   for (int j = 0; j < NCH; ++j) {
     const int64_t c = 512 * j + 8 * lane;
-    if (c < a.K) load_chunk<KIND>(a, m, c, v[j]);
-    else {
+    if (RAW) {
+      if (c < a.K) {
+        const uint16_t* p = KIND == KIND_HEADS ? a.x + (c >> 7) * a.ld_head + m * a.ldx + (c & 127) : a.x + m * a.ldx + c;
+        raw[j] = *reinterpret_cast<const uint4*>(p);
+      } else {
+        raw[j] = make_uint4(0, 0, 0, 0);
+      }
+    } else if (c < a.K) {
+      load_chunk<KIND>(a, m, c, v[j]);
+    } else {
 #pragma unroll
       for (int e = 0; e < 8; ++e) v[j][e] = 0.0f;
     }
   }
+  auto vals = [&](int j, float* out) __attribute__((always_inline)) {
+    if (RAW) unpack8(raw[j], out);
+    else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) out[e] = v[j][e];
+    }
+  };
   if (KIND == KIND_NORMMOD) {
     float ss = 0.0f;
 #pragma unroll
     for (int j = 0; j < NCH; ++j)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) ss = ss + v[j][e] * v[j][e];
+      for (int e = 0; e < 8; ++e) ss = fmaf(v[j][e], v[j][e], ss);  // x*x exact (bf16 x): same as ss + x*x
     ss = wave_sum_tree(ss);
     const float rstd = 1.0f / sqrtf(ss / static_cast<float>(a.K) + a.eps);
     const int64_t t = static_cast<int64_t>(a.idx[m]) * a.ld_tab;
@@ -110,25 +144,34 @@ __global__ void __launch_bounds__(256) quant_rows_kernel(const QuantArgs a) {
     for (int j = 0; j < NCH; ++j) {
       const int64_t c = 512 * j + 8 * lane;
       if (c < a.K) {
-        float wv[8];
+        float wv[8], sc[8], sh[8];
         if (a.w) unpack8(*reinterpret_cast<const uint4*>(a.w + c), wv);
+        tab_load8<TabT, VEC>(a.scale, t + c, sc);
+        tab_load8<TabT, VEC>(a.shift, t + c, sh);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           float y = v[j][e] * rstd;
           if (a.w) y = y * wv[e];
-          const float sc = tab_load<TabT>(a.scale, t + c + e);
-          const float sh = tab_load<TabT>(a.shift, t + c + e);
-          v[j][e] = y * (1.0f + sc) + sh;
+          v[j][e] = y * (1.0f + sc[e]) + sh[e];
         }
       }
     }
   }
   float amax = 0.0f;
 #pragma unroll
-  for (int j = 0; j < NCH; ++j)
+  for (int j = 0; j < NCH; ++j) {
+    float x[8];
+    vals(j, x);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[j][e]));
+    for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(x[e]));
+  }
   amax = wave_max(amax);
+  if (RAW) {
+    // the raw words are unpacked again below rather than kept as floats (the empty asm hides the first
+    // unpack from common-subexpression elimination, which would hold 8 floats per chunk live)
+#pragma unroll
+    for (int j = 0; j < (RAW ? NCH : 0); ++j) asm volatile("" : "+v"(raw[j].x), "+v"(raw[j].y), "+v"(raw[j].z), "+v"(raw[j].w));
+  }
   const float qmax = FP8 ? 448.0f : 127.0f;
   const float s = fmaxf(amax / qmax, 1e-12f);
   const float inv = 1.0f / s;
@@ -137,26 +180,116 @@ __global__ void __launch_bounds__(256) quant_rows_kernel(const QuantArgs a) {
   for (int j = 0; j < NCH; ++j) {
     const int64_t c = 512 * j + 8 * lane;
     if (c >= a.K) continue;
-    uint32_t b[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      if (FP8) {
-        const float t = fminf(fmaxf(v[j][e] / s, -448.0f), 448.0f);
-        b[e] = fp8_e4m3(t);
-      } else {
-        const float r = fminf(fmaxf(rint_div(v[j][e], s, inv), -127.0f), 127.0f);
-        b[e] = static_cast<uint32_t>(static_cast<int32_t>(r)) & 0xffu;
-      }
-    }
+    float x[8];
+    vals(j, x);
     uint2 out;
-    out.x = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
-    out.y = b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24);
+    if (FP8) {
+      uint32_t b[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) b[e] = fp8_e4m3(fminf(fmaxf(x[e] / s, -448.0f), 448.0f));
+      out.x = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
+      out.y = b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24);
+    } else {
+      out = quant8_i8(x, s, inv);
+    }
     *reinterpret_cast<uint2*>(static_cast<int8_t*>(a.q) + m * a.ldq + c) = out;
   }
 }
 
+// KIND_NORMMOD with the modulation rows and the norm weight staged in LDS: every token of a segment reads
+// the same table row, so a workgroup copies the row of its first token once (as fp32, plus the weight) and
+// each wavefront then quantizes RPW rows from LDS; a row with another table index reads its values from
+// global memory. Same arithmetic and order as quant_rows_kernel<NCH, KIND_NORMMOD>.
+constexpr int NM_RPW = 8;  // rows per wavefront
+template <int NCH, typename TabT>
+__global__ void __launch_bounds__(256) quant_normmod_lds_kernel(const QuantArgs a) {
+  extern __shared__ float4 nm_lds[];   // [K/4] scale, [K/4] shift, [K/8] weight (bf16 x 8 per uint4)
+  float* sc_s = reinterpret_cast<float*>(nm_lds);
+  float* sh_s = sc_s + a.K;
+  uint16_t* w_s = reinterpret_cast<uint16_t*>(sh_s + a.K);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * 4 * NM_RPW;
+  const int32_t idx0 = a.idx[r0];
+  const int64_t t0 = static_cast<int64_t>(idx0) * a.ld_tab;
+  for (int64_t c = threadIdx.x * 4; c < a.K; c += 256 * 4) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      sc_s[c + e] = 1.0f + tab_load<TabT>(a.scale, t0 + c + e);  // the (1 + scale) of every token of the row
+      sh_s[c + e] = tab_load<TabT>(a.shift, t0 + c + e);
+    }
+  }
+  for (int64_t c = threadIdx.x * 8; c < a.K; c += 256 * 8)
+    *reinterpret_cast<uint4*>(w_s + c) = a.w ? *reinterpret_cast<const uint4*>(a.w + c) : make_uint4(0, 0, 0, 0);
+  __syncthreads();
+  for (int i = 0; i < NM_RPW; ++i) {
+    const int64_t m = r0 + static_cast<int64_t>(i) * 4 + wave;
+    if (m >= a.M) break;
+    float v[NCH][8];
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      const int64_t c = 512 * j + 8 * lane;
+      if (c < a.K) unpack8(*reinterpret_cast<const uint4*>(a.x + m * a.ldx + c), v[j]);
+      else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[j][e] = 0.0f;
+      }
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NCH; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss = fmaf(v[j][e], v[j][e], ss);  // x*x exact (bf16 x): same as ss + x*x
+    ss = wave_sum_tree(ss);
+    const float rstd = 1.0f / sqrtf(ss / static_cast<float>(a.K) + a.eps);
+    const int32_t im = a.idx[m];
+    const int64_t t = static_cast<int64_t>(im) * a.ld_tab;
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      const int64_t c = 512 * j + 8 * lane;
+      if (c < a.K) {
+        float wv[8], sc[8], sh[8];
+        if (a.w) unpack8(*reinterpret_cast<const uint4*>(w_s + c), wv);
+        if (im == idx0) {
+          const float4* ps = reinterpret_cast<const float4*>(sc_s + c);
+          const float4* ph = reinterpret_cast<const float4*>(sh_s + c);
+          const float4 s0 = ps[0], s1 = ps[1], h0 = ph[0], h1 = ph[1];
+          sc[0] = s0.x; sc[1] = s0.y; sc[2] = s0.z; sc[3] = s0.w; sc[4] = s1.x; sc[5] = s1.y; sc[6] = s1.z; sc[7] = s1.w;
+          sh[0] = h0.x; sh[1] = h0.y; sh[2] = h0.z; sh[3] = h0.w; sh[4] = h1.x; sh[5] = h1.y; sh[6] = h1.z; sh[7] = h1.w;
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            sc[e] = 1.0f + tab_load<TabT>(a.scale, t + c + e);
+            sh[e] = tab_load<TabT>(a.shift, t + c + e);
+          }
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          float y = v[j][e] * rstd;
+          if (a.w) y = y * wv[e];
+          v[j][e] = y * sc[e] + sh[e];
+        }
+      }
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NCH; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[j][e]));
+    amax = wave_max(amax);
+    const float s = fmaxf(amax / 127.0f, 1e-12f);
+    const float inv = 1.0f / s;
+    if (lane == 0) a.s[m] = s;
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      const int64_t c = 512 * j + 8 * lane;
+      if (c >= a.K) continue;
+      *reinterpret_cast<uint2*>(static_cast<int8_t*>(a.q) + m * a.ldq + c) = quant8_i8(v[j], s, inv);
+    }
+  }
+}
+
 // Rows wider than 8192: same arithmetic, re-reading the row (from L2) instead of holding it.
-template <int KIND, bool FP8, typename TabT>
+template <int KIND, bool FP8, typename TabT, bool VEC>
 __global__ void __launch_bounds__(256) quant_rows_wide_kernel(const QuantArgs a) {
   const int lane = threadIdx.x & 63;
   const int64_t m = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
@@ -180,13 +313,15 @@ __global__ void __launch_bounds__(256) quant_rows_wide_kernel(const QuantArgs a)
   auto value = [&](int64_t c, float* v) {
     load_chunk<KIND>(a, m, c, v);
     if (KIND == KIND_NORMMOD) {
-      float wv[8];
+      float wv[8], sc[8], sh[8];
       if (a.w) unpack8(*reinterpret_cast<const uint4*>(a.w + c), wv);
+      tab_load8<TabT, VEC>(a.scale, t + c, sc);
+      tab_load8<TabT, VEC>(a.shift, t + c, sh);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         float y = v[e] * rstd;
         if (a.w) y = y * wv[e];
-        v[e] = y * (1.0f + tab_load<TabT>(a.scale, t + c + e)) + tab_load<TabT>(a.shift, t + c + e);
+        v[e] = y * (1.0f + sc[e]) + sh[e];
       }
     }
   };
@@ -226,19 +361,40 @@ __global__ void __launch_bounds__(256) quant_rows_wide_kernel(const QuantArgs a)
   }
 }
 
+template <int KIND, bool FP8, typename TabT, bool VEC>
+void launch_vec(const QuantArgs& a, hipStream_t st) {
+  const dim3 grid(static_cast<unsigned>((a.M + 3) / 4)), block(256);
+  const int64_t nch = (a.K + 511) / 512;
+  if (nch <= 1) hipLaunchKernelGGL((quant_rows_kernel<1, KIND, FP8, TabT, VEC>), grid, block, 0, st, a);
+  else if (nch <= 2) hipLaunchKernelGGL((quant_rows_kernel<2, KIND, FP8, TabT, VEC>), grid, block, 0, st, a);
+  else if (nch <= 4) hipLaunchKernelGGL((quant_rows_kernel<4, KIND, FP8, TabT, VEC>), grid, block, 0, st, a);
+  else if (nch <= 6) hipLaunchKernelGGL((quant_rows_kernel<6, KIND, FP8, TabT, VEC>), grid, block, 0, st, a);
+  else if (nch <= 8) hipLaunchKernelGGL((quant_rows_kernel<8, KIND, FP8, TabT, VEC>), grid, block, 0, st, a);
+  else if (nch <= 12) hipLaunchKernelGGL((quant_rows_kernel<12, KIND, FP8, TabT, VEC>), grid, block, 0, st, a);
+  else if (nch <= 16) hipLaunchKernelGGL((quant_rows_kernel<16, KIND, FP8, TabT, VEC>), grid, block, 0, st, a);
+  else hipLaunchKernelGGL((quant_rows_wide_kernel<KIND, FP8, TabT, VEC>), grid, block, 0, st, a);
+}
+
 template <int KIND, bool FP8, typename TabT>
 int launch(const QuantArgs& a, hipStream_t st, const char* name) {
   if (a.M == 0) return RH3_OK;
-  const dim3 grid(static_cast<unsigned>((a.M + 3) / 4)), block(256);
-  const int64_t nch = (a.K + 511) / 512;
-  if (nch <= 1) hipLaunchKernelGGL((quant_rows_kernel<1, KIND, FP8, TabT>), grid, block, 0, st, a);
-  else if (nch <= 2) hipLaunchKernelGGL((quant_rows_kernel<2, KIND, FP8, TabT>), grid, block, 0, st, a);
-  else if (nch <= 4) hipLaunchKernelGGL((quant_rows_kernel<4, KIND, FP8, TabT>), grid, block, 0, st, a);
-  else if (nch <= 6) hipLaunchKernelGGL((quant_rows_kernel<6, KIND, FP8, TabT>), grid, block, 0, st, a);
-  else if (nch <= 8) hipLaunchKernelGGL((quant_rows_kernel<8, KIND, FP8, TabT>), grid, block, 0, st, a);
-  else if (nch <= 12) hipLaunchKernelGGL((quant_rows_kernel<12, KIND, FP8, TabT>), grid, block, 0, st, a);
-  else if (nch <= 16) hipLaunchKernelGGL((quant_rows_kernel<16, KIND, FP8, TabT>), grid, block, 0, st, a);
-  else hipLaunchKernelGGL((quant_rows_wide_kernel<KIND, FP8, TabT>), grid, block, 0, st, a);
+  // up to 6144 columns the staged rows fit in 60 KB of LDS
+  if (KIND == KIND_NORMMOD && !FP8 && a.K <= 6144 && a.K % 8 == 0) {
+    const dim3 grid(static_cast<unsigned>((a.M + 4 * NM_RPW - 1) / (4 * NM_RPW))), block(256);
+    const size_t lds = static_cast<size_t>(a.K) * (4 + 4 + 2);
+    const int64_t nch = (a.K + 511) / 512;
+    if (nch <= 2) hipLaunchKernelGGL((quant_normmod_lds_kernel<2, TabT>), grid, block, lds, st, a);
+    else if (nch <= 4) hipLaunchKernelGGL((quant_normmod_lds_kernel<4, TabT>), grid, block, lds, st, a);
+    else if (nch <= 6) hipLaunchKernelGGL((quant_normmod_lds_kernel<6, TabT>), grid, block, lds, st, a);
+    else if (nch <= 8) hipLaunchKernelGGL((quant_normmod_lds_kernel<8, TabT>), grid, block, lds, st, a);
+    else hipLaunchKernelGGL((quant_normmod_lds_kernel<12, TabT>), grid, block, lds, st, a);
+    return launch_status(name);
+  }
+  // 16-byte modulation-table loads when every table row start is 16-byte aligned
+  const bool vec = KIND != KIND_NORMMOD || (aligned16(a.shift) && aligned16(a.scale) &&
+                                            (a.ld_tab * static_cast<int64_t>(sizeof(TabT))) % 16 == 0);
+  if (vec) launch_vec<KIND, FP8, TabT, true>(a, st);
+  else launch_vec<KIND, FP8, TabT, false>(a, st);
   return launch_status(name);
 }
 

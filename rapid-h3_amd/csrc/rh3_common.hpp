@@ -67,6 +67,31 @@ __device__ __forceinline__ float rint_div(float x, float s, float inv) {
   return n;
 }
 
+// 8 int8 codes clamp(rint(x[e] / s), -127, 127) packed little-endian into two words: the multiply by
+// inv = 1/s decides every lane except those within 2^-12 of a half-integer, and one wave-wide vote per
+// 8 values sends only those through the IEEE division (bit-identical to rint_div element by element).
+__device__ __forceinline__ uint2 quant8_i8(const float* x, float s, float inv) {
+  float n[8];
+  bool need = false;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float t = x[e] * inv;
+    n[e] = rintf(t);
+    need |= fabsf(t - n[e]) > 0.5f - 0x1p-12f;
+  }
+  if (__builtin_amdgcn_ballot_w64(need) != 0) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float t = x[e] * inv;
+      if (fabsf(t - n[e]) > 0.5f - 0x1p-12f) n[e] = rintf(x[e] / s);
+    }
+  }
+  uint32_t b[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) b[e] = static_cast<uint32_t>(static_cast<int32_t>(fminf(fmaxf(n[e], -127.0f), 127.0f))) & 0xffu;
+  return make_uint2(b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24), b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24));
+}
+
 // ---------------------------------------------------------------- device: wavefront reductions
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
