@@ -31,12 +31,18 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 
 enum Epi { EPI_PLAIN = 0, EPI_SWIGLU = 1, EPI_GATED = 2, EPI_ACC = 3 };
 
-constexpr int BM = 256, BN = 256, BK = 64, NT = 512;
-// 8 waves in a 2 (m) x 4 (n) grid, 128 x 64 outputs per wave: 2 waves per SIMD hide each other's LDS and
-// barrier latency
-constexpr int WAVES = NT / 64, WM = 128, WN = 64, TI = WN / 32, TJ = WM / 32;
+constexpr int BM = 256, BN = 256, BK = 64;
+// NW waves in a 2 (m) x NW/2 (n) grid, 128 x (512 / NW) outputs per wave. NW = 8: 2 waves per SIMD hide
+// each other's LDS and barrier latency. NW = 4: one wave per SIMD with 128 x 128 outputs (accumulators in
+// AGPRs), which reads 8 fragments per 16 MFMAs instead of 6 per 8 and so takes a third less LDS bandwidth
+// per MFMA.
+template <int NW>
+struct Cfg {
+  static constexpr int NT = NW * 64, WM = 128, WN = BN / (NW / 2), TI = WN / 32, TJ = WM / 32;
+  static constexpr int LOADS = 2 * (BM * BK / 16) / NT;  // global->LDS loads per wave per k-step (both operands)
+};
 #ifndef RH3_GEMM_GROUP_M
-#define RH3_GEMM_GROUP_M 1
+#define RH3_GEMM_GROUP_M 4
 #endif
 constexpr int GROUP_M = RH3_GEMM_GROUP_M;
 constexpr int TILE_BYTES = BM * BK;  // per operand per stage (BM == BN)
@@ -104,10 +110,20 @@ struct Mma<true> {  // e4m3: 1 MFMA of k = 64 per step, 32-byte fragments (two 1
   __device__ static float val(const acc_t& c, int r) { return c[r]; }
 };
 
-template <bool FP8, int EPI>
-__global__ void __launch_bounds__(NT, 2) gemm_kernel(const GemmArgs a) {
+#ifndef RH3_GEMM_NW
+#define RH3_GEMM_NW 8
+#endif
+
+template <bool FP8, int EPI, int NW>
+__global__ void __launch_bounds__(RH3_GEMM_NW * 64, RH3_GEMM_NW / 4) gemm_kernel(const GemmArgs a) {
+  static_assert(NW == RH3_GEMM_NW, "one wave count per build");
   using MM = Mma<FP8>;
   using acc_t = typename MM::acc_t;
+  constexpr int NT = Cfg<NW>::NT, WM = Cfg<NW>::WM, WN = Cfg<NW>::WN, TI = Cfg<NW>::TI, TJ = Cfg<NW>::TJ;
+  // loads per operand per wave per k-step (from the macro: an array sized by a template-dependent
+  // constant makes clang's host pass drop the kernel's launch stub)
+  constexpr int NL = (BM * BK / 16) / (RH3_GEMM_NW * 64);
+  static_assert(NL == Cfg<NW>::LOADS / 2, "load count");
   // 4-stage ring, each stage its own LDS object {x tile, w tile} (2 x 16 KiB) named statically: the
   // asynchronous global->LDS loads into one stage then provably do not alias the reads of another
   __shared__ __attribute__((aligned(16))) int8_t st0[2 * TILE_BYTES], st1[2 * TILE_BYTES], st2[2 * TILE_BYTES],
@@ -127,18 +143,18 @@ __global__ void __launch_bounds__(NT, 2) gemm_kernel(const GemmArgs a) {
   const int64_t m0 = static_cast<int64_t>(tm) * BM, n0 = static_cast<int64_t>(tn) * BN;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 2, wn = wave & 3;
+  const int wm = wave / (NW / 2), wn = wave % (NW / 2);
   const int l32 = lane & 31, g = lane >> 5;
 
   // Global -> LDS loads bypass VGPRs (global_load_lds_dwordx4: lane l of a wave writes LDS base + 16*l),
   // so the XOR swizzle is applied on the global side: stage position p (16-byte units, 1024 per operand)
   // holds row p / 4, logical chunk (p % 4) ^ f(row) (swz is an involution on the chunk index). Wave w
-  // fills positions (2w + i)*64 + lane, i = 0, 1, of each operand.
-  const int8_t* xp[2];
-  const int8_t* wp[2];
+  // fills positions (NL*w + i)*64 + lane, i = 0 .. NL-1, of each operand.
+  const int8_t* xp[NL];
+  const int8_t* wp[NL];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int p = (2 * wave + i) * 64 + lane, r = p >> 2;
+  for (int i = 0; i < NL; ++i) {
+    const int p = (NL * wave + i) * 64 + lane, r = p >> 2;
     const int c = (p & 3) ^ (((r >> 1) & 3) ^ ((r >> 3) & 1));
     int64_t mr = m0 + r, nr = n0 + r;
     mr = mr < a.M ? mr : a.M - 1;
@@ -152,9 +168,9 @@ __global__ void __launch_bounds__(NT, 2) gemm_kernel(const GemmArgs a) {
   auto gload = [&](int kt, int8_t* stg) __attribute__((always_inline)) {
     const int64_t k0 = static_cast<int64_t>(min(kt, nk - 1)) * BK;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      __builtin_amdgcn_global_load_lds(xp[i] + k0, stg + (2 * wave + i) * 1024, 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(wp[i] + k0, stg + TILE_BYTES + (2 * wave + i) * 1024, 16, 0, 0);
+    for (int i = 0; i < NL; ++i) {
+      __builtin_amdgcn_global_load_lds(xp[i] + k0, stg + (NL * wave + i) * 1024, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(wp[i] + k0, stg + TILE_BYTES + (NL * wave + i) * 1024, 16, 0, 0);
     }
   };
 
@@ -166,11 +182,17 @@ __global__ void __launch_bounds__(NT, 2) gemm_kernel(const GemmArgs a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
 
-  // s_waitcnt on gfx9: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14]; 0x0078 is vmcnt(8)
-  // expcnt(7) lgkmcnt(0). The empty asm statements keep the compiler from moving memory accesses across.
+  // s_waitcnt on gfx9: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14]; wait_next is vmcnt(2 x
+  // the loads of one k-step) expcnt(7) lgkmcnt(0): the loads of the next k-step have landed, the two after
+  // it stay in flight. The empty asm statements keep the compiler from moving memory accesses across.
+  static_assert(2 * Cfg<NW>::LOADS == (NW == 8 ? 8 : 16), "vmcnt immediates below");
+  auto wait_next = [&]() __attribute__((always_inline)) {
+    if constexpr (NW == 8) __builtin_amdgcn_s_waitcnt(0x0078);   // vmcnt(8)
+    else __builtin_amdgcn_s_waitcnt(0x4070);                     // vmcnt(16)
+  };
   auto sync_next = [&]() __attribute__((always_inline)) {
     asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_waitcnt(0x0078);
+    wait_next();
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
   };
@@ -183,10 +205,16 @@ __global__ void __launch_bounds__(NT, 2) gemm_kernel(const GemmArgs a) {
     for (int j = 0; j < TJ; ++j) fb[j] = MM::load(stg, wm * WM + j * 32 + l32, ks, g);
   };
   auto mma_all = [&](const typename MM::frag_t* fa, const typename MM::frag_t* fb) __attribute__((always_inline)) {
+#ifdef RH3_GEMM_SETPRIO
+    __builtin_amdgcn_s_setprio(1);
+#endif
 #pragma unroll
     for (int i = 0; i < TI; ++i)
 #pragma unroll
       for (int j = 0; j < TJ; ++j) acc[i][j] = MM::mma(fa[i], fb[j], acc[i][j]);
+#ifdef RH3_GEMM_SETPRIO
+    __builtin_amdgcn_s_setprio(0);
+#endif
   };
   // k-step kt, reading stage cur; loads step kt+3 into nxt3 (the stage of step kt-1, whose readers all
   // passed the previous step's barrier). int8 (two k = 32 halves): the fragments of half 0 were read at
@@ -211,7 +239,7 @@ __global__ void __launch_bounds__(NT, 2) gemm_kernel(const GemmArgs a) {
   gload(0, st0);
   gload(1, st1);
   gload(2, st2);
-  asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+  wait_next();  // step 0 has landed
   __syncthreads();
   if constexpr (MM::KSUB == 2) load_frags(st0, 0, fa0, fb0);
   int kt = 0;
@@ -251,11 +279,15 @@ __global__ void __launch_bounds__(NT, 2) gemm_kernel(const GemmArgs a) {
     }
   } else {
     // bf16(y) (plain: bf16(y + bias)) goes through LDS so that the global side reads and writes whole
-    // 128-byte row segments: each wave stages its 128 x 64 block (16 KiB, row r at r*128, 16-byte chunk c
-    // at c ^ (r & 7)) in the now idle ring, then lane l handles row 8*it + l/8, columns 8*(l%8)..+7.
+    // row segments of WN columns: each wave stages its 128 x WN block (row r at r * PITCH, 16-byte chunk c
+    // at c ^ (r % CPR)) in the now idle ring, then lane l handles row RPI*it + l/CPR, columns
+    // 8*(l%CPR)..+7.
+    constexpr int PITCH = WN * 2, CPR = PITCH / 16, RPI = 64 / CPR;
     __syncthreads();  // every wave is done reading the ring
-    int8_t* const stage = (wave >> 1) == 0 ? st0 : (wave >> 1) == 1 ? st1 : (wave >> 1) == 2 ? st2 : st3;
-    int8_t* const ep = stage + (wave & 1) * 16384;
+    constexpr int PER_STAGE = 2 * TILE_BYTES / (WM * PITCH);  // staged wave blocks per ring stage
+    const int sidx = wave / PER_STAGE;
+    int8_t* const stage = sidx == 0 ? st0 : sidx == 1 ? st1 : sidx == 2 ? st2 : st3;
+    int8_t* const ep = stage + (wave % PER_STAGE) * (WM * PITCH);
 #pragma unroll
     for (int j = 0; j < TJ; ++j) {
       const int row = j * 32 + l32;
@@ -284,12 +316,12 @@ __global__ void __launch_bounds__(NT, 2) gemm_kernel(const GemmArgs a) {
           o.x = pack_bf2(y[0], y[1]);
           o.y = pack_bf2(y[2], y[3]);
           const int ch = col >> 3;  // 16-byte chunk; this lane's 8 bytes are its half g
-          *reinterpret_cast<uint2*>(ep + row * 128 + ((ch ^ (row & 7)) << 4) + 8 * g) = o;
+          *reinterpret_cast<uint2*>(ep + row * PITCH + ((ch ^ (row % CPR)) << 4) + 8 * g) = o;
         }
     }
     // each lane reads back what other lanes of its own wave wrote: LDS executes a wave's accesses in
     // order, and the compiler keeps the reads after the writes (same array)
-    const int ch = lane & 7;
+    const int ch = lane % CPR;
     const int64_t n = n0 + wn * WN + ch * 8;
     const bool nok = n < a.N;
     float gv[8];
@@ -297,10 +329,10 @@ __global__ void __launch_bounds__(NT, 2) gemm_kernel(const GemmArgs a) {
       if (nok) unpack8(*reinterpret_cast<const uint4*>(a.gate + n), gv);
     }
 #pragma unroll 4
-    for (int it = 0; it < WM / 8; ++it) {
-      const int row = it * 8 + (lane >> 3);
+    for (int it = 0; it < WM / RPI; ++it) {
+      const int row = it * RPI + lane / CPR;
       const int64_t m = m0 + wm * WM + row;
-      const uint4 v = *reinterpret_cast<const uint4*>(ep + row * 128 + ((ch ^ (row & 7)) << 4));
+      const uint4 v = *reinterpret_cast<const uint4*>(ep + row * PITCH + ((ch ^ (row % CPR)) << 4));
       if (m >= a.M || !nok) continue;
       if constexpr (EPI == EPI_PLAIN) {
         *reinterpret_cast<uint4*>(static_cast<uint16_t*>(a.out) + m * a.ldo + n) = v;
@@ -334,7 +366,8 @@ int run(GemmArgs a, hipStream_t st, const char* name) {
   a.tiles_n = static_cast<int>((a.N + BN - 1) / BN);
   const int64_t nb = static_cast<int64_t>(a.tiles_m) * a.tiles_n;
   RH3_REQUIRE(nb < (1ll << 31), "%s: too many tiles", name);
-  hipLaunchKernelGGL((gemm_kernel<FP8, EPI>), dim3(static_cast<unsigned>(nb)), dim3(NT), 0, st, a);
+  hipLaunchKernelGGL((gemm_kernel<FP8, EPI, RH3_GEMM_NW>), dim3(static_cast<unsigned>(nb)), dim3(RH3_GEMM_NW * 64), 0,
+                     st, a);
   return launch_status(name);
 }
 
