@@ -1,0 +1,73 @@
+"""QuantLinear: the reference's _QuantLinear (/root/reference/custom_nodes/rapid_h3/__init__.py:83-167)
+without ComfyUI: a replacement forward for one Linear that runs kernels.linear on librh3's kernels.
+
+What it keeps from the reference:
+  * the quantized weight is made once and cached; it is remade when the weight changes (the reference
+    keys its cache by ComfyUI's patches_uuid, :123-135; here the key is the weight tensor's identity,
+    storage pointer and version counter, which change when the weight is replaced or updated in place);
+  * an already-quantized Comfy int8_convrot weight (int8 [N, K] codes rotated with group 256 plus a
+    per-row scale) is adopted as is in int8_rot mode (:107-114), see from_quantized;
+  * the bias is added in x.dtype after the GEMM (:158-159);
+  * a weight cached in SwiGLU-epilogue row order is returned to natural order (:155-157);
+  * measure_every = n > 0 records the relative L2 error against F.linear every n calls into
+    stats[name] (:139-165).
+What it does not keep: ComfyUI's cast context for off-GPU / LoRA weights, and the F.linear path for CPU
+or non-16-bit inputs (:147-148), which here raise: no CPU path.
+"""
+import torch
+
+from . import kernels
+
+
+class QuantLinear:
+    def __init__(self, weight, bias=None, mode="int8_rot", name="linear", measure_every=0, stats=None):
+        if mode not in kernels.MODES or mode == "bf16":
+            raise ValueError(f"QuantLinear: mode {mode!r} (one of {kernels.MODES[1:]})")
+        self.weight, self.bias, self.mode, self.name = weight, bias, mode, name
+        self.measure_every = int(measure_every)
+        self.stats = {} if stats is None else stats
+        self.qweight, self.cache_key, self.calls = None, None, 0
+
+    @classmethod
+    def from_quantized(cls, qdata, scale, bias=None, group=256, transposed=False, name="linear", **kw):
+        """An int8_convrot checkpoint weight taken as is (no bf16 copy); measure_every needs a bf16 weight
+        and is off."""
+        self = cls(None, bias, "int8_rot", name, 0, kw.get("stats"))
+        self.qweight = kernels.adopt_convrot(qdata, scale, group=group, transposed=transposed)
+        self.cache_key = "adopted"
+        return self
+
+    def _key(self):
+        w = self.weight
+        return (id(w), w.data_ptr(), w._version, str(w.device))
+
+    def qweight_for(self):
+        """The cached quantized weight (quantized on first use or after the weight changed)."""
+        if self.cache_key == "adopted":
+            return self.qweight
+        key = self._key()
+        if key != self.cache_key:
+            self.qweight = kernels.quantize_weight(self.weight.detach(), self.mode)
+            self.cache_key = key
+        return self.qweight
+
+    def __call__(self, x):
+        if not x.is_cuda or x.dtype != torch.bfloat16:
+            raise TypeError(f"QuantLinear {self.name}: bf16 GPU activations only (no CPU path), got {x.dtype} "
+                            f"on {x.device}")
+        qw = self.qweight_for()
+        shape = x.shape
+        y = kernels.linear(x.reshape(-1, shape[-1]), qw, self.mode)
+        if getattr(qw, "swiglu_perm", False):   # fc1 held in SwiGLU-epilogue order
+            from .gemm import swiglu_perm
+            y = y[:, torch.argsort(swiglu_perm(y.shape[-1], y.device))]
+        if self.bias is not None:
+            y = y + self.bias.to(y.dtype)
+        y = y.reshape(*shape[:-1], y.shape[-1])
+        self.calls += 1
+        if self.measure_every and self.calls % self.measure_every == 0 and self.weight is not None:
+            ref = torch.nn.functional.linear(x, self.weight.to(x.dtype), None if self.bias is None else
+                                             self.bias.to(x.dtype))
+            err = ((y.float() - ref.float()).norm() / ref.float().norm().clamp_min(1e-12)).item()
+            self.stats.setdefault(self.name, []).append(err)
+        return y
