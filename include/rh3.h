@@ -197,6 +197,53 @@ int rh3_attention_forward(int64_t Sq, int64_t Sk, int64_t H, float scale,
                           uint16_t* out, int64_t o_ss, int64_t o_sh,
                           void* workspace, int64_t workspace_bytes, hipStream_t stream);
 
+/* ---------------------------------------------------------------------------------------------
+ * INT8 flash attention with the reference's production numerics (attn_int8.cu configs 80-99: attn_fwd8
+ * :2250-2511, and the cake configs 90/94 that are bit-identical to it; configs 1xx add the q/k RMSNorm +
+ * RoPE pre-pass). Q and K per (token, head) row: K mean-smoothed (smooth_k), both rotated by the
+ * normalized H128 Walsh-Hadamard matrix (rotate), sc = max(amax, 1e-8) / 127, q = rint(x / sc). V per
+ * channel: mean-smoothed (smooth_v), vscale = max(max(vmax - vmean, vmean - vmin), 1e-6) / 127, codes
+ * rint((v - vmean) / vscale). Per 128-key tile: u8 P = rint(255 * 2^(t - tile max)), int32 P.V, fp32
+ * fold with the running max; out = bf16(O / l * vscale + vmean).
+ * ------------------------------------------------------------------------------------------- */
+
+/* Bytes of workspace the production-numerics entry points need for (Sq, Sk, H). */
+int64_t rh3_attention_u8_workspace_bytes(int64_t Sq, int64_t Sk, int64_t H);
+
+/* replaces attn_int8.attention / attention_rr / attention_rr_bias -> int8_attention(_rr, _rr_bias)
+ * (attn_int8.py:30-65, attn_int8.cu:2660-2689) with config 80-99 (or 180-199). tab NULL: no RMSNorm/RoPE
+ * (then Sq may differ from Sk); otherwise tab [S, rot/2, 2, 2] bf16, qw / kw [128] bf16, self-attention
+ * only. nbias > 0 adds bias (natural-log units) to every query's logits of keys [0, nbias) (the Jenga
+ * text bias, attn_int8.cu:2763-2774, attn_cake.cuh:97-99). */
+int rh3_int8_attention_u8(const uint16_t* q, int64_t q_ss, int64_t q_sh,
+                          const uint16_t* k, int64_t k_ss, int64_t k_sh,
+                          const uint16_t* v, int64_t v_ss, int64_t v_sh,
+                          int64_t Sq, int64_t Sk, int64_t H, const uint16_t* tab, int rot,
+                          const uint16_t* qw, const uint16_t* kw, float eps, float scale,
+                          int nbias, double bias, int smooth_k, int smooth_v, int rotate,
+                          uint16_t* out, int64_t o_ss, int64_t o_sh,
+                          void* workspace, int64_t workspace_bytes, hipStream_t stream);
+
+/* Pre-pass operands of the production numerics for verification (the reference's prepass(),
+ * attn_int8.cu:2568-2644): returns pointers into the workspace to q8 [H, Sqpad, 128] int8,
+ * qs [H, Sqpad] fp32, k8 [H, Skpad, 128], ks [H, Skpad], side [H, Skpad/128, 2048 B] (per key the pair
+ * (ks, -1.5*2^23 * ks) as fp32, padded keys (0, -inf); then per channel the int32 accumulator start
+ * 1.5*2^23 bits + 128 * sum of the tile's V codes), vt [H, 128, Skpad] int8 V codes (keys permuted within
+ * 32-key blocks), kmean, vscale, vmean [H, 128] fp32. */
+int rh3_attention_u8_prepass(const uint16_t* q, int64_t q_ss, int64_t q_sh,
+                             const uint16_t* k, int64_t k_ss, int64_t k_sh,
+                             const uint16_t* v, int64_t v_ss, int64_t v_sh,
+                             int64_t Sq, int64_t Sk, int64_t H, const uint16_t* tab, int rot,
+                             const uint16_t* qw, const uint16_t* kw, float eps,
+                             int smooth_k, int smooth_v, int rotate,
+                             void* workspace, int64_t workspace_bytes, void** ptrs /* [9] */,
+                             hipStream_t stream);
+
+/* The production main kernel alone, on a workspace rh3_attention_u8_prepass filled for (Sq, Sk, H). */
+int rh3_attention_u8_forward(int64_t Sq, int64_t Sk, int64_t H, float scale, int nbias, double bias,
+                             uint16_t* out, int64_t o_ss, int64_t o_sh,
+                             void* workspace, int64_t workspace_bytes, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

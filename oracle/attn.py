@@ -149,3 +149,158 @@ def rope_table(positions, rot=96, theta=10000.0):
     ang = np.asarray(positions, np.float64)[:, None] * inv[None, :]
     c, s = np.cos(ang), np.sin(ang)
     return np.stack([np.stack([c, -s], -1), np.stack([s, c], -1)], -2).astype(F32)
+
+
+
+# ---------------------------------------------------------------- production numerics (configs 80-99)
+# The reference's production attention (attn_int8.cu config 80 = attn_fwd8 :2250-2511; configs 90/94 run the
+# same math on a persistent schedule, attn_cake/DESIGN.md "bit-identical to config 80"):
+#   pre-pass  (attn_int8.cu:2568-2644)
+#     * kmean, vmean: per-head channel means over all S tokens (K after the optional RMSNorm + RoPE);
+#       vscale = max(max(vmax - vm, vm - vmin), 1e-6) / 127                                (:97-109)
+#     * Q, K per (token, head) row: [RMSNorm + RoPE], K - kmean, the normalized Walsh-Hadamard H128 when
+#       rotate, sc = max(amax, 1e-8) / 127, q = rint(x * (1 / sc)); padded rows 0 with scale 0  (:130-170)
+#     * ksb = (sc, fp32(-1.5*2^23 * sc)) per key; padded keys (0, -inf)                    (:138, :168)
+#     * V per channel: code = rint((v - vm) / vscale)                                        (:452-475)
+#   main kernel, per 128-key tile (:2400-2470)
+#     * t = fma(float(1.5*2^23 + acc), s_j, b_j) (the integer accumulator starts at the bits of 1.5*2^23)
+#     * tm = tile row max, n = max(m, tm), a = 2^((m - n) c), ts = 2^((tm - n) c), m = n, with
+#       c = qs * scale * log2(e)
+#     * P = sat_u8(rint(2^(fma(t, c, fma(-tm, c, log2 255))))), rs = sum P, l = fma(ts, rs, l a)
+#     * O = a O + ts * sum_j P_j v8_j; out = bf16(fma(O (1 / l), vscale, vmean))
+#   text bias (attn_cake.cuh:97-99, :210-240): t += bias*log2(e) / c on keys [0, nbias) after the dequant.
+# Orders fixed by this build: kmean / vmean are float64 sums divided by S in float64 and rounded once (the
+# reference sums in fp32 per 256-token chunk); the Walsh-Hadamard stages are the reference's own (strides
+# 1, 2, ..., 64, each stage rounded to fp32), so codes and scales are bit-exact.
+
+MAGIC = F32(12582912.0)               # 1.5 * 2^23 (attn_int8.cu:22-23)
+MAGIC_I = 0x4B400000
+LOG2_255 = F32(7.99435343685886)      # attn_int8.cu:24
+INV_SQRT128 = F32(0.08838834764831845)
+TILE = 128
+
+
+def hadamard128(x):
+    """Normalized Walsh-Hadamard transform over the last axis (attn_int8.cu:113-128): radix-2 stages at
+    strides 1, 2, 4, ..., 64, (a, b) -> (a + b, a - b) in fp32, then * fp32(1 / sqrt(128))."""
+    y = np.asarray(x, F32)
+    shp = y.shape
+    for s in (1, 2, 4, 8, 16, 32, 64):
+        v = y.reshape(shp[:-1] + (D // (2 * s), 2, s))
+        a, b = v[..., 0, :], v[..., 1, :]
+        y = np.stack([a + b, a - b], axis=-2).reshape(shp)
+    return (y * INV_SQRT128).astype(F32)
+
+
+def token_quant(x, rotate=True):
+    """x [S, H, D] fp32 -> (codes [H, Spad, D] int8, scales [H, Spad] fp32), one scale per (token, head)
+    (attn_int8.cu:130-170); rows S..Spad are code 0, scale 0."""
+    s, h, _ = x.shape
+    y = hadamard128(x) if rotate else np.asarray(x, F32)
+    amax = np.abs(y).max(axis=2)
+    sc = (np.maximum(amax, F32(1e-8)) / F32(127.0)).astype(F32)
+    inv = (F32(1.0) / sc).astype(F32)
+    q = np.rint((y * inv[..., None]).astype(F32))
+    assert np.abs(q).max() <= 127
+    sp = spad(s)
+    codes = np.zeros((h, sp, D), np.int8)
+    codes[:, :s] = q.astype(np.int8).transpose(1, 0, 2)
+    scales = np.zeros((h, sp), F32)
+    scales[:, :s] = sc.T
+    return codes, scales
+
+
+def v_int8(v, smooth_v=True):
+    """V [S, H, D] (bf16 bits) -> (codes [S, H, D] int8, vscale [H, D], vmean [H, D]) per channel
+    (attn_int8.cu:97-109, :452-475)."""
+    vf = _as_f32(v)
+    s = vf.shape[0]
+    vm = ((vf.astype(np.float64).sum(axis=0) / s).astype(F32) if smooth_v
+          else np.zeros(vf.shape[1:], F32))
+    rng = np.maximum((vf.max(axis=0) - vm).astype(F32), (vm - vf.min(axis=0)).astype(F32))
+    sc = (np.maximum(rng, F32(1e-6)) / F32(127.0)).astype(F32)
+    codes = np.rint(((vf - vm[None]).astype(F32) / sc[None]).astype(F32))
+    assert np.abs(codes).max() <= 127
+    return codes.astype(np.int8), sc, vm
+
+
+def prepass_u8(q, k, v, rr=None, smooth_k=True, smooth_v=True, rotate=True):
+    """Production pre-pass operands: dict q8, qs [H, Sqpad], k8, ks, ksb [H, Skpad, 2] fp32, kmean [H, D],
+    v8 [S, H, D] int8 codes, vscale, vmean [H, D], vinit [H, Skpad/128, D] int32 = 1.5*2^23 bits + 128 *
+    (sum of the tile's V codes per channel) (the start value of the kernel's P.V accumulator). q [Sq, H, D],
+    k, v [Sk, H, D] bf16 bits; rr = (tab, qw, kw, eps) applies the per-head RMSNorm + RoPE to q and k."""
+    if rr is not None:
+        tab, qw, kw, eps = rr
+        qf = rms_rope(q, tab, qw, eps)
+        kf = rms_rope(k, tab, kw, eps)
+        km = (kf.astype(np.float64).sum(axis=0) / kf.shape[0]).astype(F32)
+    else:
+        qf = _as_f32(q)
+        kf = _as_f32(k)
+        km = kmean(k)
+    if not smooth_k:
+        km = np.zeros_like(km)
+    q8, qs = token_quant(qf, rotate)
+    k8, ks = token_quant((kf - km[None]).astype(F32), rotate)
+    sk = kf.shape[0]
+    ksb = np.stack([ks, (F32(-MAGIC) * ks).astype(F32)], axis=-1)
+    ksb[:, sk:, 1] = -np.inf
+    v8, vs, vm = v_int8(v, smooth_v)
+    skp = spad(sk)
+    vpad = np.zeros((skp, v8.shape[1], D), np.int64)
+    vpad[:sk] = v8
+    vsum = vpad.reshape(skp // TILE, TILE, -1, D).sum(axis=1).transpose(1, 0, 2)     # [H, ntiles, D]
+    vinit = (MAGIC_I + 128 * vsum).astype(np.int32)
+    return dict(q8=q8, qs=qs, k8=k8, ks=ks, ksb=ksb, kmean=km, v8=v8, vscale=vs, vmean=vm, vinit=vinit)
+
+
+def _fma32(a, b, c):
+    """fp32 fma(a, b, c) for fp32 operands: the float64 product is exact, the sum is rounded once more
+    (a double rounding only when the float64 sum is inexact, which these magnitudes make rare)."""
+    return (np.asarray(a, np.float64) * np.asarray(b, np.float64) + np.asarray(c, np.float64)).astype(F32)
+
+
+def attention_u8_from_codes(pp, scale, rows=None, heads=None, sk=None, nbias=0, bias=0.0):
+    """The production main kernel's arithmetic on the pre-pass operands, tile by tile (128 keys): fp32 t, tile
+    max, u8 P = rint(2^x) with 2^x evaluated in float64 from the fp32 argument (the kernels' exp2 is a
+    hardware approximation, so a P next to a .5 boundary may differ by one), exact integer P.V per tile and a
+    float64 fold. Returns fp32 [len(rows), len(heads), D] before the bf16 rounding of the output."""
+    q8, qs, k8, ksb, v8 = pp["q8"], pp["qs"], pp["k8"], pp["ksb"], pp["v8"]
+    sk = v8.shape[0] if sk is None else sk
+    skp = spad(sk)
+    hh = range(q8.shape[0]) if heads is None else heads
+    rows = np.arange(q8.shape[1]) if rows is None else np.asarray(rows)
+    sl2 = F32(F32(scale) * F32(1.4426950408889634))
+    bl2 = F32(bias * 1.4426950408889634)
+    out = np.zeros((len(rows), len(hh), D), F32)
+    for hi, h in enumerate(hh):
+        vp = np.zeros((skp, D), np.int64)
+        vp[:sk] = v8[:, h]
+        # |acc| <= 128 * 127^2 < 2^53: the float64 product is the exact integer
+        acc = q8[h, rows].astype(np.float64) @ k8[h, :skp].astype(np.float64).T
+        with np.errstate(invalid="ignore"):
+            t = _fma32((MAGIC + acc).astype(F32), ksb[h, :skp, 0][None], ksb[h, :skp, 1][None])
+        c = (qs[h, rows] * sl2).astype(F32)[:, None]
+        if nbias > 0:
+            ib = np.where(c > 0, (bl2 / np.where(c > 0, c, 1)).astype(F32), F32(0)).astype(F32)
+            t[:, :nbias] = (t[:, :nbias] + ib).astype(F32)
+        m = np.full((len(rows), 1), -np.inf, F32)
+        l = np.zeros((len(rows), 1))
+        o = np.zeros((len(rows), D))
+        for j0 in range(0, skp, TILE):
+            tt = t[:, j0:j0 + TILE]
+            tm = tt.max(axis=1, keepdims=True)
+            n = np.maximum(m, tm)
+            with np.errstate(invalid="ignore"):
+                a = np.exp2(((m - n) * c).astype(F32).astype(np.float64))
+                ts = np.exp2(((tm - n) * c).astype(F32).astype(np.float64))
+            a = np.nan_to_num(a, nan=0.0)
+            m = n
+            b = _fma32(-tm, c, LOG2_255)
+            with np.errstate(invalid="ignore"):
+                e = np.exp2(_fma32(tt, c, b).astype(np.float64))
+            p = np.clip(np.rint(np.nan_to_num(e, nan=0.0)), 0, 255)
+            l = l * a + ts * p.sum(axis=1, keepdims=True)
+            o = o * a + ts * (p @ vp[j0:j0 + TILE].astype(np.float64))
+        out[:, hi] = (o / l * pp["vscale"][h][None].astype(np.float64) + pp["vmean"][h][None]).astype(F32)
+    return out

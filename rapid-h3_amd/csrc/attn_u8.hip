@@ -1,0 +1,691 @@
+// INT8 flash attention with the reference's production numerics (attn_int8.cu config 80 = attn_fwd8
+// :2250-2511; configs 90/94 run the same math on a persistent schedule, and 1xx add the q/k RMSNorm + RoPE
+// pre-pass), gfx950, head_dim 128, non-causal.
+//
+// Pre-pass (HBM-bound; attn_int8.cu:2568-2644):
+//   stats_kernel   float64 channel sums of K (after the optional RMSNorm + RoPE), per 256-token chunk
+//   vstats_kernel  float64 channel sums, max and min of V, per 256-token chunk
+//   kmean_kernel   kmean = fp32(sum / Sk)                                      (attn_int8.cu:97-109)
+//   vfinal_kernel  vmean = fp32(sum / Sk) (0 without smooth_v),
+//                  vscale = max(max(vmax - vmean, vmean - vmin), 1e-6) / 127  (attn_int8.cu:97-109)
+//   tokq_kernel    per (token, head) row: [RMSNorm + RoPE] -> [- kmean] -> [normalized H128] -> one scale
+//                  sc = max(amax, 1e-8) / 127, q = rint(x * (1 / sc))         (attn_int8.cu:113-170, :298-340);
+//                  for K also the per-key pair (sc, -1.5*2^23 * sc); padded keys get (0, -inf)
+//   vq_kernel      per (128-key tile, head): int8 V codes rint((v - vmean) / vscale) (attn_int8.cu:452-475),
+//                  transposed to [H][128][Skpad] in the key order of the P.V operand, and the tile's P.V
+//                  accumulator start 1.5*2^23 bits + 128 * (sum of its codes) per channel
+// Main kernel: per (256-query block, head) workgroup of 8 waves, 32 queries per wave, 128-key tiles.
+//   S^T = K8 . Q8^T on v_mfma_i32_32x32x32_i8 (keys on rows, queries on lanes), the accumulator starting at
+//   the bits of 1.5*2^23 so that t = fma(float bits, s_j, b_j) is the dequantized score in one instruction;
+//   tile max tm, n = max(m, tm), a = 2^((m - n) c), ts = 2^((tm - n) c); P = rint(2^(fma(t, c, log2 255 - tm c)))
+//   in [0, 255]; row sums of the integer P; O^T += V8^T . P^T on v_mfma_i32_32x32x32_i8 with P - 128 as the
+//   signed operand (the tile's 128 * sum(V codes) is the accumulator start, so the integer result is the
+//   reference's u8 x s8 product exactly); O = fma(ts, acc bits, fma(O, a, -ts * 1.5*2^23)); out =
+//   bf16(fma(O (1 / l), vscale, vmean)). Text bias (attn_cake.cuh:97-99, :210-240): t += bias*log2(e) / c on
+//   keys [0, nbias).
+#include <type_traits>
+
+#include "attn_common.hpp"
+
+namespace rh3 {
+namespace {
+
+using namespace attn;
+
+constexpr int TILE = 128;                 // keys per tile (the tile max of the u8 P)
+constexpr int SIDE = 2048;                // bytes per (head, tile): 128 (s, b) pairs, 128 int32 starts, pad
+constexpr int SIDE_VINIT = 1024;          // byte offset of the accumulator starts inside a side record
+constexpr int MAGIC_I = 0x4B400000;       // bits of 1.5 * 2^23
+constexpr float MAGIC_F = 12582912.0f;
+constexpr float LOG2_255 = 7.99435343685886f;       // attn_int8.cu:24
+constexpr float INV_SQRT128 = 0.08838834764831845f;  // attn_int8.cu:127
+
+// ------------------------------------------------------------------ V statistics
+// grid (nchunk, H), 256 threads = 16 token slots x 16 lanes (8 channels each)
+__global__ void __launch_bounds__(256) vstats_kernel(const uint16_t* __restrict__ v, int64_t v_ss, int64_t v_sh,
+                                                     int64_t S, double* __restrict__ vsum,
+                                                     float* __restrict__ vmax, float* __restrict__ vmin) {
+  __shared__ double red[16][D];
+  __shared__ float rmx[16][D], rmn[16][D];
+  const int h = blockIdx.y, c = blockIdx.x, tid = threadIdx.x;
+  const int slot = tid >> 4, l16 = tid & 15;
+  double acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  float mx[8], mn[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) { mx[e] = -INFINITY; mn[e] = INFINITY; }
+  for (int it = 0; it < CHUNK / 16; ++it) {
+    const int64_t s = static_cast<int64_t>(c) * CHUNK + it * 16 + slot;
+    if (s < S) {
+      float x[8];
+      load8(v + s * v_ss + h * v_sh + 8 * l16, x);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        acc[e] += static_cast<double>(x[e]);
+        mx[e] = fmaxf(mx[e], x[e]);
+        mn[e] = fminf(mn[e], x[e]);
+      }
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    red[slot][8 * l16 + e] = acc[e];
+    rmx[slot][8 * l16 + e] = mx[e];
+    rmn[slot][8 * l16 + e] = mn[e];
+  }
+  __syncthreads();
+  if (tid < D) {
+    double t = 0.0;
+    float a = -INFINITY, b = INFINITY;
+    for (int i = 0; i < 16; ++i) {
+      t += red[i][tid];
+      a = fmaxf(a, rmx[i][tid]);
+      b = fminf(b, rmn[i][tid]);
+    }
+    const int64_t o = (static_cast<int64_t>(h) * gridDim.x + c) * D + tid;
+    vsum[o] = t;
+    vmax[o] = a;
+    vmin[o] = b;
+  }
+}
+
+// grid H, 128 threads
+__global__ void vfinal_kernel(const double* __restrict__ vsum, const float* __restrict__ vmax,
+                              const float* __restrict__ vmin, int nchunk, int64_t S, int smooth_v,
+                              float* __restrict__ vmean, float* __restrict__ vscale) {
+  const int h = blockIdx.x, d = threadIdx.x;
+  double t = 0.0;
+  float a = -INFINITY, b = INFINITY;
+  for (int c = 0; c < nchunk; ++c) {
+    const int64_t o = (static_cast<int64_t>(h) * nchunk + c) * D + d;
+    t += vsum[o];
+    a = fmaxf(a, vmax[o]);
+    b = fminf(b, vmin[o]);
+  }
+  const float vm = smooth_v ? static_cast<float>(t / static_cast<double>(S)) : 0.0f;
+  vmean[h * D + d] = vm;
+  vscale[h * D + d] = fmaxf(fmaxf(a - vm, vm - b), 1e-6f) / 127.0f;
+}
+
+// ------------------------------------------------------------------ per-token Q / K quantizer
+// 256 threads = 16 rows of 16 lanes; row g = blockIdx.x * 16 + tid / 16 is (token g / H, head g % H), heads
+// fastest. grid = Spad * H / 16 (Spad is a multiple of 128).
+__global__ void __launch_bounds__(256) tokq_kernel(const uint16_t* __restrict__ x, int64_t x_ss, int64_t x_sh,
+                                                   int64_t S, int64_t Spad, int64_t H, RR rr,
+                                                   const float* __restrict__ mean, int rotate,
+                                                   int8_t* __restrict__ codes, float* __restrict__ scales,
+                                                   float* __restrict__ side) {
+  const int tid = threadIdx.x, lane = tid & 63, l16 = tid & 15;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 16 + (tid >> 4);
+  const int64_t s = row / H, h = row % H;
+  const int64_t co = (h * Spad + s) * D + 8 * l16;
+  if (s >= S) {  // uniform per 16-lane row: padded rows and keys
+    *reinterpret_cast<uint2*>(codes + co) = make_uint2(0, 0);
+    if (l16 == 0) {
+      scales[h * Spad + s] = 0.0f;
+      if (side) {
+        float* p = side + ((h * (Spad / TILE) + s / TILE) * SIDE) / 4 + 2 * (s % TILE);
+        *reinterpret_cast<float2*>(p) = make_float2(0.0f, -INFINITY);
+      }
+    }
+    return;
+  }
+  float v[8];
+  load8(x + s * x_ss + h * x_sh + 8 * l16, v);
+  if (rr.tab) rms_rope8(v, lane, rr, s);
+  if (mean) {
+    float m[8];
+    const float4 a = *reinterpret_cast<const float4*>(mean + h * D + 8 * l16);
+    const float4 b = *reinterpret_cast<const float4*>(mean + h * D + 8 * l16 + 4);
+    m[0] = a.x; m[1] = a.y; m[2] = a.z; m[3] = a.w; m[4] = b.x; m[5] = b.y; m[6] = b.z; m[7] = b.w;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = v[e] - m[e];
+  }
+  if (rotate) {
+    // Walsh-Hadamard stages at channel strides 1, 2, 4 (inside the lane), then 8, 16, 32, 64 (lane
+    // distances 1, 2, 4, 8): (lo, hi) -> (lo + hi, lo - hi), each rounded to fp32, the reference's order
+#pragma unroll
+    for (int st = 1; st < 8; st <<= 1)
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (!(e & st)) {
+          const float lo = v[e], hi = v[e + st];
+          v[e] = lo + hi;
+          v[e + st] = lo - hi;
+        }
+#pragma unroll
+    for (int m = 1; m < 16; m <<= 1) {
+      const bool hi = l16 & m;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float y = __shfl_xor(v[e], m, 64);
+        v[e] = hi ? y - v[e] : v[e] + y;
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = v[e] * INV_SQRT128;
+  }
+  float amax = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[e]));
+#pragma unroll
+  for (int m = 8; m > 0; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 64));
+  const float sc = fmaxf(amax, 1e-8f) / 127.0f;
+  const float inv = 1.0f / sc;
+  uint32_t b[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) b[e] = static_cast<uint32_t>(static_cast<int32_t>(rintf(v[e] * inv))) & 0xffu;
+  uint2 o;
+  o.x = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
+  o.y = b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24);
+  *reinterpret_cast<uint2*>(codes + co) = o;
+  if (l16 == 0) {
+    scales[h * Spad + s] = sc;
+    if (side) {
+      float* p = side + ((h * (Spad / TILE) + s / TILE) * SIDE) / 4 + 2 * (s % TILE);
+      *reinterpret_cast<float2*>(p) = make_float2(sc, -MAGIC_F * sc);
+    }
+  }
+}
+
+// ------------------------------------------------------------------ V codes, transposed
+// Position p of a 32-key block holds key perm_u8(p): p = 16 g + r <-> key 8 (r / 4) + 4 g + r % 4, the key of
+// register r of lane group g in the S^T accumulator, so that a lane's 16 P bytes are its P.V B operand.
+__device__ __forceinline__ int perm_u8(int p) {
+  const int g = p >> 4, r = p & 15;
+  return 8 * (r >> 2) + 4 * g + (r & 3);
+}
+
+// grid (Skpad / 128, H), 256 threads
+__global__ void __launch_bounds__(256) vq_kernel(const uint16_t* __restrict__ v, int64_t v_ss, int64_t v_sh,
+                                                 int64_t S, int64_t Spad, const float* __restrict__ vmean,
+                                                 const float* __restrict__ vscale, int8_t* __restrict__ vt,
+                                                 int32_t* __restrict__ side) {
+  constexpr int P = D + 16;  // row pitch of the key-major code tile
+  __shared__ int8_t tile[TILE * P];
+  const int h = blockIdx.y, tid = threadIdx.x, l16 = tid & 15;
+  const int64_t s0 = static_cast<int64_t>(blockIdx.x) * TILE;
+  float vm[8], vs[8], iv[8];
+  {
+    const float4 a = *reinterpret_cast<const float4*>(vmean + h * D + 8 * l16);
+    const float4 b = *reinterpret_cast<const float4*>(vmean + h * D + 8 * l16 + 4);
+    const float4 c = *reinterpret_cast<const float4*>(vscale + h * D + 8 * l16);
+    const float4 d = *reinterpret_cast<const float4*>(vscale + h * D + 8 * l16 + 4);
+    vm[0] = a.x; vm[1] = a.y; vm[2] = a.z; vm[3] = a.w; vm[4] = b.x; vm[5] = b.y; vm[6] = b.z; vm[7] = b.w;
+    vs[0] = c.x; vs[1] = c.y; vs[2] = c.z; vs[3] = c.w; vs[4] = d.x; vs[5] = d.y; vs[6] = d.z; vs[7] = d.w;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) iv[e] = 1.0f / vs[e];
+  }
+  // 128 keys x 16 lanes: 8 passes of 16 keys
+  for (int r = tid >> 4; r < TILE; r += 16) {
+    uint2 o = make_uint2(0, 0);
+    if (s0 + r < S) {
+      float x[8];
+      load8(v + (s0 + r) * v_ss + h * v_sh + 8 * l16, x);
+      uint32_t b[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        b[e] = static_cast<uint32_t>(static_cast<int32_t>(rint_div(x[e] - vm[e], vs[e], iv[e]))) & 0xffu;
+      o.x = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
+      o.y = b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24);
+    }
+    *reinterpret_cast<uint2*>(&tile[r * P + 8 * l16]) = o;
+  }
+  __syncthreads();
+  // V^T rows: channel d, 16 positions per store (8 stores of 16 B per row)
+  for (int i = tid; i < D * (TILE / 16); i += 256) {
+    const int d = i >> 3, pc = (i & 7) * 16;  // positions pc..pc+15 of this tile
+    uint32_t w[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int p = pc + e;
+      const int key = (p & ~31) + perm_u8(p & 31);
+      w[e >> 2] |= (static_cast<uint32_t>(static_cast<uint8_t>(tile[key * P + d]))) << (8 * (e & 3));
+    }
+    *reinterpret_cast<uint4*>(vt + (static_cast<int64_t>(h) * D + d) * Spad + s0 + pc) =
+        make_uint4(w[0], w[1], w[2], w[3]);
+  }
+  // accumulator starts: 1.5*2^23 bits + 128 * (sum of the tile's codes of channel d); the pad is zeroed
+  int32_t* rec = side + (static_cast<int64_t>(h) * (Spad / TILE) + blockIdx.x) * (SIDE / 4);
+  if (tid < D) {
+    int sum = 0;
+    for (int k = 0; k < TILE; ++k) sum += static_cast<int8_t>(tile[k * P + tid]);
+    rec[SIDE_VINIT / 4 + tid] = MAGIC_I + 128 * sum;
+  } else {
+    rec[SIDE_VINIT / 4 + tid] = 0;
+  }
+}
+
+// ------------------------------------------------------------------ main kernel
+struct U8Args {
+  const int8_t* q8;    // [H][Sqpad][128]
+  const float* qs;     // [H][Sqpad]
+  const int8_t* k8;    // [H][Skpad][128]
+  const int8_t* side;  // [H][Skpad/128][2048 B]: (s, b) pairs, accumulator starts
+  const int8_t* vt;    // [H][128][Skpad]
+  const float* vscale;  // [H][128]
+  const float* vmean;   // [H][128]
+  uint16_t* out;
+  int64_t o_ss, o_sh;
+  int64_t Sq, Sk, Sqpad, Skpad;
+  float scale_log2;
+  int nbias;
+  float bias_log2;
+};
+
+constexpr int U8_WAVES = 8, U8_NT = U8_WAVES * 64, U8_BQ = U8_WAVES * 32;
+#ifndef U8_LAG_MASK
+#define U8_LAG_MASK 2  // bit i set: waves 4i..4i+3 (one per SIMD) run half a tile behind
+#endif
+
+typedef __attribute__((address_space(3))) const v4i lds_v4i_u8;
+
+// Tile j reads K(j), V^T(j) and its side record from ring slot j % 4 and first loads tile j + 2 into slot
+// (j + 2) % 4, whose last reader ran before the barrier that ended tile j - 1 (see the barrier comment).
+// A slot holds K: 128 keys x 128 B (chunk c of row r at c ^ ((r ^ (r >> 3)) & 7)), V^T: 128 channels x 128
+// keys (the same swizzle), then the 2 KiB side record. Padded keys carry b = -inf, so every tile runs unmasked.
+__global__ void __launch_bounds__(U8_NT, 1) attn_u8_kernel(const U8Args a) {
+  constexpr int KB = TILE * D, VB = D * TILE, SLOT = KB + VB + SIDE;
+  __shared__ __attribute__((aligned(16))) int8_t ring[4 * SLOT];
+  const int h = blockIdx.y, qb = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l32 = lane & 31, g = lane >> 5;
+  const int64_t q = static_cast<int64_t>(qb) * U8_BQ + wave * 32 + l32;
+  const int ntiles = static_cast<int>(a.Skpad / TILE);
+
+  // Q operands are padded to 128 queries; a workgroup's last rows may lie past them (computed on zero codes
+  // with c = 0 and never stored)
+  const bool qin = q < a.Sqpad;
+  v4i qf[4];
+  {
+    const int8_t* qp = a.q8 + (static_cast<int64_t>(h) * a.Sqpad + q) * D + g * 16;
+#pragma unroll
+    for (int ds = 0; ds < 4; ++ds) qf[ds] = qin ? *reinterpret_cast<const v4i*>(qp + ds * 32) : v4i{0, 0, 0, 0};
+  }
+  const float c = (qin ? a.qs[static_cast<int64_t>(h) * a.Sqpad + q] : 0.0f) * a.scale_log2;
+  const float ib = (a.nbias > 0 && c > 0.0f) ? a.bias_log2 / c : 0.0f;
+
+  // global -> LDS copies (lane l of a wave writes LDS base + 16 l; the swizzle is applied on the global side):
+  // K and V^T positions p = 64 w + lane and 512 + 64 w + lane (rows p / 8 and p / 8 + 64, same swizzle) for
+  // every wave, the 128 side chunks by waves 0 and 1. Waves 0-1 issue 5 copies per tile, waves 2-7 issue 4.
+  const int8_t* kbase = a.k8 + static_cast<int64_t>(h) * a.Skpad * D;
+  const int8_t* vbase = a.vt + static_cast<int64_t>(h) * D * a.Skpad;
+  const int8_t* sbase = a.side + static_cast<int64_t>(h) * ntiles * SIDE;
+  const int p0 = wave * 64 + lane, row0 = p0 >> 3, pc0 = p0 & 7, sw0 = (pc0 ^ ((row0 ^ (row0 >> 3)) & 7)) << 4;
+  const int8_t* ksrc = kbase + row0 * D + sw0;
+  const int8_t* vsrc = vbase + static_cast<int64_t>(row0) * a.Skpad + sw0;
+  const int8_t* ssrc = sbase + p0 * 16;  // waves 0, 1 only
+  const int64_t vhalf = 64 * a.Skpad;
+  const uint32_t ring_lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(ring));
+  const uint32_t kdst = ring_lds + wave * 1024, vdst = kdst + KB, sdst = ring_lds + KB + VB + wave * 1024;
+  const bool side_wave = wave < 2;
+  auto load_tile = [&](int j) __attribute__((always_inline)) {
+    const uint32_t so = static_cast<uint32_t>(j & 3) * SLOT;
+    j = min(j, ntiles - 1);  // clamped: every tile issues the same copies; a copy past the end lands unread
+    const int8_t* kp = ksrc + static_cast<int64_t>(j) * KB;
+    const int8_t* vp = vsrc + static_cast<int64_t>(j) * TILE;
+    lds_dma16(kp, kdst + so);
+    lds_dma16(kp + 64 * D, kdst + so + 8192);
+    lds_dma16(vp, vdst + so);
+    lds_dma16(vp + vhalf, vdst + so + 8192);
+    if (side_wave) lds_dma16(ssrc + static_cast<int64_t>(j) * SIDE, sdst + so);
+  };
+
+  // lane parts of the LDS reads inside a slot. K fragment (kb, ds): row 32 kb + l32, chunk 2 ds + g, stored at
+  // chunk ^ ((row ^ (row >> 3)) & 7) = (2 ds ^ 4 (kb & 1)) ^ y, y = (g ^ l32 ^ (l32 >> 3)) & 7: lane offsets
+  // koff[ds ^ 2 (kb & 1)] plus the immediate 4096 kb. V^T fragment (db, kc) likewise, plus KB.
+  uint32_t koff[4];
+  {
+    const int y = (g ^ l32 ^ (l32 >> 3)) & 7;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) koff[i] = ring_lds + l32 * 128 + (((2 * i) ^ y) << 4);
+  }
+  // side record: pairs of keys 32 kb + 8 i + 4 g .. +3 at byte 8 key, accumulator starts of channels
+  // 32 db + 8 i + 4 g .. +3 at SIDE_VINIT + 4 d
+  const uint32_t soff = ring_lds + KB + VB + 32 * g;
+  const uint32_t ioff = ring_lds + KB + VB + SIDE_VINIT + 16 * g;
+
+  v16f o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[i][r] = 0.0f;
+  float mx = -INFINITY, lrow = 0.0f;
+  v16i magic;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) magic[r] = MAGIC_I;
+
+  // S^T of tile j: lane (l32, g) of s[kb] holds query l32 and keys 32 kb + 8 (r / 4) + 4 g + r % 4
+  v16i s[4];
+  auto qk = [&](const int j) __attribute__((always_inline)) {
+    const uint32_t so = static_cast<uint32_t>(j & 3) * SLOT;
+#pragma unroll
+    for (int ds = 0; ds < 4; ++ds)
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        const v4i kf = *reinterpret_cast<lds_v4i_u8*>(
+            static_cast<uintptr_t>(koff[ds ^ (2 * (kb & 1))] + so + kb * 4096));
+        s[kb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf, qf[ds], ds == 0 ? magic : s[kb], 0, 0, 0);
+      }
+  };
+
+  auto softmax_pv = [&](const int j) __attribute__((always_inline)) {
+    const uint32_t so = static_cast<uint32_t>(j & 3) * SLOT;
+    // t = fma(1.5*2^23 + acc, s_key, b_key), in place over the accumulator registers
+    float t[4][16];
+    float tm = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const v4i p01 = *reinterpret_cast<lds_v4i_u8*>(static_cast<uintptr_t>(soff + so + kb * 256 + i * 64));
+        const v4i p23 = *reinterpret_cast<lds_v4i_u8*>(static_cast<uintptr_t>(soff + so + kb * 256 + i * 64 + 16));
+        const float ps[4] = {__int_as_float(p01[0]), __int_as_float(p01[2]), __int_as_float(p23[0]),
+                             __int_as_float(p23[2])};
+        const float pb[4] = {__int_as_float(p01[1]), __int_as_float(p01[3]), __int_as_float(p23[1]),
+                             __int_as_float(p23[3])};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) t[kb][4 * i + e] = fmaf(__int_as_float(s[kb][4 * i + e]), ps[e], pb[e]);
+      }
+    if (a.nbias > j * TILE) {  // text bias on keys [0, nbias) (uniform branch)
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = j * TILE + 32 * kb + 8 * (r >> 2) + 4 * g + (r & 3);
+          if (key < a.nbias) t[kb][r] = t[kb][r] + ib;
+        }
+    }
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; r += 2) tm = fmaxf(tm, fmaxf(t[kb][r], t[kb][r + 1]));
+    {
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_int(tm), __float_as_int(tm), false, false);
+      tm = fmaxf(__int_as_float(sw[0]), __int_as_float(sw[1]));
+    }
+    const float n = fmaxf(mx, tm);
+    const float al = __builtin_amdgcn_exp2f((mx - n) * c);
+    const float ts = __builtin_amdgcn_exp2f((tm - n) * c);
+    mx = n;
+    const float bb = fmaf(-tm, c, LOG2_255);
+    // P - 128 as a signed byte: the low byte of the bits of 2^x + (1.5*2^23 - 128) (round to nearest even).
+    // 2^x stays below 255.5 while the rounding of x = fma(t, c, bb) is under 2^-9, i.e. |tm c| < 2^15; a tile
+    // past that (a wave vote) clamps 2^x to 255 first, as the reference's saturating conversion does.
+    uint32_t pw[4][4];
+    int rs = 0;
+    auto make_p = [&](auto clamp) __attribute__((always_inline)) {
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          uint32_t x[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            float p = __builtin_amdgcn_exp2f(fmaf(t[kb][4 * w + e], c, bb));
+            if constexpr (decltype(clamp)::value) p = fminf(p, 255.0f);
+            x[e] = __float_as_uint(p + (MAGIC_F - 128.0f));
+          }
+          const uint32_t lo = __builtin_amdgcn_perm(x[1], x[0], 0x0c0c0400u);
+          const uint32_t hi = __builtin_amdgcn_perm(x[3], x[2], 0x0c0c0400u);
+          pw[kb][w] = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+          rs = __builtin_amdgcn_sdot4(static_cast<int>(pw[kb][w]), 0x01010101, rs, false);
+        }
+    };
+    if (__builtin_amdgcn_ballot_w64(fabsf(tm * c) >= 32768.0f) != 0) make_p(std::true_type{});
+    else make_p(std::false_type{});
+    // l adds the integer row sum of P (64 keys per lane, each stored as P - 128)
+    lrow = fmaf(ts, static_cast<float>(rs + 128 * 64), lrow * al);
+    const float nm = -ts * MAGIC_F;
+    // O^T[d][query] += V^T . P^T per 32-channel block db, then the fold into fp32
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      v16i acc;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const v4i st = *reinterpret_cast<lds_v4i_u8*>(static_cast<uintptr_t>(ioff + so + db * 128 + i * 32));
+        acc[4 * i + 0] = st[0]; acc[4 * i + 1] = st[1]; acc[4 * i + 2] = st[2]; acc[4 * i + 3] = st[3];
+      }
+#pragma unroll
+      for (int kc = 0; kc < 4; ++kc) {
+        const v4i vf = *reinterpret_cast<lds_v4i_u8*>(
+            static_cast<uintptr_t>(koff[kc ^ (2 * (db & 1))] + so + KB + db * 4096));
+        v4i pf;
+        pf[0] = pw[kc][0]; pf[1] = pw[kc][1]; pf[2] = pw[kc][2]; pf[3] = pw[kc][3];
+        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(vf, pf, acc, 0, 0, 0);
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[db][r] = fmaf(ts, __int_as_float(acc[r]), fmaf(o[db][r], al, nm));
+    }
+  };
+
+  // Barrier B_j ends the use of ring slot j. Leading waves reach B_j after softmax_pv(j), lagging waves after
+  // qk(j), so between B_(j-1) and B_j a lagging wave runs softmax_pv(j-1) while a leading wave runs qk(j). Each
+  // wave issues its copies of tile j+2 right after B_(j-1), into slot (j+2) % 4, whose last reader
+  // (softmax_pv(j-2) of a lagging wave) ran before B_(j-1); before B_j it waits for its copies of tile j+1
+  // (vmcnt(n) leaves the n issued after B_(j-1) in flight), so slot j+1 is complete past B_j.
+  const bool lag = (U8_LAG_MASK >> (wave >> 2)) & 1;
+  auto barrier = [&]() __attribute__((always_inline)) {
+    if (side_wave) asm volatile("s_waitcnt vmcnt(5)" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+
+  load_tile(0);
+  load_tile(1);
+  // vmcnt(0) through the builtin, so the compiler also sees the Q loads above as complete and adds no wait of
+  // its own inside the loop (gfx9 s_waitcnt: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8])
+  __builtin_amdgcn_s_waitcnt(0x0f70);
+  __syncthreads();
+  if (lag) load_tile(2);
+  for (int j = 0; j < ntiles; ++j) {
+    if (!lag) load_tile(j + 2);
+    qk(j);
+    if (lag) {
+      barrier();
+      load_tile(j + 3);
+    }
+    softmax_pv(j);
+    if (!lag) barrier();
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no global->LDS copy outlives the workgroup
+
+  const float lt = lrow + __shfl_xor(lrow, 32, 64);
+  const float il = 1.0f / lt;
+  if (q < a.Sq) {
+    uint16_t* op = a.out + q * a.o_ss + static_cast<int64_t>(h) * a.o_sh;
+    const float* vs = a.vscale + h * D;
+    const float* vm = a.vmean + h * D;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int d = db * 32 + 8 * i + 4 * g;
+        const float4 s4 = *reinterpret_cast<const float4*>(vs + d);
+        const float4 m4 = *reinterpret_cast<const float4*>(vm + d);
+        uint2 w;
+        w.x = pack_bf2(fmaf(o[db][4 * i + 0] * il, s4.x, m4.x), fmaf(o[db][4 * i + 1] * il, s4.y, m4.y));
+        w.y = pack_bf2(fmaf(o[db][4 * i + 2] * il, s4.z, m4.z), fmaf(o[db][4 * i + 3] * il, s4.w, m4.w));
+        *reinterpret_cast<uint2*>(op + d) = w;
+      }
+  }
+}
+
+// ------------------------------------------------------------------ host
+int64_t padk(int64_t s) { return (s + TILE - 1) / TILE * TILE; }
+int64_t up256(int64_t b) { return (b + 255) / 256 * 256; }
+
+struct WorkU8 {
+  int8_t* q8; float* qs; int8_t* k8; float* ks; int8_t* side; int8_t* vt;
+  float* kmean; float* vmean; float* vscale;
+  double* kpart; double* vsum; float* vmax; float* vmin;
+  int64_t bytes;
+};
+
+WorkU8 layout_u8(void* base, int64_t Sq, int64_t Sk, int64_t H) {
+  const int64_t sqp = padk(Sq), skp = padk(Sk), nchunk = (Sk + CHUNK - 1) / CHUNK;
+  char* p = static_cast<char*>(base);
+  int64_t off = 0;
+  WorkU8 w{};
+  auto take = [&](int64_t n) { char* r = p ? p + off : nullptr; off += up256(n); return r; };
+  w.q8 = reinterpret_cast<int8_t*>(take(H * sqp * D));
+  w.qs = reinterpret_cast<float*>(take(H * sqp * 4));
+  w.k8 = reinterpret_cast<int8_t*>(take(H * skp * D));
+  w.ks = reinterpret_cast<float*>(take(H * skp * 4));
+  w.side = reinterpret_cast<int8_t*>(take(H * (skp / TILE) * SIDE));
+  w.vt = reinterpret_cast<int8_t*>(take(H * D * skp));
+  w.kmean = reinterpret_cast<float*>(take(H * D * 4));
+  w.vmean = reinterpret_cast<float*>(take(H * D * 4));
+  w.vscale = reinterpret_cast<float*>(take(H * D * 4));
+  w.kpart = reinterpret_cast<double*>(take(H * nchunk * D * 8));
+  w.vsum = reinterpret_cast<double*>(take(H * nchunk * D * 8));
+  w.vmax = reinterpret_cast<float*>(take(H * nchunk * D * 4));
+  w.vmin = reinterpret_cast<float*>(take(H * nchunk * D * 4));
+  w.bytes = off;
+  return w;
+}
+
+int check_qkv_u8(const char* name, const uint16_t* q, int64_t q_ss, int64_t q_sh, const uint16_t* k, int64_t k_ss,
+                 int64_t k_sh, const uint16_t* v, int64_t v_ss, int64_t v_sh, int64_t Sq, int64_t Sk, int64_t H) {
+  RH3_REQUIRE(Sq > 0 && Sk > 0 && H > 0, "%s: sizes must be positive (Sq=%lld Sk=%lld H=%lld)", name, (long long)Sq,
+              (long long)Sk, (long long)H);
+  RH3_REQUIRE(H < 65536 && (Sq + U8_BQ - 1) / U8_BQ < (1ll << 31), "%s: grid too large", name);
+  RH3_REQUIRE(padk(Sq) * H < (1ll << 31) && padk(Sk) * H < (1ll << 31), "%s: Spad * H must stay below 2^31", name);
+  RH3_REQUIRE(q && k && v, "%s: null q/k/v", name);
+  RH3_REQUIRE(aligned16(q) && aligned16(k) && aligned16(v), "%s: q/k/v must be 16-byte aligned", name);
+  RH3_REQUIRE(q_ss % 8 == 0 && q_sh % 8 == 0 && k_ss % 8 == 0 && k_sh % 8 == 0 && v_ss % 8 == 0 && v_sh % 8 == 0,
+              "%s: token/head strides must be multiples of 8 elements", name);
+  return RH3_OK;
+}
+
+int check_rr_u8(const char* name, const uint16_t* tab, int rot, const uint16_t* qw, const uint16_t* kw) {
+  RH3_REQUIRE(tab && qw && kw, "%s: tab, qw and kw are required", name);
+  RH3_REQUIRE(rot == 96 || rot == 128, "%s: rot_dim %d (96 or 128 supported)", name, rot);
+  RH3_REQUIRE(aligned16(tab) && aligned16(qw) && aligned16(kw), "%s: tab/qw/kw must be 16-byte aligned", name);
+  return RH3_OK;
+}
+
+int prepass_u8(const uint16_t* q, int64_t q_ss, int64_t q_sh, const uint16_t* k, int64_t k_ss, int64_t k_sh,
+               const uint16_t* v, int64_t v_ss, int64_t v_sh, int64_t Sq, int64_t Sk, int64_t H, const RR& rq,
+               const RR& rk, int smooth_k, int smooth_v, int rotate, const WorkU8& w, hipStream_t st) {
+  const int64_t sqp = padk(Sq), skp = padk(Sk);
+  const int nchunk = static_cast<int>((Sk + CHUNK - 1) / CHUNK);
+  const float* mean = nullptr;
+  if (smooth_k) {
+    hipLaunchKernelGGL(stats_kernel, dim3(nchunk, H), dim3(256), 0, st, k, k_ss, k_sh, Sk, rk, w.kpart);
+    hipLaunchKernelGGL(kmean_kernel, dim3(H), dim3(D), 0, st, w.kpart, nchunk, Sk, w.kmean);
+    mean = w.kmean;
+  } else {
+    // a fill kernel, not hipMemsetAsync, so the call stays safe inside a captured HIP graph
+    hipLaunchKernelGGL(zero_kernel, dim3((H * D + 255) / 256), dim3(256), 0, st, w.kmean, H * D);
+  }
+  hipLaunchKernelGGL(vstats_kernel, dim3(nchunk, H), dim3(256), 0, st, v, v_ss, v_sh, Sk, w.vsum, w.vmax, w.vmin);
+  hipLaunchKernelGGL(vfinal_kernel, dim3(H), dim3(D), 0, st, w.vsum, w.vmax, w.vmin, nchunk, Sk, smooth_v, w.vmean,
+                     w.vscale);
+  hipLaunchKernelGGL(tokq_kernel, dim3(sqp * H / 16), dim3(256), 0, st, q, q_ss, q_sh, Sq, sqp, H, rq,
+                     static_cast<const float*>(nullptr), rotate, w.q8, w.qs, static_cast<float*>(nullptr));
+  hipLaunchKernelGGL(tokq_kernel, dim3(skp * H / 16), dim3(256), 0, st, k, k_ss, k_sh, Sk, skp, H, rk, mean, rotate,
+                     w.k8, w.ks, reinterpret_cast<float*>(w.side));
+  hipLaunchKernelGGL(vq_kernel, dim3(skp / TILE, H), dim3(256), 0, st, v, v_ss, v_sh, Sk, skp, w.vmean, w.vscale,
+                     w.vt, reinterpret_cast<int32_t*>(w.side));
+  return launch_status("attention_u8 prepass");
+}
+
+int forward_u8(const WorkU8& w, int64_t Sq, int64_t Sk, int64_t H, float scale, int nbias, double bias, uint16_t* out,
+               int64_t o_ss, int64_t o_sh, hipStream_t st) {
+  U8Args f{w.q8, w.qs, w.k8, w.side, w.vt, w.vscale, w.vmean, out, o_ss, o_sh, Sq, Sk, padk(Sq), padk(Sk),
+           scale * 1.4426950408889634f, nbias, static_cast<float>(bias * 1.4426950408889634)};
+  hipLaunchKernelGGL(attn_u8_kernel, dim3((Sq + U8_BQ - 1) / U8_BQ, H), dim3(U8_NT), 0, st, f);
+  return launch_status("attention_u8 forward");
+}
+
+int check_out_u8(const char* name, const uint16_t* out, int64_t o_ss, int64_t o_sh) {
+  RH3_REQUIRE(out && (reinterpret_cast<uintptr_t>(out) & 7) == 0 && o_ss % 4 == 0 && o_sh % 4 == 0,
+              "%s: out must be 8-byte aligned with strides multiple of 4", name);
+  return RH3_OK;
+}
+
+int check_bias_u8(const char* name, int nbias, int64_t Sk) {
+  RH3_REQUIRE(nbias >= 0 && nbias <= Sk, "%s: nbias %d outside [0, Sk=%lld]", name, nbias, (long long)Sk);
+  return RH3_OK;
+}
+
+}  // namespace
+}  // namespace rh3
+
+using namespace rh3;
+
+extern "C" int64_t rh3_attention_u8_workspace_bytes(int64_t Sq, int64_t Sk, int64_t H) {
+  if (Sq <= 0 || Sk <= 0 || H <= 0) return 0;
+  return layout_u8(nullptr, Sq, Sk, H).bytes;
+}
+
+extern "C" int rh3_attention_u8_prepass(const uint16_t* q, int64_t q_ss, int64_t q_sh, const uint16_t* k,
+                                        int64_t k_ss, int64_t k_sh, const uint16_t* v, int64_t v_ss, int64_t v_sh,
+                                        int64_t Sq, int64_t Sk, int64_t H, const uint16_t* tab, int rot,
+                                        const uint16_t* qw, const uint16_t* kw, float eps, int smooth_k, int smooth_v,
+                                        int rotate, void* workspace, int64_t workspace_bytes, void** ptrs,
+                                        hipStream_t stream) {
+  clear_error();
+  if (int e = check_qkv_u8("attention_u8_prepass", q, q_ss, q_sh, k, k_ss, k_sh, v, v_ss, v_sh, Sq, Sk, H)) return e;
+  RH3_REQUIRE(ptrs, "attention_u8_prepass: ptrs required");
+  const WorkU8 w = layout_u8(workspace, Sq, Sk, H);
+  RH3_REQUIRE(workspace && aligned16(workspace) && workspace_bytes >= w.bytes,
+              "attention_u8_prepass: workspace %lld bytes < required %lld", (long long)workspace_bytes,
+              (long long)w.bytes);
+  RR rq{nullptr, nullptr, 0.f, 0}, rk{nullptr, nullptr, 0.f, 0};
+  if (tab) {
+    if (int e = check_rr_u8("attention_u8_prepass", tab, rot, qw, kw)) return e;
+    RH3_REQUIRE(Sq == Sk, "attention_u8_prepass: RMSNorm+RoPE needs self-attention (Sq == Sk)");
+    rq = RR{tab, qw, eps, rot};
+    rk = RR{tab, kw, eps, rot};
+  }
+  if (int e = prepass_u8(q, q_ss, q_sh, k, k_ss, k_sh, v, v_ss, v_sh, Sq, Sk, H, rq, rk, smooth_k, smooth_v, rotate,
+                         w, stream))
+    return e;
+  ptrs[0] = w.q8; ptrs[1] = w.qs; ptrs[2] = w.k8; ptrs[3] = w.ks; ptrs[4] = w.side; ptrs[5] = w.vt;
+  ptrs[6] = w.kmean; ptrs[7] = w.vscale; ptrs[8] = w.vmean;
+  return RH3_OK;
+}
+
+extern "C" int rh3_attention_u8_forward(int64_t Sq, int64_t Sk, int64_t H, float scale, int nbias, double bias,
+                                        uint16_t* out, int64_t o_ss, int64_t o_sh, void* workspace,
+                                        int64_t workspace_bytes, hipStream_t stream) {
+  clear_error();
+  RH3_REQUIRE(Sq > 0 && Sk > 0 && H > 0, "attention_u8_forward: sizes must be positive");
+  if (int e = check_out_u8("attention_u8_forward", out, o_ss, o_sh)) return e;
+  if (int e = check_bias_u8("attention_u8_forward", nbias, Sk)) return e;
+  const WorkU8 w = layout_u8(workspace, Sq, Sk, H);
+  RH3_REQUIRE(workspace && aligned16(workspace) && workspace_bytes >= w.bytes,
+              "attention_u8_forward: workspace %lld bytes < required %lld", (long long)workspace_bytes,
+              (long long)w.bytes);
+  return forward_u8(w, Sq, Sk, H, scale, nbias, bias, out, o_ss, o_sh, stream);
+}
+
+extern "C" int rh3_int8_attention_u8(const uint16_t* q, int64_t q_ss, int64_t q_sh, const uint16_t* k, int64_t k_ss,
+                                     int64_t k_sh, const uint16_t* v, int64_t v_ss, int64_t v_sh, int64_t Sq,
+                                     int64_t Sk, int64_t H, const uint16_t* tab, int rot, const uint16_t* qw,
+                                     const uint16_t* kw, float eps, float scale, int nbias, double bias, int smooth_k,
+                                     int smooth_v, int rotate, uint16_t* out, int64_t o_ss, int64_t o_sh,
+                                     void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+  clear_error();
+  if (int e = check_qkv_u8("int8_attention_u8", q, q_ss, q_sh, k, k_ss, k_sh, v, v_ss, v_sh, Sq, Sk, H)) return e;
+  if (int e = check_out_u8("int8_attention_u8", out, o_ss, o_sh)) return e;
+  if (int e = check_bias_u8("int8_attention_u8", nbias, Sk)) return e;
+  const WorkU8 w = layout_u8(workspace, Sq, Sk, H);
+  RH3_REQUIRE(workspace && aligned16(workspace) && workspace_bytes >= w.bytes,
+              "int8_attention_u8: workspace %lld bytes < required %lld", (long long)workspace_bytes,
+              (long long)w.bytes);
+  RR rq{nullptr, nullptr, 0.f, 0}, rk{nullptr, nullptr, 0.f, 0};
+  if (tab) {
+    if (int e = check_rr_u8("int8_attention_u8", tab, rot, qw, kw)) return e;
+    RH3_REQUIRE(Sq == Sk, "int8_attention_u8: RMSNorm+RoPE needs self-attention (Sq == Sk)");
+    rq = RR{tab, qw, eps, rot};
+    rk = RR{tab, kw, eps, rot};
+  }
+  if (int e = prepass_u8(q, q_ss, q_sh, k, k_ss, k_sh, v, v_ss, v_sh, Sq, Sk, H, rq, rk, smooth_k, smooth_v, rotate,
+                         w, stream))
+    return e;
+  return forward_u8(w, Sq, Sk, H, scale, nbias, bias, out, o_ss, o_sh, stream);
+}

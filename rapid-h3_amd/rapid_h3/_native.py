@@ -14,6 +14,7 @@ _P = ctypes.c_void_p
 _I = ctypes.c_int64
 _F = ctypes.c_float
 _C = ctypes.c_int
+_D = ctypes.c_double
 
 # name -> argument types, in header order (include/rh3.h)
 SIGNATURES = {
@@ -42,6 +43,12 @@ SIGNATURES = {
     "rh3_attention_forward": ([_I, _I, _I, _F, _P, _I, _I, _P, _I, _P], _C),
     "rh3_attention_prepass": ([_P, _I, _I, _P, _I, _I, _P, _I, _I, _I, _I, _I, _P, _C, _P, _P, _F, _C, _P, _I,
                                ctypes.POINTER(ctypes.c_void_p), _P], _C),
+    "rh3_attention_u8_workspace_bytes": ([_I, _I, _I], ctypes.c_int64),
+    "rh3_int8_attention_u8": ([_P, _I, _I, _P, _I, _I, _P, _I, _I, _I, _I, _I, _P, _C, _P, _P, _F, _F, _C, _D, _C,
+                               _C, _C, _P, _I, _I, _P, _I, _P], _C),
+    "rh3_attention_u8_prepass": ([_P, _I, _I, _P, _I, _I, _P, _I, _I, _I, _I, _I, _P, _C, _P, _P, _F, _C, _C, _C,
+                                  _P, _I, ctypes.POINTER(ctypes.c_void_p), _P], _C),
+    "rh3_attention_u8_forward": ([_I, _I, _I, _F, _C, _D, _P, _I, _I, _P, _I, _P], _C),
 }
 
 RH3_DTYPE_BF16 = 1

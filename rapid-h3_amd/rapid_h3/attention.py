@@ -1,9 +1,18 @@
-"""INT8 flash attention on the HIP kernels (librh3: rh3_int8_attention*, rh3_attention_prepass).
+"""INT8 flash attention on the HIP kernels (librh3: rh3_int8_attention*, rh3_attention_prepass,
+rh3_*attention_u8*).
 
-Signatures follow /root/reference/custom_nodes/rapid_h3/attn_int8.py:30-65. Numerics of this build
-(the BASELINE recipe): Q and K int8 with one scale per (head, 128-token block), K mean-smoothed over
-all tokens, Q.K^T on int8 MFMA, fp32 online softmax, P.V on bf16 MFMA. Arguments the reference uses
-to pick its own variants are accepted for signature parity and mapped as documented per function.
+Signatures follow /root/reference/custom_nodes/rapid_h3/attn_int8.py:30-65. Two numerics, picked by config:
+  * config=None: the per-block recipe of this build's benchmark: Q and K int8 with one scale per (head,
+    128-token block), K mean-smoothed over all tokens, Q.K^T on int8 MFMA, fp32 online softmax, P.V on
+    bf16 MFMA with V in bf16;
+  * config=c (an int): the reference's production numerics, configs 80-99 (attn_int8.cu attn_fwd8 :2250-2511
+    and the cake kernels bit-identical to it): per-token H128-rotated Q/K (rotate), K mean-smoothed
+    (smooth_k), per-channel int8 V (smooth_v), u8 P against each 128-key tile's max, int32 P.V, fp32 fold.
+    1xx / 2xx select the same math (the reference's node-level fused-pre-pass and checked variants).
+    The reference's other kernel configs run this same arithmetic here; the 64-key-tile configs (0, 1, 4-8,
+    10-12, 20-29) and those with the acc * ks dequant (0-12) differ from their own outputs by the tile-max
+    granularity and the rounding of t. Configs 50-69 (FP8 P.V, per-block K) and 3xx (the qkv-GEMM
+    epilogue pre-pass) are not built and raise NotImplementedError.
 """
 import torch
 
@@ -42,13 +51,46 @@ def workspace(sq, sk, h, device):
     return torch.empty(n, device=device, dtype=torch.uint8)
 
 
+def _production(config, name):
+    """True when config selects the reference's production numerics (see the module docstring)."""
+    if config is None:
+        return False
+    c = int(config)
+    if c < 0 or c >= 300:
+        raise NotImplementedError(f"{name}: config {c} is not built for gfx950 (3xx needs the qkv-GEMM epilogue "
+                                  "pre-pass)")
+    if 50 <= c % 100 < 70:
+        raise NotImplementedError(f"{name}: config {c} (FP8 P.V / per-block K) is not built for gfx950")
+    return True
+
+
+def workspace_u8(sq, sk, h, device):
+    n = nat.lib().rh3_attention_u8_workspace_bytes(sq, sk, h)
+    return torch.empty(n, device=device, dtype=torch.uint8)
+
+
+def _attention_u8(name, q, k, v, rr, scale, nbias, bias, smooth_k, smooth_v, rotate, out):
+    sq, h, _ = q.shape
+    sk = k.shape[0]
+    out = _out(q, out)
+    tab, qw, kw, eps, rot = rr if rr is not None else (None, None, None, 0.0, 0)
+    ws = workspace_u8(sq, sk, h, q.device)
+    nat.call("rh3_int8_attention_u8", nat.ptr(q), q.stride(0), q.stride(1), nat.ptr(k), k.stride(0), k.stride(1),
+             nat.ptr(v), v.stride(0), v.stride(1), sq, sk, h, nat.ptr(tab), rot, nat.ptr(qw), nat.ptr(kw),
+             float(eps), float(scale), int(nbias), float(bias), int(bool(smooth_k)), int(bool(smooth_v)),
+             int(bool(rotate)), nat.ptr(out), out.stride(0), out.stride(1), nat.ptr(ws), ws.numel(),
+             nat.stream(q.device))
+    return out
+
+
 def attention(q, k, v, scale=None, config=None, smooth_k=True, smooth_v=True, rotate=True, out=None):
     """q [Sq, H, 128], k / v [Sk, H, 128] bf16 (strided ok, last dim contiguous) -> [Sq, H, 128] bf16.
-    Sq may differ from Sk (cross-attention). config / smooth_v / rotate select reference-only variants
-    (its kernel configs, int8 V, H128 rotation) and are accepted without effect: V stays bf16 and Q/K
-    are not rotated in this recipe."""
+    Sq may differ from Sk (cross-attention). config None: the per-block bf16 P.V recipe (smooth_v and
+    rotate do not apply to it); an int config: the production numerics with smooth_v / rotate."""
     _check_qkv(q, k, v, "attention")
     scale = q.shape[-1] ** -0.5 if scale is None else scale
+    if _production(config, "attention"):
+        return _attention_u8("attention", q, k, v, None, scale, 0, 0.0, smooth_k, smooth_v, rotate, out)
     out = _out(q, out)
     sq, h, _ = q.shape
     sk = k.shape[0]
@@ -84,10 +126,14 @@ def attention_rr(q, k, v, tab, qw, kw, eps, scale=None, config=94, smooth_k=True
                  out=None):
     """attention() on the raw qkv-projection q, k ([S, H, 128] bf16, strided ok) with the per-head
     RMSNorm (qw / kw, eps) and split-half RoPE (tab [1, S, 1, rot/2, 2, 2] bf16) fused into the
-    pre-pass; q, k untouched. Self-attention only."""
+    pre-pass; q, k untouched. Self-attention only. The default config 94 is the production numerics, as in
+    the reference; config=None runs the per-block bf16 P.V recipe."""
     _check_qkv(q, k, v, "attention_rr", self_only=True)
     tab, qw, kw, rot = _check_rr(q, tab, qw, kw)
     scale = q.shape[-1] ** -0.5 if scale is None else scale
+    if _production(config, "attention_rr"):
+        return _attention_u8("attention_rr", q, k, v, (tab, qw, kw, eps, rot), scale, 0, 0.0, smooth_k, smooth_v,
+                             rotate, out)
     out = _out(q, out)
     s, h, _ = q.shape
     ws = workspace(s, s, h, q.device)
@@ -141,4 +187,78 @@ def forward(pp, sq, out=None, scale=None):
     ws = pp["_ws"]
     nat.call("rh3_attention_forward", sq, sk, h, float(scale), nat.ptr(out), out.stride(0), out.stride(1),
              nat.ptr(ws), ws.numel(), nat.stream(out.device))
+    return out
+
+
+def attention_rr_bias(q, k, v, tab, qw, kw, eps, nbias, bias, scale=None, config=94, smooth_k=True, smooth_v=True,
+                      rotate=True, out=None):
+    """attention_rr with the Jenga text-attention bias (attn_int8.py:60-65, attn_int8.cu:2680-2689): every
+    query's logits on keys [0, nbias) get + bias (natural-log units). Config 94 or 90 only (the reference's
+    check, attn_int8.cu:2764); nbias 0 is attention_rr."""
+    nbias = int(nbias)
+    if nbias == 0:
+        return attention_rr(q, k, v, tab, qw, kw, eps, scale=scale, config=config, smooth_k=smooth_k,
+                            smooth_v=smooth_v, rotate=rotate, out=out)
+    if config is None or int(config) % 100 not in (90, 94):
+        raise RuntimeError("text bias: config 94 or 90 only")
+    _check_qkv(q, k, v, "attention_rr_bias", self_only=True)
+    if nbias < 0 or nbias > q.shape[0]:
+        raise RuntimeError("text bias: nbias > S")
+    tab, qw, kw, rot = _check_rr(q, tab, qw, kw)
+    scale = q.shape[-1] ** -0.5 if scale is None else scale
+    return _attention_u8("attention_rr_bias", q, k, v, (tab, qw, kw, eps, rot), scale, nbias, float(bias), smooth_k,
+                         smooth_v, rotate, out)
+
+
+def prepass_u8(q, k, v, tab=None, qw=None, kw=None, eps=1e-5, smooth_k=True, smooth_v=True, rotate=True):
+    """Production pre-pass operands (the reference's int8_prepass, attn_int8.cu:2691-2704, for verification):
+    dict of q8 [H, Sqpad, 128] int8, qs [H, Sqpad] fp32, k8, ks, ksb [H, Skpad, 2] fp32, vinit
+    [H, Skpad/128, 128] int32 (P.V accumulator starts), vt [H, 128, Skpad] int8 (keys permuted within 32-key
+    blocks), kmean, vscale, vmean [H, 128] fp32."""
+    import ctypes
+    _check_qkv(q, k, v, "prepass_u8")
+    sq, h, _ = q.shape
+    sk = k.shape[0]
+    rot = 0
+    if tab is not None:
+        tab, qw, kw, rot = _check_rr(q, tab, qw, kw)
+    ws = workspace_u8(sq, sk, h, q.device)
+    ptrs = (ctypes.c_void_p * 9)()
+    nat.call("rh3_attention_u8_prepass", nat.ptr(q), q.stride(0), q.stride(1), nat.ptr(k), k.stride(0), k.stride(1),
+             nat.ptr(v), v.stride(0), v.stride(1), sq, sk, h, nat.ptr(tab), rot, nat.ptr(qw), nat.ptr(kw),
+             float(eps), int(bool(smooth_k)), int(bool(smooth_v)), int(bool(rotate)), nat.ptr(ws), ws.numel(), ptrs,
+             nat.stream(q.device))
+    sqp, skp = (sq + 127) // 128 * 128, (sk + 127) // 128 * 128
+    base = ws.data_ptr()
+
+    def view(i, nbytes):
+        off = ptrs[i] - base
+        return ws[off:off + nbytes]
+
+    side = view(4, h * (skp // 128) * 2048).view(h, skp // 128, 2048)
+    return {
+        "q8": view(0, h * sqp * D).view(torch.int8).view(h, sqp, D),
+        "qs": view(1, h * sqp * 4).view(torch.float32).view(h, sqp),
+        "k8": view(2, h * skp * D).view(torch.int8).view(h, skp, D),
+        "ks": view(3, h * skp * 4).view(torch.float32).view(h, skp),
+        "ksb": side[:, :, :1024].contiguous().view(torch.float32).view(h, skp, 2),
+        "vinit": side[:, :, 1024:1536].contiguous().view(torch.int32).view(h, skp // 128, D),
+        "vt": view(5, h * D * skp).view(torch.int8).view(h, D, skp),
+        "kmean": view(6, h * D * 4).view(torch.float32).view(h, D),
+        "vscale": view(7, h * D * 4).view(torch.float32).view(h, D),
+        "vmean": view(8, h * D * 4).view(torch.float32).view(h, D),
+        "_ws": ws, "_sk": sk,
+    }
+
+
+def forward_u8(pp, sq, out=None, scale=None, nbias=0, bias=0.0):
+    """The production main kernel alone on operands prepass_u8() produced: out [Sq, H, 128] bf16."""
+    h = pp["q8"].shape[0]
+    sk = pp["_sk"]
+    scale = D ** -0.5 if scale is None else scale
+    if out is None:
+        out = torch.empty((sq, h, D), device=pp["q8"].device, dtype=torch.bfloat16)
+    ws = pp["_ws"]
+    nat.call("rh3_attention_u8_forward", sq, sk, h, float(scale), int(nbias), float(bias), nat.ptr(out),
+             out.stride(0), out.stride(1), nat.ptr(ws), ws.numel(), nat.stream(out.device))
     return out

@@ -156,12 +156,39 @@ def rot_case(rng):
                         wt=wt, wq=wq, ws=ws, wf=wf, wfq=wfq, wfs=wfs, cx=cx, cy=cy)
 
 
-CASES = ("quant", "norm_mod", "heads", "gemm", "attn", "rot")
+def attn_u8_case(rng):
+    """Production attention numerics (configs 80-99): plain, fused RMSNorm + RoPE, without rotation and V
+    smoothing, cross-attention (300 queries over 200 keys) and the text bias. Outputs are stored rounded to
+    bf16, as the kernels return them."""
+    s, h = 300, 2
+    q = bf16(rng.standard_normal((s, h, 128)))
+    k = bf16(rng.standard_normal((s, h, 128)) + 2.0 * rng.standard_normal((1, h, 128)))
+    v = bf16(rng.standard_normal((s, h, 128)) + 0.5 * rng.standard_normal((1, h, 128)))
+    tab = bf16(oa.rope_table(np.arange(s) % 41, rot=96).reshape(s, 48, 2, 2))
+    qw = bf16(1.0 + 0.3 * rng.standard_normal(128))
+    kw = bf16(1.0 + 0.3 * rng.standard_normal(128))
+    sc = 128 ** -0.5
+    keys = ("q8", "qs", "k8", "ks", "ksb", "vinit", "v8", "vscale", "vmean", "kmean")
+    vkeys = ("vinit", "v8", "vscale", "vmean")     # V operands do not depend on the q/k prologue
+    out = {}
+    for pre, kw_ in (("", {}), ("r", {"rr": (tab, qw, kw, 1e-5)}), ("n", {"rotate": False, "smooth_v": False})):
+        pp = oa.prepass_u8(q, k, v, **kw_)
+        out.update({pre + n: pp[n] for n in keys if not (pre == "r" and n in vkeys)})
+        out[pre + "out"] = bf16(oa.attention_u8_from_codes(pp, sc)[:s])
+        if pre == "r":
+            out["bout"] = bf16(oa.attention_u8_from_codes(pp, sc, nbias=77, bias=1.5)[:s])
+    pp = oa.prepass_u8(q, k[:200], v[:200])
+    out.update({"c" + n: pp[n] for n in keys if n not in ("q8", "qs")})
+    out["cout"] = bf16(oa.attention_u8_from_codes(pp, sc)[:s])
+    np.savez_compressed(os.path.join(HERE, "attention_u8.npz"), q=q, k=k, v=v, tab=tab, qw=qw, kw=kw, **out)
+
+
+CASES = ("quant", "norm_mod", "heads", "gemm", "attn", "rot", "attn_u8")
 
 
 def main(which=CASES):
     """Each group draws from its own fixed stream: the first five share seed 0 in this order, rot uses
-    seed 1, so regenerating one file leaves the others' inputs unchanged."""
+    seed 1 and attn_u8 seed 2, so regenerating one file leaves the others' inputs unchanged."""
     if set(which) & set(CASES[:5]):
         rng = np.random.default_rng(0)
         quant_case(rng)
@@ -171,6 +198,8 @@ def main(which=CASES):
         attn_case(rng)
     if "rot" in which:
         rot_case(np.random.default_rng(1))
+    if "attn_u8" in which:
+        attn_u8_case(np.random.default_rng(2))
     for f in sorted(os.listdir(HERE)):
         if f.endswith(".npz"):
             print(f, os.path.getsize(os.path.join(HERE, f)))

@@ -46,6 +46,15 @@ def test_argument_validation_without_gpu():
     st = lib.rh3_int8_attention_rr(fake, 128, 128, fake, 128, 128, fake, 128, 128, 10, 1, fake, 64, fake, fake,
                                    1e-5, 0.1, 1, fake, 128, 128, fake, 1 << 30, None)
     assert st == 1 and "rot_dim" in nat.last_error()
+    st = lib.rh3_int8_attention_u8(fake, 128, 128, fake, 128, 128, fake, 128, 128, 10, 10, 1, None, 0, None, None,
+                                   1e-5, 0.1, 0, 0.0, 1, 1, 1, fake, 128, 128, fake, 16, None)
+    assert st == 1 and "workspace" in nat.last_error()
+    st = lib.rh3_int8_attention_u8(fake, 128, 128, fake, 128, 128, fake, 128, 128, 10, 10, 1, None, 0, None, None,
+                                   1e-5, 0.1, 11, 0.0, 1, 1, 1, fake, 128, 128, fake, 1 << 30, None)
+    assert st == 1 and "nbias" in nat.last_error()
+    st = lib.rh3_attention_u8_prepass(fake, 128, 128, fake, 128, 128, fake, 128, 128, 10, 12, 1, fake, 96, fake,
+                                      fake, 1e-5, 1, 1, 1, fake, 1 << 30, fake, None)
+    assert st == 1 and "self-attention" in nat.last_error()
     with pytest.raises(RuntimeError, match="multiple of 64"):
         nat.call("rh3_gemm_i8", fake, 96, fake, fake, 96, fake, None, fake, 16, 4, 16, 96, None)
 

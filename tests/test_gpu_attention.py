@@ -60,7 +60,7 @@ def test_attention_rr_golden(dev, golden):
     pp = attention.prepass(q, k, v, tab, qw, kw, 1e-5)
     _check_prepass(pp, g["rq8"], g["rqs"], g["rk8"], g["rks"], g["rkmean"], g["v"], s)
     q0, k0 = q.clone(), k.clone()
-    out = attention.attention_rr(q, k, v, tab, qw, kw, 1e-5)
+    out = attention.attention_rr(q, k, v, tab, qw, kw, 1e-5, config=None)     # the per-block recipe
     assert torch.equal(q, q0) and torch.equal(k, k0)        # q, k untouched
     assert rel_l2(bf16_to_f32(to_np(out)), g["rout"]) < TOL
 

@@ -451,3 +451,135 @@ def test_golden_fixtures_regenerate(golden):
     q, s = oq.norm_mod_rot_quant_rows_i8(r["xn"], r["w"], float(r["eps"]), r["idx"], r["shift"], r["scale"])
     assert np.array_equal(q, r["qn"]) and np.array_equal(s, r["sn"])
     assert np.array_equal(oq.convrot(r["cx"]), r["cy"])
+    u = golden("attention_u8")
+    pp = oa.prepass_u8(u["q"], u["k"], u["v"])
+    for n in ("q8", "qs", "k8", "ksb", "vinit", "v8", "vscale", "vmean"):
+        assert np.array_equal(pp[n], u[n]), n
+
+
+# ----------------------------------------------------------------------------- production attention numerics
+def _u8_inputs(seed, s=300, h=2, sk=None):
+    rng = np.random.default_rng(seed)
+    sk = s if sk is None else sk
+    q = f32_to_bf16(rng.standard_normal((s, h, 128)).astype(np.float32))
+    k = f32_to_bf16((rng.standard_normal((sk, h, 128)) + 2 * rng.standard_normal((1, h, 128))).astype(np.float32))
+    v = f32_to_bf16((rng.standard_normal((sk, h, 128)) + 0.5 * rng.standard_normal((1, h, 128))).astype(np.float32))
+    return q, k, v
+
+
+def test_hadamard128_sylvester_closed_form():
+    """Small integers keep every fp32 stage exact, so the staged transform must equal scipy's Sylvester
+    matrix times x, scaled once by fp32(1/sqrt(128)); a real row agrees with the float64 product to fp32
+    rounding and the transform is its own inverse."""
+    from scipy.linalg import hadamard
+    hm = hadamard(128).astype(np.float64)
+    rng = np.random.default_rng(3)
+    xi = rng.integers(-8, 9, size=(5, 128)).astype(np.float32)
+    exp = ((xi.astype(np.float64) @ hm.T) * np.float64(oa.INV_SQRT128)).astype(np.float32)
+    assert np.array_equal(oa.hadamard128(xi), exp)
+    xr = rng.standard_normal((7, 128)).astype(np.float32)
+    y = oa.hadamard128(xr)
+    assert np.allclose(y, xr.astype(np.float64) @ hm.T / np.sqrt(128), rtol=0, atol=2e-6)
+    assert np.allclose(oa.hadamard128(y), xr, rtol=0, atol=4e-6)
+
+
+def test_token_quant_known_answers():
+    """One-hot rows rotate to +-1/sqrt(128) everywhere: every code is +-127 with the signs of Sylvester
+    column i; zero rows give sc = 1e-8/127 and code 0; padded rows are zero; without rotation the codes
+    are torch's round(x / sc) and the absmax code is 127."""
+    from scipy.linalg import hadamard
+    x = np.zeros((3, 2, 128), np.float32)
+    x[0, 0, 5] = 1.0
+    x[2, 1, 77] = -3.0
+    x[1] = np.random.default_rng(4).standard_normal((2, 128)).astype(np.float32)
+    codes, sc = oa.token_quant(x, rotate=True)
+    hm = hadamard(128)
+    assert np.array_equal(codes[0, 0], (127 * hm[:, 5]).astype(np.int8))
+    assert np.array_equal(codes[1, 2], (-127 * hm[:, 77]).astype(np.int8))
+    assert sc[0, 0] == np.float32(oa.INV_SQRT128 / np.float32(127))
+    assert not codes[1, 0].any() and sc[1, 0] == np.float32(np.float32(1e-8) / np.float32(127))
+    assert codes.shape == (2, 128, 128) and not codes[:, 3:].any() and not sc[:, 3:].any()
+    c2, s2 = oa.token_quant(x, rotate=False)
+    t = torch.from_numpy(x[1, 1]).double()
+    ref = (t.float() * (1.0 / torch.tensor(s2[1, 1]))).round()
+    assert np.array_equal(c2[1, 1].astype(np.float32), ref.numpy()) and np.abs(c2[1, 1]).max() == 127
+
+
+def test_v_int8_matches_torch():
+    _, _, v = _u8_inputs(5)
+    codes, sc, vm = oa.v_int8(v)
+    tv = t_bf16(v).float()
+    ref = ((tv - torch.from_numpy(vm)) / torch.from_numpy(sc)).round()
+    assert np.array_equal(codes.astype(np.float32), ref.numpy())
+    assert (np.abs(codes.astype(np.int32)).max(axis=0) == 127).all()     # the extreme deviation is +-127
+    assert np.allclose(vm, bf16_to_f32(v).astype(np.float64).mean(axis=0), atol=1e-6)
+    codes0, sc0, vm0 = oa.v_int8(v, smooth_v=False)
+    assert not vm0.any() and np.allclose(sc0 * 127, np.abs(bf16_to_f32(v)).max(axis=0), rtol=1e-6)
+
+
+def test_prepass_u8_side_records():
+    q, k, v = _u8_inputs(6, s=300)
+    pp = oa.prepass_u8(q, k, v)
+    assert np.array_equal(pp["ksb"][:, :300, 1], (np.float32(-oa.MAGIC) * pp["ks"][:, :300]).astype(np.float32))
+    assert (pp["ksb"][:, 300:, 1] == -np.inf).all() and not pp["ksb"][:, 300:, 0].any()
+    vs = np.zeros((384, 2, 128), np.int64)
+    vs[:300] = pp["v8"]
+    for t in range(3):
+        assert np.array_equal(pp["vinit"][:, t], oa.MAGIC_I + 128 * vs[128 * t:128 * t + 128].sum(axis=0))
+    # K smoothing removes the per-head channel offset before the rotation
+    assert np.allclose(pp["kmean"], bf16_to_f32(k).astype(np.float64).mean(axis=0), atol=1e-6)
+
+
+def test_attention_u8_single_key_and_closed_form():
+    """One key: P = 255, so the output is that key's dequantized V. Three tiles: the online rescaling equals
+    the closed form sum_t 2^((tm_t - M) c) sum_j P_tj v_j / (same with v = 1), P_tj = rint(2^(fma(t, c,
+    log2 255 - tm_t c))) against each tile's own max tm_t; the P.V integer start values are consistent."""
+    q, k, v = _u8_inputs(7, s=1)
+    pp = oa.prepass_u8(q, k, v)
+    out = oa.attention_u8_from_codes(pp, 128 ** -0.5)[:1]
+    dq = (pp["v8"].astype(np.float64) * pp["vscale"][None] + pp["vmean"][None]).astype(np.float32)
+    assert np.allclose(out, dq, rtol=0, atol=1e-6)
+    q, k, v = _u8_inputs(8, s=5, sk=300)
+    pp = oa.prepass_u8(q, k, v)
+    sl2 = np.float32(np.float32(128 ** -0.5) * np.float32(1.4426950408889634))
+    out = oa.attention_u8_from_codes(pp, 128 ** -0.5)[:5]
+    for h in range(2):
+        acc = pp["q8"][h, :5].astype(np.int64) @ pp["k8"][h].astype(np.int64).T
+        t = (((oa.MAGIC + acc) * pp["ksb"][h, :, 0][None].astype(np.float64)
+              + pp["ksb"][h, :, 1][None].astype(np.float64))).astype(np.float32)
+        c = (pp["qs"][h, :5] * sl2).astype(np.float32)[:, None]
+        tms = [t[:, j:j + 128].max(axis=1, keepdims=True) for j in (0, 128, 256)]
+        mm = np.maximum.reduce(tms)
+        num = np.zeros((5, 128))
+        den = np.zeros((5, 1))
+        vq = np.zeros((384, 128))
+        vq[:300] = pp["v8"][:, h]
+        for ti, j in enumerate((0, 128, 256)):
+            bb = (np.float64(-1) * tms[ti] * c + np.float64(oa.LOG2_255)).astype(np.float32)
+            with np.errstate(invalid="ignore"):
+                p = np.nan_to_num(np.rint(np.exp2((t[:, j:j + 128].astype(np.float64) * c + bb).astype(np.float32))))
+            w = np.exp2(((tms[ti] - mm) * c).astype(np.float32).astype(np.float64))
+            num += w * (p @ vq[j:j + 128])
+            den += w * p.sum(axis=1, keepdims=True)
+        ref = num / den * pp["vscale"][h][None] + pp["vmean"][h][None]
+        assert np.allclose(out[:, h], ref, rtol=0, atol=1e-5)
+
+
+def test_attention_u8_accuracy_and_bias():
+    """Within the reference's error band of exact attention (its production configs measure 0.7-1.2 % on
+    real q/k/v); with a text bias the output follows exact attention with + bias on the biased keys."""
+    q, k, v = _u8_inputs(9)
+    ex = oa.attention_exact(q, k, v, 128 ** -0.5)
+    pp = oa.prepass_u8(q, k, v)
+    out = oa.attention_u8_from_codes(pp, 128 ** -0.5)[:300]
+    assert og.rel_l2(out, ex) < 0.03
+    nb, bias = 40, 2.0
+    outb = oa.attention_u8_from_codes(pp, 128 ** -0.5, nbias=nb, bias=bias)[:300]
+    qf, kf, vf = (bf16_to_f32(a).astype(np.float64) for a in (q, k, v))
+    exb = np.zeros_like(ex)
+    for h in range(2):
+        lg = qf[:, h] @ kf[:, h].T * 128 ** -0.5
+        lg[:, :nb] += bias
+        p = np.exp(lg - lg.max(axis=1, keepdims=True))
+        exb[:, h] = (p @ vf[:, h]) / p.sum(axis=1, keepdims=True)
+    assert og.rel_l2(outb, exb) < 0.03 and og.rel_l2(outb, ex) > 0.1
