@@ -142,6 +142,8 @@ __device__ __forceinline__ int vswz(int r, int c) { return r * 256 + ((c ^ (r & 
 // ~168 registers per wave, so a step covers 64 keys. Per wave and step: 8 i8 MFMAs (S^T = K Q^T), 16 bf16
 // MFMAs (O^T += V^T P^T) and ~150 VALU instructions (32 scores: convert, scale, exp2, pack, row sum, max).
 constexpr int FWD_WAVES = 12, FWD_NT = FWD_WAVES * 64, FWD_BQ = FWD_WAVES * 32;
+constexpr int MAGIC_I = 0x4B400000;  // bits of 1.5 * 2^23
+constexpr float MAGIC_F = 12582912.0f;
 constexpr int STEP = 64;  // keys per step
 #ifndef LAG_MASK
 #define LAG_MASK 2  // bit i set: waves 4i..4i+3 (one per SIMD) run half a step behind
@@ -243,6 +245,11 @@ __global__ void __launch_bounds__(FWD_NT, 1) attn_fwd_kernel(const FwdArgs a) {
     for (int r = 0; r < 16; ++r) o[i][r] = 0.0f;
   float mref = -INFINITY, lrow = 0.0f;
   const v2bf ones = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
+  // S^T accumulators start at the bits of 1.5*2^23: the integer register then reads as the float
+  // 1.5*2^23 + acc (|acc| <= 128 * 127^2 < 2^22), so the exponent needs no int -> float conversion
+  v16i magic;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) magic[r] = MAGIC_I;
 
   // S^T[key][query] = K8 . Q8^T of step j: lane (l32, g) of s[kb] holds query l32 and step keys
   // kb*32 + 8*(r/4) + 4*g + r%4
@@ -256,15 +263,11 @@ __global__ void __launch_bounds__(FWD_NT, 1) attn_fwd_kernel(const FwdArgs a) {
     __builtin_amdgcn_s_setprio(1);
 #endif
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) s[kb][r] = 0;
-#pragma unroll
     for (int ds = 0; ds < 4; ++ds) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
         const v4i kf = lds_read16(ka[ds ^ (2 * kb)] + kb * 4096);
-        s[kb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf, qf[ds], s[kb], 0, 0, 0);
+        s[kb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf, qf[ds], ds == 0 ? magic : s[kb], 0, 0, 0);
       }
     }
 #ifdef RH3_SETPRIO
@@ -289,7 +292,7 @@ __global__ void __launch_bounds__(FWD_NT, 1) attn_fwd_kernel(const FwdArgs a) {
         if (!TAIL || kb * 32 + 8 * (r >> 2) + 4 * g + (r & 3) < nvalid) mi = max(mi, s[kb][r]);
     mi = max_halves(mi);
     const float c = qscale * kscale[j >> 1];
-    const float mt = static_cast<float>(mi) * c;
+    const float mt = static_cast<float>(mi - MAGIC_I) * c;
     if (__builtin_amdgcn_ballot_w64(mt > mref + RESCALE_LOG2) != 0) {
       const float mnew = fmaxf(mref, mt);
       const float alpha = __builtin_amdgcn_exp2f(mref - mnew);
@@ -300,15 +303,17 @@ __global__ void __launch_bounds__(FWD_NT, 1) attn_fwd_kernel(const FwdArgs a) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[db][r] = o[db][r] * alpha;
     }
-    const float nb = -mref;
+    // the accumulator holds the bits of 1.5*2^23 + acc, so fma(bits, c, nb) = acc c - mref with the constant
+    // nb = -1.5*2^23 c - mref rounded once: the same rounding error for every score of this query and step
+    const float nb = fmaf(-MAGIC_F, c, -mref);
     // P = 2^(t - mref) in bf16 (P <= 2^8); keys past Sk get P = 0 (lane mask on the packed words)
     uint32_t pk[2][8];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int r = 0; r < 16; r += 2) {
-        const float p0 = __builtin_amdgcn_exp2f(fmaf(static_cast<float>(s[kb][r]), c, nb));
-        const float p1 = __builtin_amdgcn_exp2f(fmaf(static_cast<float>(s[kb][r + 1]), c, nb));
+        const float p0 = __builtin_amdgcn_exp2f(fmaf(__int_as_float(s[kb][r]), c, nb));
+        const float p1 = __builtin_amdgcn_exp2f(fmaf(__int_as_float(s[kb][r + 1]), c, nb));
         pk[kb][r >> 1] = pk_bf16(p0, p1);
       }
     if constexpr (TAIL) {

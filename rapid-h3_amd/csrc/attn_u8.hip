@@ -23,8 +23,6 @@
 //   reference's u8 x s8 product exactly); O = fma(ts, acc bits, fma(O, a, -ts * 1.5*2^23)); out =
 //   bf16(fma(O (1 / l), vscale, vmean)). Text bias (attn_cake.cuh:97-99, :210-240): t += bias*log2(e) / c on
 //   keys [0, nbias).
-#include <type_traits>
-
 #include "attn_common.hpp"
 
 namespace rh3 {
@@ -279,6 +277,13 @@ constexpr int U8_WAVES = 8, U8_NT = U8_WAVES * 64, U8_BQ = U8_WAVES * 32;
 
 typedef __attribute__((address_space(3))) const v4i lds_v4i_u8;
 
+// max of three floats in one instruction (fmaxf chains get a NaN-quieting max inserted per operand)
+__device__ __forceinline__ float max3f(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+
 // Tile j reads K(j), V^T(j) and its side record from ring slot j % 4 and first loads tile j + 2 into slot
 // (j + 2) % 4, whose last reader ran before the barrier that ended tile j - 1 (see the barrier comment).
 // A slot holds K: 128 keys x 128 B (chunk c of row r at c ^ ((r ^ (r >> 3)) & 7)), V^T: 128 channels x 128
@@ -359,12 +364,15 @@ __global__ void __launch_bounds__(U8_NT, 1) attn_u8_kernel(const U8Args a) {
   v16i s[4];
   auto qk = [&](const int j) __attribute__((always_inline)) {
     const uint32_t so = static_cast<uint32_t>(j & 3) * SLOT;
+    uint32_t ka[4];
 #pragma unroll
-    for (int ds = 0; ds < 4; ++ds)
+    for (int i = 0; i < 4; ++i) ka[i] = koff[i] + so;
+    // key-block outer, so that block kb is complete while the MFMAs of block kb + 1 still run
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb) {
-        const v4i kf = *reinterpret_cast<lds_v4i_u8*>(
-            static_cast<uintptr_t>(koff[ds ^ (2 * (kb & 1))] + so + kb * 4096));
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int ds = 0; ds < 4; ++ds) {
+        const v4i kf = *reinterpret_cast<lds_v4i_u8*>(static_cast<uintptr_t>(ka[ds ^ (2 * (kb & 1))] + kb * 4096));
         s[kb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf, qf[ds], ds == 0 ? magic : s[kb], 0, 0, 0);
       }
   };
@@ -399,7 +407,7 @@ __global__ void __launch_bounds__(U8_NT, 1) attn_u8_kernel(const U8Args a) {
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-      for (int r = 0; r < 16; r += 2) tm = fmaxf(tm, fmaxf(t[kb][r], t[kb][r + 1]));
+      for (int r = 0; r < 16; r += 2) tm = max3f(tm, t[kb][r], t[kb][r + 1]);
     {
       const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_int(tm), __float_as_int(tm), false, false);
       tm = fmaxf(__int_as_float(sw[0]), __int_as_float(sw[1]));
@@ -409,34 +417,27 @@ __global__ void __launch_bounds__(U8_NT, 1) attn_u8_kernel(const U8Args a) {
     const float ts = __builtin_amdgcn_exp2f((tm - n) * c);
     mx = n;
     const float bb = fmaf(-tm, c, LOG2_255);
-    // P - 128 as a signed byte: the low byte of the bits of 2^x + (1.5*2^23 - 128) (round to nearest even).
-    // 2^x stays below 255.5 while the rounding of x = fma(t, c, bb) is under 2^-9, i.e. |tm c| < 2^15; a tile
-    // past that (a wave vote) clamps 2^x to 255 first, as the reference's saturating conversion does.
+    // P = sat_u8(rint(2^x)) with v_cvt_pk_u8_f32 (round to nearest even, saturating at 0 and 255: the
+    // reference's cvt.pack.sat.u8 of __float2int_rn), four per word; the signed operand of the MFMA is P - 128
     uint32_t pw[4][4];
-    int rs = 0;
-    auto make_p = [&](auto clamp) __attribute__((always_inline)) {
+    uint32_t rs = 0;
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb)
+    for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          uint32_t x[4];
+      for (int w = 0; w < 4; ++w) {
+        uint32_t x = 0;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            float p = __builtin_amdgcn_exp2f(fmaf(t[kb][4 * w + e], c, bb));
-            if constexpr (decltype(clamp)::value) p = fminf(p, 255.0f);
-            x[e] = __float_as_uint(p + (MAGIC_F - 128.0f));
-          }
-          const uint32_t lo = __builtin_amdgcn_perm(x[1], x[0], 0x0c0c0400u);
-          const uint32_t hi = __builtin_amdgcn_perm(x[3], x[2], 0x0c0c0400u);
-          pw[kb][w] = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
-          rs = __builtin_amdgcn_sdot4(static_cast<int>(pw[kb][w]), 0x01010101, rs, false);
-        }
-    };
-    if (__builtin_amdgcn_ballot_w64(fabsf(tm * c) >= 32768.0f) != 0) make_p(std::true_type{});
-    else make_p(std::false_type{});
-    // l adds the integer row sum of P (64 keys per lane, each stored as P - 128)
-    lrow = fmaf(ts, static_cast<float>(rs + 128 * 64), lrow * al);
+        for (int e = 0; e < 4; ++e)
+          x = __builtin_amdgcn_cvt_pk_u8_f32(__builtin_amdgcn_exp2f(fmaf(t[kb][4 * w + e], c, bb)), e, x);
+        rs = __builtin_amdgcn_udot4(x, 0x01010101u, rs, false);
+        pw[kb][w] = x ^ 0x80808080u;
+      }
+    // l adds the integer row sum of P (the lane's 64 keys)
+    lrow = fmaf(ts, static_cast<float>(rs), lrow * al);
     const float nm = -ts * MAGIC_F;
+    uint32_t va[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) va[i] = koff[i] + so + KB;
     // O^T[d][query] += V^T . P^T per 32-channel block db, then the fold into fp32
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
@@ -448,8 +449,7 @@ __global__ void __launch_bounds__(U8_NT, 1) attn_u8_kernel(const U8Args a) {
       }
 #pragma unroll
       for (int kc = 0; kc < 4; ++kc) {
-        const v4i vf = *reinterpret_cast<lds_v4i_u8*>(
-            static_cast<uintptr_t>(koff[kc ^ (2 * (db & 1))] + so + KB + db * 4096));
+        const v4i vf = *reinterpret_cast<lds_v4i_u8*>(static_cast<uintptr_t>(va[kc ^ (2 * (db & 1))] + db * 4096));
         v4i pf;
         pf[0] = pw[kc][0]; pf[1] = pw[kc][1]; pf[2] = pw[kc][2]; pf[3] = pw[kc][3];
         acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(vf, pf, acc, 0, 0, 0);
