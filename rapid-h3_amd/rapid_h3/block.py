@@ -78,12 +78,16 @@ _QUANTIZERS = {
 }
 
 
-def fused_block(x, w: BlockWeights, mod, segments, rope_tab, idx=None, mark=None, trace=None):
+def fused_block(x, w: BlockWeights, mod, segments, rope_tab, idx=None, mark=None, trace=None, attn_config=None,
+                text_bias=None):
     """One DiT block forward on x [S, hidden] bf16 (modified in place). mod = (shift_msa, scale_msa,
     gate_msa, shift_mlp, scale_mlp, gate_mlp), each [R, hidden]; rope_tab [1, S, 1, rot/2, 2, 2] bf16.
     mark: optional callable, called with each name of PHASES after that phase is enqueued (a timer
     records a stream event there); the kernels and their order are the same with or without it.
-    trace: optional dict that receives every intermediate (a checker's view of each stage)."""
+    trace: optional dict that receives every intermediate (a checker's view of each stage).
+    attn_config: None runs the per-block bf16 P.V attention; an int runs the reference's production
+    numerics with that config (its 1xx presets, __init__.py:274-291). text_bias = (nbias, bias) adds the
+    Jenga text bias (configs 90 / 94 only)."""
     shift_msa, scale_msa, gate_msa, shift_mlp, scale_mlp, gate_mlp = mod
     tick = mark or (lambda name: None)
     keep = trace.__setitem__ if trace is not None else (lambda k, v: None)
@@ -103,9 +107,20 @@ def fused_block(x, w: BlockWeights, mod, segments, rope_tab, idx=None, mark=None
     q, k, v = (t.view(s, h, D) for t in qkv.split(h * D, dim=-1))
     o = torch.empty(1, h, s, D, dtype=x.dtype, device=x.device)
     # attention_rr = pre-pass (RMSNorm + RoPE + stats + INT8) then the main kernel, as two calls
-    pp = _attn.prepass(q, k, v, rope_tab, w.q_norm_w, w.k_norm_w, w.qk_eps)
-    tick("attn_prepass")
-    _attn.forward(pp, s, out=o[0].transpose(0, 1))
+    if attn_config is None:
+        if text_bias is not None:
+            raise RuntimeError("text bias: needs the production attention (attn_config 90 or 94)")
+        pp = _attn.prepass(q, k, v, rope_tab, w.q_norm_w, w.k_norm_w, w.qk_eps)
+        tick("attn_prepass")
+        _attn.forward(pp, s, out=o[0].transpose(0, 1))
+    else:
+        nbias, bias = text_bias if text_bias is not None else (0, 0.0)
+        _attn._production(attn_config, "fused_block")
+        if nbias and int(attn_config) % 100 not in (90, 94):
+            raise RuntimeError("text bias: config 94 or 90 only")
+        pp = _attn.prepass_u8(q, k, v, rope_tab, w.q_norm_w, w.k_norm_w, w.qk_eps)
+        tick("attn_prepass")
+        _attn.forward_u8(pp, s, out=o[0].transpose(0, 1), nbias=nbias, bias=bias)
     keep("o", o)
     tick("attn_main")
     del qkv, pp

@@ -111,3 +111,15 @@ def test_dropin_modules_keep_reference_names():
     assert p.tolist() == [0, 1, 2, 3, 8, 9, 10, 11, 4, 5, 6, 7, 12, 13, 14, 15]
     with pytest.raises(ValueError):
         kernels.quantize_rows(torch.zeros(2, 8, dtype=torch.bfloat16), "bogus")
+
+
+def test_override_host_logic():
+    """RapidH3Int8Attention's host logic (__init__.py:994-1046): segment spans merge, config tags."""
+    from rapid_h3 import override
+    assert override.merge_spans([(0, 10, "text"), (10, 20, "text"), (20, 50, "video"), (50, 60, "text"),
+                                 (60, 60, "text")], {"text"}) == [(0, 20), (50, 60)]
+    o = override.make_override(194)
+    assert o.rapidh3_rmsrope == 94 and o.rapidh3_rrcheck is False
+    assert override.make_override(290).rapidh3_rrcheck is True
+    assert not hasattr(override.make_override(194, exact_rows="text"), "rapidh3_rmsrope")
+    assert not hasattr(override.make_override(94), "rapidh3_rmsrope")

@@ -103,3 +103,32 @@ def test_fused_block_chain(dev, recipe):
         xf[a:b] = og.int8_gemm_gated_residual(T["hq"][a:b], T["hs"][a:b], *oqw["fc2"], _bf(gate_mlp[r]), xf[a:b])
     assert np.array_equal(to_np(out), xf)
     assert out.data_ptr() == x.data_ptr()          # in place, like the reference's residual stream
+
+
+@pytest.mark.parametrize("text_bias", [None, (150, 1.25)])
+def test_fused_block_production_attention(dev, text_bias):
+    """The block chain with the reference's production attention (attn_config 94, its 194 preset): the
+    attention stage matches the oracle's tile-by-tile emulation on the GPU's own qkv (with and without the
+    text bias), and the head-major quantizer that follows consumes it bit-exactly."""
+    from rapid_h3 import gemm, kernels
+    from rapid_h3.block import BlockWeights, fused_block
+    rng = np.random.default_rng(22)
+    x0, ws, norms, mod, tab = _setup(rng)
+    qw = {n: kernels.quantize_weight(to_dev(w, dev), "int8_rowwise") for n, w in ws.items()}
+    perm = gemm.swiglu_perm(2 * FFN, dev)
+    fc1 = kernels.QWeight(qw["fc1"].q[perm].contiguous(), qw["fc1"].scale[:, perm].contiguous())
+    w = BlockWeights(qkv=qw["qkv"], out=qw["out"], fc1_perm=fc1, fc2=qw["fc2"], norm1_w=to_dev(norms["norm1"], dev),
+                     norm2_w=to_dev(norms["norm2"], dev), q_norm_w=to_dev(norms["qn"], dev),
+                     k_norm_w=to_dev(norms["kn"], dev), heads=HEADS, eps=1e-6, qk_eps=1e-6)
+    tr = {}
+    fused_block(to_dev(x0, dev), w, tuple(to_dev(m, dev) for m in mod), SEGMENTS,
+                to_dev(tab, dev).view(1, S, 1, 48, 2, 2), trace=tr, attn_config=94, text_bias=text_bias)
+    T = {k: to_np(v) for k, v in tr.items()}
+    qkv = T["qkv"].reshape(S, 3, HEADS, 128)
+    pp = oa.prepass_u8(qkv[:, 0], qkv[:, 1], qkv[:, 2], rr=(tab, norms["qn"], norms["kn"], 1e-6))
+    nb, bias = text_bias if text_bias is not None else (0, 0.0)
+    att = oa.attention_u8_from_codes(pp, 128 ** -0.5, nbias=nb, bias=bias)[:S]
+    o = T["o"][0]
+    assert rel_l2(bf16_to_f32(o).transpose(1, 0, 2), att) < 2e-3
+    oq_, os_ = oq.heads_quant_rows_i8(o)
+    assert np.array_equal(T["oq"], oq_) and np.array_equal(T["os"], os_)
