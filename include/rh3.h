@@ -140,6 +140,21 @@ int rh3_gemm_i8_gated(const int8_t* xq, int64_t ldx, const float* xs, const int8
 int rh3_gemm_i8_acc(const int8_t* xq, int64_t ldx, const int8_t* wq, int64_t ldw, int32_t* acc, int64_t ldc,
                     int64_t M, int64_t N, int64_t K, hipStream_t stream);
 
+/* The qkv projection with the attention pre-pass partly fused into its epilogue.
+ * replaces cutlass_fp8.int8_gemm_qkv_prep -> run_qkv_prep / VisitorQkvPrep (cutlass_fp8.py:42-46,
+ * fp8_rowwise.cu:108-272, :635-655): out [M, 3*H*128] = bf16((acc * xs) * ws [+ bias]) for the k and v columns
+ * (the q columns are left unwritten); the q columns go, after the per-head RMSNorm + RoPE (tab [M, rot/2, 2, 2],
+ * qw; tab NULL: none), straight to the Q operands of the attention workspace (rh3_attention_workspace_bytes /
+ * rh3_attention_u8_workspace_bytes for Sq = Sk = M): numerics 0 one scale per (head, 128-token block),
+ * numerics 1 per token after the H128 rotation (rotate); the per-256-token channel sums of RMSNorm + RoPE(k)
+ * (kw) and, for numerics 1, the V sums / max / min go to the same workspace. H must be even. Continue with
+ * rh3_attention_prepass_qkv (numerics 0) or rh3_attention_u8_prepass_qkv (numerics 1). */
+int rh3_gemm_i8_qkv(const int8_t* xq, int64_t ldx, const float* xs, const int8_t* wq, int64_t ldw,
+                    const float* ws, const uint16_t* bias, uint16_t* out, int64_t ldo,
+                    int64_t M, int64_t H, int64_t K, const uint16_t* tab, int rot,
+                    const uint16_t* qw, const uint16_t* kw, float eps, int numerics, int rotate,
+                    void* workspace, int64_t workspace_bytes, hipStream_t stream);
+
 /* FP8 (OCP e4m3fn) row-wise GEMM, fp32 accumulate, same epilogue as rh3_gemm_i8.
  * replaces cutlass_fp8.fp8_gemm -> fp8_rowwise_gemm (cutlass_fp8.py:32-34, fp8_rowwise.cu:512-544) */
 int rh3_gemm_fp8(const uint8_t* xq, int64_t ldx, const float* xs, const uint8_t* wq, int64_t ldw,
@@ -190,6 +205,17 @@ int rh3_attention_prepass(const uint16_t* q, int64_t q_ss, int64_t q_sh,
                           void* workspace, int64_t workspace_bytes, void** ptrs /* [6] */,
                           hipStream_t stream);
 
+/* The rest of the pre-pass after rh3_gemm_i8_qkv (numerics 0) on the same workspace: kmean from the GEMM's
+ * K sums, the K quantizer (RMSNorm + RoPE with kw when tab is given) and the V relayout, reading k and v
+ * [S, H, 128] from the GEMM output. ptrs as rh3_attention_prepass. Self-attention (Sq = Sk = S).
+ * replaces attn_int8.attention_pre -> int8_attention_pre's pre-pass (attn_int8.py:50-57,
+ * attn_int8.cu:2595-2610) for the per-block numerics. */
+int rh3_attention_prepass_qkv(const uint16_t* k, int64_t k_ss, int64_t k_sh,
+                              const uint16_t* v, int64_t v_ss, int64_t v_sh, int64_t S, int64_t H,
+                              const uint16_t* tab, int rot, const uint16_t* kw, float eps, int smooth_k,
+                              void* workspace, int64_t workspace_bytes, void** ptrs /* [6] */,
+                              hipStream_t stream);
+
 /* The main kernel alone, on a workspace rh3_attention_prepass filled for the same (Sq, Sk, H): the
  * second half of int8_attention (attn_int8.cu:2749-2849 after prepass()). Lets a caller time or
  * schedule the pre-pass and the main kernel separately. */
@@ -206,6 +232,13 @@ int rh3_attention_forward(int64_t Sq, int64_t Sk, int64_t H, float scale,
  * rint((v - vmean) / vscale). Per 128-key tile: u8 P = rint(255 * 2^(t - tile max)), int32 P.V, fp32
  * fold with the running max; out = bf16(O / l * vscale + vmean).
  * ------------------------------------------------------------------------------------------- */
+
+/* Byte offsets of the arrays inside an attention workspace for (Sq, Sk, H), with the workspace size last.
+ * numerics 0 (rh3_attention_workspace_bytes): q8, qs, k8, ks, kmean, part, vt, bytes (8 values);
+ * numerics 1 (rh3_attention_u8_workspace_bytes): q8, qs, k8, ks, side, vt, kmean, vmean, vscale, kpart, vsum,
+ * vmax, vmin, bytes (14 values). No device access. No counterpart in the reference, whose operands are
+ * separate torch tensors (attn_int8.cu:2568-2644); callers use it to view what rh3_gemm_i8_qkv wrote. */
+int rh3_attention_workspace_layout(int numerics, int64_t Sq, int64_t Sk, int64_t H, int64_t* offsets);
 
 /* Bytes of workspace the production-numerics entry points need for (Sq, Sk, H). */
 int64_t rh3_attention_u8_workspace_bytes(int64_t Sq, int64_t Sk, int64_t H);
@@ -238,6 +271,17 @@ int rh3_attention_u8_prepass(const uint16_t* q, int64_t q_ss, int64_t q_sh,
                              int smooth_k, int smooth_v, int rotate,
                              void* workspace, int64_t workspace_bytes, void** ptrs /* [9] */,
                              hipStream_t stream);
+
+/* The rest of the production pre-pass after rh3_gemm_i8_qkv (numerics 1): kmean and vmean / vscale from the
+ * GEMM's statistics, the per-token K quantizer with its (scale, bias) pairs, the int8 V codes. ptrs as
+ * rh3_attention_u8_prepass. replaces attn_int8.cu int8_attention_pre's pre-pass (:2595-2610: stats_final,
+ * quant_k_rr, quant_v). */
+int rh3_attention_u8_prepass_qkv(const uint16_t* k, int64_t k_ss, int64_t k_sh,
+                                 const uint16_t* v, int64_t v_ss, int64_t v_sh, int64_t S, int64_t H,
+                                 const uint16_t* tab, int rot, const uint16_t* kw, float eps,
+                                 int smooth_k, int smooth_v, int rotate,
+                                 void* workspace, int64_t workspace_bytes, void** ptrs /* [9] */,
+                                 hipStream_t stream);
 
 /* The production main kernel alone, on a workspace rh3_attention_u8_prepass filled for (Sq, Sk, H). */
 int rh3_attention_u8_forward(int64_t Sq, int64_t Sk, int64_t H, float scale, int nbias, double bias,

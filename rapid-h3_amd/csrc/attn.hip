@@ -19,6 +19,7 @@
 #include <type_traits>
 
 #include "attn_common.hpp"
+#include "attn_layout.hpp"
 
 namespace rh3 {
 namespace {
@@ -407,30 +408,9 @@ __global__ void __launch_bounds__(FWD_NT, 1) attn_fwd_kernel(const FwdArgs a) {
 }
 
 // ------------------------------------------------------------------ host
-int64_t pad(int64_t s) { return (s + BLK - 1) / BLK * BLK; }
-int64_t up256(int64_t b) { return (b + 255) / 256 * 256; }
-
-struct Work {
-  int8_t* q8; float* qs; int8_t* k8; float* ks; float* kmean; double* part; uint16_t* vt;
-  int64_t bytes;
-};
-
-Work layout(void* base, int64_t Sq, int64_t Sk, int64_t H) {
-  const int64_t sqp = pad(Sq), skp = pad(Sk), nchunk = (Sk + CHUNK - 1) / CHUNK;
-  char* p = static_cast<char*>(base);
-  int64_t off = 0;
-  Work w{};
-  auto take = [&](int64_t n) { char* r = p ? p + off : nullptr; off += up256(n); return r; };
-  w.q8 = reinterpret_cast<int8_t*>(take(H * sqp * D));
-  w.qs = reinterpret_cast<float*>(take(H * (sqp / BLK) * 4));
-  w.k8 = reinterpret_cast<int8_t*>(take(H * skp * D));
-  w.ks = reinterpret_cast<float*>(take(H * (skp / BLK) * 4));
-  w.kmean = reinterpret_cast<float*>(take(H * D * 4));
-  w.part = reinterpret_cast<double*>(take(H * nchunk * D * 8));
-  w.vt = reinterpret_cast<uint16_t*>(take(H * D * skp * 2));
-  w.bytes = off;
-  return w;
-}
+using attn_ws::pad;
+using attn_ws::Work;
+using attn_ws::layout;
 
 int check_qkv(const char* name, const uint16_t* q, int64_t q_ss, int64_t q_sh, const uint16_t* k, int64_t k_ss,
               int64_t k_sh, const uint16_t* v, int64_t v_ss, int64_t v_sh, int64_t Sq, int64_t Sk, int64_t H) {
@@ -513,6 +493,41 @@ extern "C" int rh3_attention_prepass(const uint16_t* q, int64_t q_ss, int64_t q_
     rk = RR{tab, kw, eps, rot};
   }
   if (int e = prepass(q, q_ss, q_sh, k, k_ss, k_sh, v, v_ss, v_sh, Sq, Sk, H, rq, rk, smooth_k, w, stream)) return e;
+  ptrs[0] = w.q8; ptrs[1] = w.qs; ptrs[2] = w.k8; ptrs[3] = w.ks; ptrs[4] = w.kmean; ptrs[5] = w.vt;
+  return RH3_OK;
+}
+
+extern "C" int rh3_attention_prepass_qkv(const uint16_t* k, int64_t k_ss, int64_t k_sh, const uint16_t* v,
+                                         int64_t v_ss, int64_t v_sh, int64_t S, int64_t H, const uint16_t* tab,
+                                         int rot, const uint16_t* kw, float eps, int smooth_k, void* workspace,
+                                         int64_t workspace_bytes, void** ptrs, hipStream_t stream) {
+  clear_error();
+  if (int e = check_qkv("attention_prepass_qkv", k, k_ss, k_sh, k, k_ss, k_sh, v, v_ss, v_sh, S, S, H)) return e;
+  RH3_REQUIRE(ptrs, "attention_prepass_qkv: ptrs required");
+  const Work w = layout(workspace, S, S, H);
+  RH3_REQUIRE(workspace && aligned16(workspace) && workspace_bytes >= w.bytes,
+              "attention_prepass_qkv: workspace %lld bytes < required %lld", (long long)workspace_bytes,
+              (long long)w.bytes);
+  RR rk{nullptr, nullptr, 0.f, 0};
+  if (tab) {
+    RH3_REQUIRE(kw && (rot == 96 || rot == 128) && aligned16(tab) && aligned16(kw),
+                "attention_prepass_qkv: kw (16-byte aligned) and rot_dim 96 or 128 required with tab");
+    rk = RR{tab, kw, eps, rot};
+  }
+  // q8, qs and the K channel sums come from rh3_gemm_i8_qkv (numerics 0) on this workspace
+  const int64_t skp = pad(S);
+  const int nchunk = static_cast<int>((S + CHUNK - 1) / CHUNK);
+  const float* mean = nullptr;
+  if (smooth_k) {
+    hipLaunchKernelGGL(kmean_kernel, dim3(H), dim3(D), 0, stream, w.part, nchunk, S, w.kmean);
+    mean = w.kmean;
+  } else {
+    hipLaunchKernelGGL(zero_kernel, dim3((H * D + 255) / 256), dim3(256), 0, stream, w.kmean, H * D);
+  }
+  hipLaunchKernelGGL(quant_kernel, dim3(skp / BLK, H), dim3(256), 0, stream, k, k_ss, k_sh, S, skp, rk, mean, w.k8,
+                     w.ks);
+  hipLaunchKernelGGL(vt_kernel, dim3(skp / 64, H), dim3(256), 0, stream, v, v_ss, v_sh, S, skp, w.vt);
+  if (int e = launch_status("attention prepass_qkv")) return e;
   ptrs[0] = w.q8; ptrs[1] = w.qs; ptrs[2] = w.k8; ptrs[3] = w.ks; ptrs[4] = w.kmean; ptrs[5] = w.vt;
   return RH3_OK;
 }

@@ -3,7 +3,7 @@
 // prologue of a 16-lane row, K statistics, and the asynchronous global -> LDS copy.
 #pragma once
 
-#include "rh3_common.hpp"
+#include "attn_prologue.hpp"
 
 namespace rh3 {
 namespace attn {
@@ -16,62 +16,6 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
-
-struct RR {
-  const uint16_t* tab;  // [S][rot/2][2][2] bf16, nullptr = no RMSNorm/RoPE
-  const uint16_t* w;    // [128] bf16
-  float eps;
-  int rot;
-};
-
-__device__ __forceinline__ void load8(const uint16_t* p, float* v) {
-  unpack8(*reinterpret_cast<const uint4*>(p), v);
-}
-
-// Per-head RMSNorm + split-half RoPE of one 128-channel row held by 16 lanes (8 channels each,
-// lane l16 owns channels 8*l16..8*l16+7). Fixed order: per-lane x*x sum over e, then xor 8,4,2,1.
-__device__ __forceinline__ void rms_rope8(float* x, int lane, const RR& rr, int64_t s) {
-  const int l16 = lane & 15;
-  float ss = 0.0f;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) ss = ss + x[e] * x[e];
-  ss = ss + __shfl_xor(ss, 8, 64);
-  ss = ss + __shfl_xor(ss, 4, 64);
-  ss = ss + __shfl_xor(ss, 2, 64);
-  ss = ss + __shfl_xor(ss, 1, 64);
-  const float r = 1.0f / sqrtf(ss / 128.0f + rr.eps);
-  float w[8];
-  load8(rr.w + 8 * l16, w);
-  float y[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) y[e] = round_bf((r * x[e]) * w[e]);
-  const int hr = rr.rot >> 1, step = hr >> 3;  // partner lane distance in 8-channel units
-  const int c0 = 8 * l16;
-  int src = l16;
-  if (c0 < hr) src = l16 + step;
-  else if (c0 < rr.rot) src = l16 - step;
-  float py[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) py[e] = __shfl(y[e], (lane & ~15) + src, 64);
-  if (c0 < rr.rot) {
-    const bool first = c0 < hr;
-    const int i0 = first ? c0 : c0 - hr;  // rotary pair index of channel e is i0 + e
-    const uint16_t* t = rr.tab + (s * hr + i0) * 4;
-    float tv[32];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) load8(t + 8 * q, tv + 8 * q);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float a = first ? y[e] : py[e];
-      const float b = first ? py[e] : y[e];
-      x[e] = first ? round_bf((a * tv[4 * e + 0]) + (b * tv[4 * e + 1]))
-                   : round_bf((a * tv[4 * e + 2]) + (b * tv[4 * e + 3]));
-    }
-  } else {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) x[e] = y[e];
-  }
-}
 
 // ------------------------------------------------------------------ statistics
 // grid (nchunk, H), 256 threads = 16 token slots x 16 lanes

@@ -1,0 +1,75 @@
+// Workspace layouts of the two attention numerics, shared by the attention pre-pass / main kernels and by the
+// qkv GEMM whose epilogue writes the Q operands and the K / V statistics straight into the workspace.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <cstdint>
+
+namespace rh3 {
+namespace attn_ws {
+
+constexpr int D = 128;
+constexpr int BLK = 128;    // token padding, quantization block, production key tile
+constexpr int CHUNK = 256;  // statistics chunk (tokens)
+constexpr int SIDE = 2048;  // production side record bytes per (head, 128-key tile)
+
+__host__ __device__ inline int64_t pad(int64_t s) { return (s + BLK - 1) / BLK * BLK; }
+__host__ __device__ inline int64_t up256(int64_t b) { return (b + 255) / 256 * 256; }
+__host__ __device__ inline int64_t nchunks(int64_t s) { return (s + CHUNK - 1) / CHUNK; }
+
+// per-128-block recipe (bf16 P.V)
+struct Work {
+  int8_t* q8; float* qs; int8_t* k8; float* ks; float* kmean; double* part; uint16_t* vt;
+  int64_t bytes;
+};
+
+inline Work layout(void* base, int64_t Sq, int64_t Sk, int64_t H) {
+  const int64_t sqp = pad(Sq), skp = pad(Sk), nchunk = nchunks(Sk);
+  char* p = static_cast<char*>(base);
+  int64_t off = 0;
+  Work w{};
+  auto take = [&](int64_t n) { char* r = p ? p + off : nullptr; off += up256(n); return r; };
+  w.q8 = reinterpret_cast<int8_t*>(take(H * sqp * D));
+  w.qs = reinterpret_cast<float*>(take(H * (sqp / BLK) * 4));
+  w.k8 = reinterpret_cast<int8_t*>(take(H * skp * D));
+  w.ks = reinterpret_cast<float*>(take(H * (skp / BLK) * 4));
+  w.kmean = reinterpret_cast<float*>(take(H * D * 4));
+  w.part = reinterpret_cast<double*>(take(H * nchunk * D * 8));
+  w.vt = reinterpret_cast<uint16_t*>(take(H * D * skp * 2));
+  w.bytes = off;
+  return w;
+}
+
+// production numerics (u8 P, int8 V)
+struct WorkU8 {
+  int8_t* q8; float* qs; int8_t* k8; float* ks; int8_t* side; int8_t* vt;
+  float* kmean; float* vmean; float* vscale;
+  double* kpart; double* vsum; float* vmax; float* vmin;
+  int64_t bytes;
+};
+
+inline WorkU8 layout_u8(void* base, int64_t Sq, int64_t Sk, int64_t H) {
+  const int64_t sqp = pad(Sq), skp = pad(Sk), nchunk = nchunks(Sk);
+  char* p = static_cast<char*>(base);
+  int64_t off = 0;
+  WorkU8 w{};
+  auto take = [&](int64_t n) { char* r = p ? p + off : nullptr; off += up256(n); return r; };
+  w.q8 = reinterpret_cast<int8_t*>(take(H * sqp * D));
+  w.qs = reinterpret_cast<float*>(take(H * sqp * 4));
+  w.k8 = reinterpret_cast<int8_t*>(take(H * skp * D));
+  w.ks = reinterpret_cast<float*>(take(H * skp * 4));
+  w.side = reinterpret_cast<int8_t*>(take(H * (skp / BLK) * SIDE));
+  w.vt = reinterpret_cast<int8_t*>(take(H * D * skp));
+  w.kmean = reinterpret_cast<float*>(take(H * D * 4));
+  w.vmean = reinterpret_cast<float*>(take(H * D * 4));
+  w.vscale = reinterpret_cast<float*>(take(H * D * 4));
+  w.kpart = reinterpret_cast<double*>(take(H * nchunk * D * 8));
+  w.vsum = reinterpret_cast<double*>(take(H * nchunk * D * 8));
+  w.vmax = reinterpret_cast<float*>(take(H * nchunk * D * 4));
+  w.vmin = reinterpret_cast<float*>(take(H * nchunk * D * 4));
+  w.bytes = off;
+  return w;
+}
+
+}  // namespace attn_ws
+}  // namespace rh3

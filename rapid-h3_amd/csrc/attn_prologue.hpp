@@ -1,0 +1,117 @@
+// Device helpers of the attention pre-pass that other kernels reuse (the qkv GEMM epilogue): one 128-channel
+// row held by 16 lanes (8 channels each, lane l16 owns channels 8*l16..8*l16+7), the per-head RMSNorm + RoPE
+// prologue and the normalized 128-point Walsh-Hadamard transform.
+#pragma once
+
+#include "rh3_common.hpp"
+
+namespace rh3 {
+namespace attn {
+
+struct RR {
+  const uint16_t* tab;  // [S][rot/2][2][2] bf16, nullptr = no RMSNorm/RoPE
+  const uint16_t* w;    // [128] bf16
+  float eps;
+  int rot;
+};
+
+__device__ __forceinline__ void load8(const uint16_t* p, float* v) {
+  unpack8(*reinterpret_cast<const uint4*>(p), v);
+}
+
+// Per-head RMSNorm + split-half RoPE of one 128-channel row held by 16 lanes (8 channels each,
+// lane l16 owns channels 8*l16..8*l16+7). Fixed order: per-lane x*x sum over e, then xor 8,4,2,1.
+__device__ __forceinline__ void rms_rope8(float* x, int lane, const RR& rr, int64_t s) {
+  const int l16 = lane & 15;
+  float ss = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ss = ss + x[e] * x[e];
+  ss = ss + __shfl_xor(ss, 8, 64);
+  ss = ss + __shfl_xor(ss, 4, 64);
+  ss = ss + __shfl_xor(ss, 2, 64);
+  ss = ss + __shfl_xor(ss, 1, 64);
+  const float r = 1.0f / sqrtf(ss / 128.0f + rr.eps);
+  float w[8];
+  load8(rr.w + 8 * l16, w);
+  float y[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) y[e] = round_bf((r * x[e]) * w[e]);
+  const int hr = rr.rot >> 1, step = hr >> 3;  // partner lane distance in 8-channel units
+  const int c0 = 8 * l16;
+  int src = l16;
+  if (c0 < hr) src = l16 + step;
+  else if (c0 < rr.rot) src = l16 - step;
+  float py[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) py[e] = __shfl(y[e], (lane & ~15) + src, 64);
+  if (c0 < rr.rot) {
+    const bool first = c0 < hr;
+    const int i0 = first ? c0 : c0 - hr;  // rotary pair index of channel e is i0 + e
+    const uint16_t* t = rr.tab + (s * hr + i0) * 4;
+    float tv[32];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) load8(t + 8 * q, tv + 8 * q);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float a = first ? y[e] : py[e];
+      const float b = first ? py[e] : y[e];
+      x[e] = first ? round_bf((a * tv[4 * e + 0]) + (b * tv[4 * e + 1]))
+                   : round_bf((a * tv[4 * e + 2]) + (b * tv[4 * e + 3]));
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = y[e];
+  }
+}
+
+// Normalized Walsh-Hadamard transform of the 16-lane row (attn_int8.cu:113-128): stages at channel strides 1,
+// 2, 4 inside the lane, then 8, 16, 32, 64 (lane distances 1, 2, 4, 8), (lo, hi) -> (lo + hi, lo - hi), each
+// rounded to fp32 (the reference's order), then * fp32(1 / sqrt(128)).
+__device__ __forceinline__ void wht128_row(float* v, int l16) {
+#pragma unroll
+  for (int st = 1; st < 8; st <<= 1)
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      if (!(e & st)) {
+        const float lo = v[e], hi = v[e + st];
+        v[e] = lo + hi;
+        v[e + st] = lo - hi;
+      }
+#pragma unroll
+  for (int m = 1; m < 16; m <<= 1) {
+    const bool hi = l16 & m;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float y = __shfl_xor(v[e], m, 64);
+      v[e] = hi ? y - v[e] : v[e] + y;
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = v[e] * 0.08838834764831845f;
+}
+
+// absmax of the 16-lane row (lanes of one row group)
+__device__ __forceinline__ float row_amax16(const float* v) {
+  float amax = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[e]));
+#pragma unroll
+  for (int m = 8; m > 0; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 64));
+  return amax;
+}
+
+// per-token INT8 of the 16-lane row (attn_int8.cu:157-163): sc = max(amax, 1e-8) / 127, q = rint(x * (1 / sc));
+// returns sc, writes the lane's 8 codes
+__device__ __forceinline__ float token_quant_row(const float* v, uint2& codes) {
+  const float sc = fmaxf(row_amax16(v), 1e-8f) / 127.0f;
+  const float inv = 1.0f / sc;
+  uint32_t b[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) b[e] = static_cast<uint32_t>(static_cast<int32_t>(rintf(v[e] * inv))) & 0xffu;
+  codes.x = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
+  codes.y = b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24);
+  return sc;
+}
+
+}  // namespace attn
+}  // namespace rh3

@@ -24,6 +24,7 @@
 //   bf16(fma(O (1 / l), vscale, vmean)). Text bias (attn_cake.cuh:97-99, :210-240): t += bias*log2(e) / c on
 //   keys [0, nbias).
 #include "attn_common.hpp"
+#include "attn_layout.hpp"
 
 namespace rh3 {
 namespace {
@@ -138,43 +139,9 @@ __global__ void __launch_bounds__(256) tokq_kernel(const uint16_t* __restrict__ 
 #pragma unroll
     for (int e = 0; e < 8; ++e) v[e] = v[e] - m[e];
   }
-  if (rotate) {
-    // Walsh-Hadamard stages at channel strides 1, 2, 4 (inside the lane), then 8, 16, 32, 64 (lane
-    // distances 1, 2, 4, 8): (lo, hi) -> (lo + hi, lo - hi), each rounded to fp32, the reference's order
-#pragma unroll
-    for (int st = 1; st < 8; st <<= 1)
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        if (!(e & st)) {
-          const float lo = v[e], hi = v[e + st];
-          v[e] = lo + hi;
-          v[e + st] = lo - hi;
-        }
-#pragma unroll
-    for (int m = 1; m < 16; m <<= 1) {
-      const bool hi = l16 & m;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float y = __shfl_xor(v[e], m, 64);
-        v[e] = hi ? y - v[e] : v[e] + y;
-      }
-    }
-#pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = v[e] * INV_SQRT128;
-  }
-  float amax = 0.0f;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[e]));
-#pragma unroll
-  for (int m = 8; m > 0; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 64));
-  const float sc = fmaxf(amax, 1e-8f) / 127.0f;
-  const float inv = 1.0f / sc;
-  uint32_t b[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) b[e] = static_cast<uint32_t>(static_cast<int32_t>(rintf(v[e] * inv))) & 0xffu;
+  if (rotate) wht128_row(v, l16);
   uint2 o;
-  o.x = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
-  o.y = b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24);
+  const float sc = token_quant_row(v, o);
   *reinterpret_cast<uint2*>(codes + co) = o;
   if (l16 == 0) {
     scales[h * Spad + s] = sc;
@@ -513,38 +480,10 @@ __global__ void __launch_bounds__(U8_NT, 1) attn_u8_kernel(const U8Args a) {
 }
 
 // ------------------------------------------------------------------ host
-int64_t padk(int64_t s) { return (s + TILE - 1) / TILE * TILE; }
-int64_t up256(int64_t b) { return (b + 255) / 256 * 256; }
-
-struct WorkU8 {
-  int8_t* q8; float* qs; int8_t* k8; float* ks; int8_t* side; int8_t* vt;
-  float* kmean; float* vmean; float* vscale;
-  double* kpart; double* vsum; float* vmax; float* vmin;
-  int64_t bytes;
-};
-
-WorkU8 layout_u8(void* base, int64_t Sq, int64_t Sk, int64_t H) {
-  const int64_t sqp = padk(Sq), skp = padk(Sk), nchunk = (Sk + CHUNK - 1) / CHUNK;
-  char* p = static_cast<char*>(base);
-  int64_t off = 0;
-  WorkU8 w{};
-  auto take = [&](int64_t n) { char* r = p ? p + off : nullptr; off += up256(n); return r; };
-  w.q8 = reinterpret_cast<int8_t*>(take(H * sqp * D));
-  w.qs = reinterpret_cast<float*>(take(H * sqp * 4));
-  w.k8 = reinterpret_cast<int8_t*>(take(H * skp * D));
-  w.ks = reinterpret_cast<float*>(take(H * skp * 4));
-  w.side = reinterpret_cast<int8_t*>(take(H * (skp / TILE) * SIDE));
-  w.vt = reinterpret_cast<int8_t*>(take(H * D * skp));
-  w.kmean = reinterpret_cast<float*>(take(H * D * 4));
-  w.vmean = reinterpret_cast<float*>(take(H * D * 4));
-  w.vscale = reinterpret_cast<float*>(take(H * D * 4));
-  w.kpart = reinterpret_cast<double*>(take(H * nchunk * D * 8));
-  w.vsum = reinterpret_cast<double*>(take(H * nchunk * D * 8));
-  w.vmax = reinterpret_cast<float*>(take(H * nchunk * D * 4));
-  w.vmin = reinterpret_cast<float*>(take(H * nchunk * D * 4));
-  w.bytes = off;
-  return w;
-}
+static_assert(TILE == attn_ws::BLK && SIDE == attn_ws::SIDE, "workspace layout constants");
+using attn_ws::WorkU8;
+using attn_ws::layout_u8;
+inline int64_t padk(int64_t s) { return attn_ws::pad(s); }
 
 int check_qkv_u8(const char* name, const uint16_t* q, int64_t q_ss, int64_t q_sh, const uint16_t* k, int64_t k_ss,
                  int64_t k_sh, const uint16_t* v, int64_t v_ss, int64_t v_sh, int64_t Sq, int64_t Sk, int64_t H) {
@@ -616,6 +555,27 @@ int check_bias_u8(const char* name, int nbias, int64_t Sk) {
 
 using namespace rh3;
 
+extern "C" int rh3_attention_workspace_layout(int numerics, int64_t Sq, int64_t Sk, int64_t H, int64_t* offsets) {
+  clear_error();
+  RH3_REQUIRE(Sq > 0 && Sk > 0 && H > 0 && offsets, "attention_workspace_layout: sizes must be positive, offsets set");
+  char* const b = reinterpret_cast<char*>(static_cast<uintptr_t>(256));  // any aligned base; offsets relative
+  auto off = [&](const void* p) { return static_cast<int64_t>(static_cast<const char*>(p) - b); };
+  if (numerics == 0) {
+    const attn_ws::Work w = attn_ws::layout(b, Sq, Sk, H);
+    const void* ps[7] = {w.q8, w.qs, w.k8, w.ks, w.kmean, w.part, w.vt};
+    for (int i = 0; i < 7; ++i) offsets[i] = off(ps[i]);
+    offsets[7] = w.bytes;
+    return RH3_OK;
+  }
+  RH3_REQUIRE(numerics == 1, "attention_workspace_layout: numerics %d (0 per-block, 1 production)", numerics);
+  const WorkU8 w = layout_u8(b, Sq, Sk, H);
+  const void* ps[13] = {w.q8, w.qs, w.k8, w.ks, w.side, w.vt, w.kmean, w.vmean, w.vscale,
+                        w.kpart, w.vsum, w.vmax, w.vmin};
+  for (int i = 0; i < 13; ++i) offsets[i] = off(ps[i]);
+  offsets[13] = w.bytes;
+  return RH3_OK;
+}
+
 extern "C" int64_t rh3_attention_u8_workspace_bytes(int64_t Sq, int64_t Sk, int64_t H) {
   if (Sq <= 0 || Sk <= 0 || H <= 0) return 0;
   return layout_u8(nullptr, Sq, Sk, H).bytes;
@@ -644,6 +604,46 @@ extern "C" int rh3_attention_u8_prepass(const uint16_t* q, int64_t q_ss, int64_t
   if (int e = prepass_u8(q, q_ss, q_sh, k, k_ss, k_sh, v, v_ss, v_sh, Sq, Sk, H, rq, rk, smooth_k, smooth_v, rotate,
                          w, stream))
     return e;
+  ptrs[0] = w.q8; ptrs[1] = w.qs; ptrs[2] = w.k8; ptrs[3] = w.ks; ptrs[4] = w.side; ptrs[5] = w.vt;
+  ptrs[6] = w.kmean; ptrs[7] = w.vscale; ptrs[8] = w.vmean;
+  return RH3_OK;
+}
+
+extern "C" int rh3_attention_u8_prepass_qkv(const uint16_t* k, int64_t k_ss, int64_t k_sh, const uint16_t* v,
+                                            int64_t v_ss, int64_t v_sh, int64_t S, int64_t H, const uint16_t* tab,
+                                            int rot, const uint16_t* kw, float eps, int smooth_k, int smooth_v,
+                                            int rotate, void* workspace, int64_t workspace_bytes, void** ptrs,
+                                            hipStream_t stream) {
+  clear_error();
+  if (int e = check_qkv_u8("attention_u8_prepass_qkv", k, k_ss, k_sh, k, k_ss, k_sh, v, v_ss, v_sh, S, S, H)) return e;
+  RH3_REQUIRE(ptrs, "attention_u8_prepass_qkv: ptrs required");
+  const WorkU8 w = layout_u8(workspace, S, S, H);
+  RH3_REQUIRE(workspace && aligned16(workspace) && workspace_bytes >= w.bytes,
+              "attention_u8_prepass_qkv: workspace %lld bytes < required %lld", (long long)workspace_bytes,
+              (long long)w.bytes);
+  RR rk{nullptr, nullptr, 0.f, 0};
+  if (tab) {
+    RH3_REQUIRE(kw && (rot == 96 || rot == 128) && aligned16(tab) && aligned16(kw),
+                "attention_u8_prepass_qkv: kw (16-byte aligned) and rot_dim 96 or 128 required with tab");
+    rk = RR{tab, kw, eps, rot};
+  }
+  // q8, qs and the K / V channel statistics come from rh3_gemm_i8_qkv (numerics 1) on this workspace
+  const int64_t skp = padk(S);
+  const int nchunk = static_cast<int>((S + CHUNK - 1) / CHUNK);
+  const float* mean = nullptr;
+  if (smooth_k) {
+    hipLaunchKernelGGL(kmean_kernel, dim3(H), dim3(D), 0, stream, w.kpart, nchunk, S, w.kmean);
+    mean = w.kmean;
+  } else {
+    hipLaunchKernelGGL(zero_kernel, dim3((H * D + 255) / 256), dim3(256), 0, stream, w.kmean, H * D);
+  }
+  hipLaunchKernelGGL(vfinal_kernel, dim3(H), dim3(D), 0, stream, w.vsum, w.vmax, w.vmin, nchunk, S, smooth_v, w.vmean,
+                     w.vscale);
+  hipLaunchKernelGGL(tokq_kernel, dim3(skp * H / 16), dim3(256), 0, stream, k, k_ss, k_sh, S, skp, H, rk, mean, rotate,
+                     w.k8, w.ks, reinterpret_cast<float*>(w.side));
+  hipLaunchKernelGGL(vq_kernel, dim3(skp / TILE, H), dim3(256), 0, stream, v, v_ss, v_sh, S, skp, w.vmean, w.vscale,
+                     w.vt, reinterpret_cast<int32_t*>(w.side));
+  if (int e = launch_status("attention_u8 prepass_qkv")) return e;
   ptrs[0] = w.q8; ptrs[1] = w.qs; ptrs[2] = w.k8; ptrs[3] = w.ks; ptrs[4] = w.side; ptrs[5] = w.vt;
   ptrs[6] = w.kmean; ptrs[7] = w.vscale; ptrs[8] = w.vmean;
   return RH3_OK;

@@ -6,6 +6,12 @@
 //   EPI_SWIGLU  g, u = bf16(y) over the swiglu_perm interleave; h = bf16((g * sigmoid(g)) * u) at n / 2
 //   EPI_GATED   resid = bf16(fma(bf16(y), gate[n], resid))     (in place)
 //   EPI_ACC     raw int32 accumulators (verification)
+//   EPI_QKV     the qkv projection with the attention pre-pass partly fused (the reference's config 3xx,
+//               fp8_rowwise.cu:108-272): the 256x256 tile (two heads of q, k or v, 256 tokens = one statistics
+//               chunk) is staged whole in LDS; q: per-head RMSNorm + RoPE and the Q quantization of the
+//               attention numerics (per 128-token block, or per token after the H128 rotation), the bf16 q is
+//               not written; k: written, plus the float64 channel sums of RMSNorm + RoPE(k); v: written, plus
+//               (production numerics) float64 channel sums, max and min
 //
 // Schedule: 256x256 output tile per workgroup, 8 waves (2 per SIMD, so each hides the other's LDS and
 // barrier latency) in a 2x4 grid, 128x64 per wave held in registers (int8: 2x4 v_mfma_i32_32x32x32_i8
@@ -20,6 +26,8 @@
 // workgroup ids land on different XCDs, so the tile order is remapped to give every XCD a
 // contiguous run of tiles that walk N fastest (one activation panel stays in that XCD's L2).
 #include "rh3_common.hpp"
+#include "attn_layout.hpp"
+#include "attn_prologue.hpp"
 
 namespace rh3 {
 namespace {
@@ -29,7 +37,7 @@ typedef int v8i __attribute__((ext_vector_type(8)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 
-enum Epi { EPI_PLAIN = 0, EPI_SWIGLU = 1, EPI_GATED = 2, EPI_ACC = 3 };
+enum Epi { EPI_PLAIN = 0, EPI_SWIGLU = 1, EPI_GATED = 2, EPI_ACC = 3, EPI_QKV = 4 };
 
 constexpr int BM = 256, BN = 256, BK = 64;
 // NW waves in a 2 (m) x NW/2 (n) grid, 128 x (512 / NW) outputs per wave. NW = 8: 2 waves per SIMD hide
@@ -47,6 +55,20 @@ struct Cfg {
 constexpr int GROUP_M = RH3_GEMM_GROUP_M;
 constexpr int TILE_BYTES = BM * BK;  // per operand per stage (BM == BN)
 
+// EPI_QKV operands (pointers into the attention workspace of the chosen numerics)
+struct QkvPrep {
+  int64_t H, Spad;           // heads, tokens padded to 128
+  int mode;                  // 0: one Q scale per (head, 128-token block); 1: per token after the H128 rotation
+  int rotate;
+  attn::RR rq, rk;           // q / k RMSNorm + RoPE (tab null: none)
+  int8_t* q8;                // [H][Spad][128]
+  float* qs;                 // mode 0: [H][Spad/128]; mode 1: [H][Spad]
+  double* kpart;             // [H][nchunk][128] channel sums of the (RMSNorm + RoPE'd) k
+  double* vsum;              // mode 1: [H][nchunk][128]
+  float* vmax;
+  float* vmin;
+};
+
 struct GemmArgs {
   const int8_t* x;  // [M, K] int8 or e4m3 codes
   int64_t ldx;
@@ -60,6 +82,7 @@ struct GemmArgs {
   int64_t ldo;
   int64_t M, N, K;
   int tiles_m, tiles_n;
+  QkvPrep qp;
 };
 
 // 16-byte chunk c (0..3) of LDS row r: rows r, r+1 share a 128-byte line; the XOR keeps 16
@@ -277,6 +300,198 @@ __global__ void __launch_bounds__(RH3_GEMM_NW * 64, RH3_GEMM_NW / 4) gemm_kernel
           }
         }
     }
+  } else if constexpr (EPI == EPI_QKV) {
+    static_assert(NT == 512 && BM == 256 && BN == 256 && 2 * TILE_BYTES == 64 * 512, "tile staging layout");
+    // the whole 256 x 256 bf16 tile in the idle ring: row r in stage r / 64 at (r % 64) * 512, 16-byte chunk c
+    // (columns 8c..8c+7) at c ^ (r % 32), so 32 rows of one chunk and one row's 32 chunks are both spread
+    // over the banks
+    __shared__ float qred[64];  // per-group block absmax (mode 0), then the block scales
+    auto tp = [&](int r, int c) __attribute__((always_inline)) -> int8_t* {
+      const int sidx = r >> 6;
+      int8_t* const stg = sidx == 0 ? st0 : sidx == 1 ? st1 : sidx == 2 ? st2 : st3;
+      return stg + (r & 63) * 512 + ((c ^ (r & 31)) << 4);
+    };
+    __syncthreads();  // every wave is done reading the ring
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) {
+      const int row = wm * WM + j * 32 + l32;
+      const int64_t m = m0 + row;
+      const float xsm = m < a.M ? a.xs[m] : 0.0f;
+#pragma unroll
+      for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int rq = 0; rq < 4; ++rq) {
+          const int col = wn * WN + i * 32 + 8 * rq + 4 * g;
+          const int64_t n = n0 + col;
+          const float4 wsn = *reinterpret_cast<const float4*>(a.ws + n);
+          float y[4] = {(MM::val(acc[i][j], 4 * rq + 0) * xsm) * wsn.x, (MM::val(acc[i][j], 4 * rq + 1) * xsm) * wsn.y,
+                        (MM::val(acc[i][j], 4 * rq + 2) * xsm) * wsn.z, (MM::val(acc[i][j], 4 * rq + 3) * xsm) * wsn.w};
+          if (a.bias) {
+            const uint2 bb = *reinterpret_cast<const uint2*>(a.bias + n);
+            y[0] = y[0] + __uint_as_float(bb.x << 16);
+            y[1] = y[1] + __uint_as_float(bb.x & 0xffff0000u);
+            y[2] = y[2] + __uint_as_float(bb.y << 16);
+            y[3] = y[3] + __uint_as_float(bb.y & 0xffff0000u);
+          }
+          uint2 o;
+          o.x = pack_bf2(y[0], y[1]);
+          o.y = pack_bf2(y[2], y[3]);
+          *reinterpret_cast<uint2*>(tp(row, col >> 3) + 8 * g) = o;
+        }
+    }
+    __syncthreads();
+    const QkvPrep& qp = a.qp;
+    const int64_t hd = qp.H * 128;
+    const int role = static_cast<int>(n0 / hd);    // 0 q, 1 k, 2 v (a 256-column tile never straddles two)
+    const int64_t hb = (n0 % hd) / 128;            // first of the tile's two heads
+    const int grp = tid >> 4, l16 = tid & 15, hh = grp & 1;
+    const int64_t nrows = a.M - m0 < 256 ? a.M - m0 : 256;
+    const int64_t nchunk = attn_ws::nchunks(a.M);
+    // 16-lane row groups: group grp handles head hb + (grp & 1) and rows 16 it + grp / 2, it = 0..15
+    auto load_row = [&](int row, float* v) __attribute__((always_inline)) {
+      unpack8(*reinterpret_cast<const uint4*>(tp(row, hh * 16 + l16)), v);
+    };
+    if (role == 0 && qp.mode == 1) {
+      for (int it = 0; it < 16; ++it) {
+        const int row = it * 16 + (grp >> 1);
+        const int64_t s = m0 + row, h = hb + hh;
+        if (s >= qp.Spad) continue;  // uniform per row group
+        int8_t* co = qp.q8 + (h * qp.Spad + s) * 128 + 8 * l16;
+        if (s >= a.M) {
+          *reinterpret_cast<uint2*>(co) = make_uint2(0, 0);
+          if (l16 == 0) qp.qs[h * qp.Spad + s] = 0.0f;
+          continue;
+        }
+        float v[8];
+        load_row(row, v);
+        if (qp.rq.tab) attn::rms_rope8(v, lane, qp.rq, s);
+        if (qp.rotate) attn::wht128_row(v, l16);
+        uint2 codes;
+        const float sc = attn::token_quant_row(v, codes);
+        *reinterpret_cast<uint2*>(co) = codes;
+        if (l16 == 0) qp.qs[h * qp.Spad + s] = sc;
+      }
+    } else if (role == 0) {
+      // one scale per (head, 128-token block): absmax pass, block reduction, then the codes from the same
+      // values recomputed (rows past M count as 0, as in the pre-pass quantizer)
+      float bmax[2] = {0.0f, 0.0f};
+      for (int it = 0; it < 16; ++it) {
+        const int row = it * 16 + (grp >> 1);
+        const int64_t s = m0 + row;
+        if (s >= a.M) continue;
+        float v[8];
+        load_row(row, v);
+        if (qp.rq.tab) attn::rms_rope8(v, lane, qp.rq, s);
+        float am = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) am = fmaxf(am, fabsf(v[e]));
+        bmax[it >> 3] = fmaxf(bmax[it >> 3], am);
+      }
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+#pragma unroll
+        for (int m = 8; m > 0; m >>= 1) bmax[b] = fmaxf(bmax[b], __shfl_xor(bmax[b], m, 64));
+      }
+      if (l16 == 0) {
+        qred[2 * grp] = bmax[0];
+        qred[2 * grp + 1] = bmax[1];
+      }
+      __syncthreads();
+      float sc[2], inv[2];
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        float am = 0.0f;
+        for (int gg = hh; gg < 32; gg += 2) am = fmaxf(am, qred[2 * gg + b]);
+        sc[b] = fmaxf(am, 1e-8f) / 127.0f;
+        inv[b] = 1.0f / sc[b];
+      }
+      if (tid < 4) {  // scale of (head hb + th, block b), reduced over that head's row groups
+        const int th = tid & 1, b = tid >> 1;
+        float am = 0.0f;
+        for (int gg = th; gg < 32; gg += 2) am = fmaxf(am, qred[2 * gg + b]);
+        const int64_t blk = m0 / 128 + b;
+        if (blk * 128 < qp.Spad) qp.qs[(hb + th) * (qp.Spad / 128) + blk] = fmaxf(am, 1e-8f) / 127.0f;
+      }
+      for (int it = 0; it < 16; ++it) {
+        const int row = it * 16 + (grp >> 1), b = it >> 3;
+        const int64_t s = m0 + row, h = hb + hh;
+        if (s >= qp.Spad) continue;
+        float v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        if (s < a.M) {
+          load_row(row, v);
+          if (qp.rq.tab) attn::rms_rope8(v, lane, qp.rq, s);
+        }
+        uint32_t cb[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float r = fminf(fmaxf(rint_div(v[e], sc[b], inv[b]), -127.0f), 127.0f);
+          cb[e] = static_cast<uint32_t>(static_cast<int32_t>(r)) & 0xffu;
+        }
+        uint2 o;
+        o.x = cb[0] | (cb[1] << 8) | (cb[2] << 16) | (cb[3] << 24);
+        o.y = cb[4] | (cb[5] << 8) | (cb[6] << 16) | (cb[7] << 24);
+        *reinterpret_cast<uint2*>(qp.q8 + (h * qp.Spad + s) * 128 + 8 * l16) = o;
+      }
+    } else {
+      // k / v: the bf16 columns go out as whole 512-byte row segments
+      for (int it = 0; it < 16; ++it) {
+        const int qi = it * 512 + tid, row = qi >> 5, ch = qi & 31;
+        if (row < nrows)
+          *reinterpret_cast<uint4*>(static_cast<uint16_t*>(a.out) + (m0 + row) * a.ldo + n0 + ch * 8) =
+              *reinterpret_cast<const uint4*>(tp(row, ch));
+      }
+      const bool vstats = role == 2 && qp.mode == 1;
+      if (role == 1 || vstats) {
+        // channel statistics of this 256-token chunk: float64 sums of bf16 values are exact, so the partial
+        // equals the pre-pass statistics kernel's bit for bit whatever the summation order
+        double acc8[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        float mx[8], mn[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) { mx[e] = -INFINITY; mn[e] = INFINITY; }
+        for (int it = 0; it < 16; ++it) {
+          const int row = it * 16 + (grp >> 1);
+          if (row >= nrows) continue;
+          float v[8];
+          load_row(row, v);
+          if (role == 1 && qp.rk.tab) attn::rms_rope8(v, lane, qp.rk, m0 + row);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            acc8[e] += static_cast<double>(v[e]);
+            mx[e] = fmaxf(mx[e], v[e]);
+            mn[e] = fminf(mn[e], v[e]);
+          }
+        }
+        __syncthreads();  // the tile is no longer read: stage 0 / 1 take the per-group partials
+        double* red = reinterpret_cast<double*>(st0);     // [32 groups][128 channels]
+        float* rmx = reinterpret_cast<float*>(st1);       // [32][128]
+        float* rmn = rmx + 32 * 128;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          red[grp * 128 + 8 * l16 + e] = acc8[e];
+          rmx[grp * 128 + 8 * l16 + e] = mx[e];
+          rmn[grp * 128 + 8 * l16 + e] = mn[e];
+        }
+        __syncthreads();
+        if (tid < 256) {
+          const int th = tid >> 7, d = tid & 127;
+          double t = 0.0;
+          float x = -INFINITY, y = INFINITY;
+          for (int gg = th; gg < 32; gg += 2) {
+            t += red[gg * 128 + d];
+            x = fmaxf(x, rmx[gg * 128 + d]);
+            y = fminf(y, rmn[gg * 128 + d]);
+          }
+          const int64_t o = ((hb + th) * nchunk + m0 / 256) * 128 + d;
+          if (role == 1) {
+            qp.kpart[o] = t;
+          } else {
+            qp.vsum[o] = t;
+            qp.vmax[o] = x;
+            qp.vmin[o] = y;
+          }
+        }
+      }
+    }
   } else {
     // bf16(y) (plain: bf16(y + bias)) goes through LDS so that the global side reads and writes whole
     // row segments of WN columns: each wave stages its 128 x WN block (row r at r * PITCH, 16-byte chunk c
@@ -429,6 +644,50 @@ extern "C" int rh3_gemm_i8_acc(const int8_t* xq, int64_t ldx, const int8_t* wq, 
   if (int e = check("gemm_i8_acc", xq, ldx, wq, ldw, acc, ldc, M, N, K, N)) return e;
   GemmArgs a{xq, ldx, wq, ldw, nullptr, nullptr, nullptr, nullptr, acc, ldc, M, N, K, 0, 0};
   return run<false, EPI_ACC>(a, stream, "gemm_i8_acc");
+}
+
+extern "C" int rh3_gemm_i8_qkv(const int8_t* xq, int64_t ldx, const float* xs, const int8_t* wq, int64_t ldw,
+                               const float* ws, const uint16_t* bias, uint16_t* out, int64_t ldo, int64_t M, int64_t H,
+                               int64_t K, const uint16_t* tab, int rot, const uint16_t* qw, const uint16_t* kw,
+                               float eps, int numerics, int rotate, void* workspace, int64_t workspace_bytes,
+                               hipStream_t stream) {
+  clear_error();
+  RH3_REQUIRE(H > 0 && H % 2 == 0 && H < 65536, "gemm_i8_qkv: H=%lld must be even (two heads per 256-column tile)",
+              (long long)H);
+  RH3_REQUIRE(numerics == 0 || numerics == 1, "gemm_i8_qkv: numerics %d (0 per-block, 1 production)", numerics);
+  RH3_REQUIRE(M > 0, "gemm_i8_qkv: M must be positive");
+  const int64_t N = 3 * H * 128;
+  if (int e = check("gemm_i8_qkv", xq, ldx, wq, ldw, out, ldo, M, N, K, N)) return e;
+  RH3_REQUIRE(xs && ws && aligned16(ws), "gemm_i8_qkv: scales required (ws 16-byte aligned)");
+  RH3_REQUIRE(!bias || aligned16(bias), "gemm_i8_qkv: bias must be 16-byte aligned");
+  QkvPrep qp{};
+  qp.H = H;
+  qp.Spad = attn_ws::pad(M);
+  qp.mode = numerics;
+  qp.rotate = rotate;
+  if (tab) {
+    RH3_REQUIRE(qw && kw && (rot == 96 || rot == 128) && aligned16(tab) && aligned16(qw) && aligned16(kw),
+                "gemm_i8_qkv: tab, qw, kw (16-byte aligned) and rot_dim 96 or 128 required");
+    qp.rq = attn::RR{tab, qw, eps, rot};
+    qp.rk = attn::RR{tab, kw, eps, rot};
+  } else {
+    qp.rq = attn::RR{nullptr, nullptr, 0.f, 0};
+    qp.rk = qp.rq;
+  }
+  int64_t need = 0;
+  if (numerics == 0) {
+    const attn_ws::Work w = attn_ws::layout(workspace, M, M, H);
+    need = w.bytes;
+    qp.q8 = w.q8; qp.qs = w.qs; qp.kpart = w.part;
+  } else {
+    const attn_ws::WorkU8 w = attn_ws::layout_u8(workspace, M, M, H);
+    need = w.bytes;
+    qp.q8 = w.q8; qp.qs = w.qs; qp.kpart = w.kpart; qp.vsum = w.vsum; qp.vmax = w.vmax; qp.vmin = w.vmin;
+  }
+  RH3_REQUIRE(workspace && aligned16(workspace) && workspace_bytes >= need,
+              "gemm_i8_qkv: workspace %lld bytes < required %lld", (long long)workspace_bytes, (long long)need);
+  GemmArgs a{xq, ldx, wq, ldw, xs, ws, bias, nullptr, out, ldo, M, N, K, 0, 0, qp};
+  return run<false, EPI_QKV>(a, stream, "gemm_i8_qkv");
 }
 
 extern "C" int rh3_gemm_fp8(const uint8_t* xq, int64_t ldx, const float* xs, const uint8_t* wq, int64_t ldw,

@@ -35,6 +35,7 @@ SIGNATURES = {
     "rh3_gemm_i8_swiglu": ([_P, _I, _P, _P, _I, _P, _P, _I, _I, _I, _I, _P], _C),
     "rh3_gemm_i8_gated": ([_P, _I, _P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _P], _C),
     "rh3_gemm_i8_acc": ([_P, _I, _P, _I, _P, _I, _I, _I, _I, _P], _C),
+    "rh3_gemm_i8_qkv": ([_P, _I, _P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _P, _C, _P, _P, _F, _C, _C, _P, _I, _P], _C),
     "rh3_gemm_fp8": ([_P, _I, _P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _P], _C),
     "rh3_attention_workspace_bytes": ([_I, _I, _I], ctypes.c_int64),
     "rh3_int8_attention": ([_P, _I, _I, _P, _I, _I, _P, _I, _I, _I, _I, _I, _F, _C, _P, _I, _I, _P, _I, _P], _C),
@@ -43,6 +44,11 @@ SIGNATURES = {
     "rh3_attention_forward": ([_I, _I, _I, _F, _P, _I, _I, _P, _I, _P], _C),
     "rh3_attention_prepass": ([_P, _I, _I, _P, _I, _I, _P, _I, _I, _I, _I, _I, _P, _C, _P, _P, _F, _C, _P, _I,
                                ctypes.POINTER(ctypes.c_void_p), _P], _C),
+    "rh3_attention_prepass_qkv": ([_P, _I, _I, _P, _I, _I, _I, _I, _P, _C, _P, _F, _C, _P, _I,
+                                   ctypes.POINTER(ctypes.c_void_p), _P], _C),
+    "rh3_attention_u8_prepass_qkv": ([_P, _I, _I, _P, _I, _I, _I, _I, _P, _C, _P, _F, _C, _C, _C, _P, _I,
+                                      ctypes.POINTER(ctypes.c_void_p), _P], _C),
+    "rh3_attention_workspace_layout": ([_C, _I, _I, _I, ctypes.POINTER(ctypes.c_int64)], _C),
     "rh3_attention_u8_workspace_bytes": ([_I, _I, _I], ctypes.c_int64),
     "rh3_int8_attention_u8": ([_P, _I, _I, _P, _I, _I, _P, _I, _I, _I, _I, _I, _P, _C, _P, _P, _F, _F, _C, _D, _C,
                                _C, _C, _P, _I, _I, _P, _I, _P], _C),

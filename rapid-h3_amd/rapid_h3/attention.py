@@ -210,6 +210,105 @@ def attention_rr_bias(q, k, v, tab, qw, kw, eps, nbias, bias, scale=None, config
                          smooth_v, rotate, out)
 
 
+def _ptr_views(ws, ptrs, spec):
+    """Views into the workspace tensor ws at the device pointers the library returned."""
+    base = ws.data_ptr()
+    out = {}
+    for name, (i, shape, dtype) in spec.items():
+        off = ptrs[i] - base
+        n = 1
+        for d in shape:
+            n *= d
+        out[name] = ws[off:off + n * torch.tensor([], dtype=dtype).element_size()].view(dtype).view(shape)
+    return out
+
+
+def _u8_views(ws, ptrs, sq, sk, h):
+    sqp, skp = (sq + 127) // 128 * 128, (sk + 127) // 128 * 128
+    v = _ptr_views(ws, ptrs, {
+        "q8": (0, (h, sqp, D), torch.int8), "qs": (1, (h, sqp), torch.float32),
+        "k8": (2, (h, skp, D), torch.int8), "ks": (3, (h, skp), torch.float32),
+        "_side": (4, (h, skp // 128, 2048), torch.uint8), "vt": (5, (h, D, skp), torch.int8),
+        "kmean": (6, (h, D), torch.float32), "vscale": (7, (h, D), torch.float32),
+        "vmean": (8, (h, D), torch.float32)})
+    side = v.pop("_side")
+    v["ksb"] = side[:, :, :1024].contiguous().view(torch.float32).view(h, skp, 2)
+    v["vinit"] = side[:, :, 1024:1536].contiguous().view(torch.int32).view(h, skp // 128, D)
+    v["_ws"], v["_sk"] = ws, sk
+    return v
+
+
+def _blk_views(ws, ptrs, sq, sk, h):
+    sqp, skp = (sq + 127) // 128 * 128, (sk + 127) // 128 * 128
+    v = _ptr_views(ws, ptrs, {
+        "q8": (0, (h, sqp, D), torch.int8), "qs": (1, (h, sqp // 128), torch.float32),
+        "k8": (2, (h, skp, D), torch.int8), "ks": (3, (h, skp // 128), torch.float32),
+        "kmean": (4, (h, D), torch.float32), "vt": (5, (h, D, skp), torch.bfloat16)})
+    v["_ws"], v["_sk"] = ws, sk
+    return v
+
+
+def workspace_offsets(numerics, sq, sk, h):
+    """Byte offsets of the workspace arrays (rh3_attention_workspace_layout), as a dict."""
+    import ctypes
+    names = (("q8", "qs", "k8", "ks", "kmean", "part", "vt", "bytes") if numerics == 0 else
+             ("q8", "qs", "k8", "ks", "side", "vt", "kmean", "vmean", "vscale", "kpart", "vsum", "vmax", "vmin",
+              "bytes"))
+    offs = (ctypes.c_int64 * len(names))()
+    nat.call("rh3_attention_workspace_layout", int(numerics), sq, sk, h, offs)
+    return dict(zip(names, offs))
+
+
+def workspace_views_u8(ws, sq, sk, h):
+    """q8, qs and the statistics block ("part": the float64 K and V sums and the V max / min, to the end of the
+    workspace) of a production workspace, as views (what int8_gemm_qkv_prep returns)."""
+    o = workspace_offsets(1, sq, sk, h)
+    sqp = (sq + 127) // 128 * 128
+    return {"q8": ws[o["q8"]:o["q8"] + h * sqp * D].view(torch.int8).view(h, sqp, D),
+            "qs": ws[o["qs"]:o["qs"] + h * sqp * 4].view(torch.float32).view(h, sqp),
+            "part": ws[o["kpart"]:o["bytes"]]}
+
+
+def prepass_qkv(k, v, workspace, numerics, tab=None, kw=None, eps=1e-5, smooth_k=True, smooth_v=True, rotate=True):
+    """The rest of the pre-pass after gemm.int8_gemm_qkv on the same workspace (k, v [S, H, 128] bf16 views of
+    its output): dict as prepass() (numerics 0) or prepass_u8() (numerics 1)."""
+    import ctypes
+    _check_qkv(k, k, v, "prepass_qkv", self_only=True)
+    s, h, _ = k.shape
+    rot = 0
+    if tab is not None:
+        if tab.dim() != 6 or tab.shape[1] != s or tab.dtype != torch.bfloat16 or kw is None:
+            raise RuntimeError("prepass_qkv: tab [1, S, 1, rot/2, 2, 2] bf16 and kw required together")
+        rot = tab.shape[3] * 2
+        tab, kw = tab.contiguous(), kw.contiguous()
+    if numerics == 0:
+        ptrs = (ctypes.c_void_p * 6)()
+        nat.call("rh3_attention_prepass_qkv", nat.ptr(k), k.stride(0), k.stride(1), nat.ptr(v), v.stride(0),
+                 v.stride(1), s, h, nat.ptr(tab), rot, nat.ptr(kw), float(eps), int(bool(smooth_k)),
+                 nat.ptr(workspace), workspace.numel(), ptrs, nat.stream(k.device))
+        return _blk_views(workspace, ptrs, s, s, h)
+    ptrs = (ctypes.c_void_p * 9)()
+    nat.call("rh3_attention_u8_prepass_qkv", nat.ptr(k), k.stride(0), k.stride(1), nat.ptr(v), v.stride(0),
+             v.stride(1), s, h, nat.ptr(tab), rot, nat.ptr(kw), float(eps), int(bool(smooth_k)), int(bool(smooth_v)),
+             int(bool(rotate)), nat.ptr(workspace), workspace.numel(), ptrs, nat.stream(k.device))
+    return _u8_views(workspace, ptrs, s, s, h)
+
+
+def attention_pre(k, v, q8, qs, part, tab, kw, eps, scale=None, config=94, smooth_k=True, smooth_v=True,
+                  rotate=True, out=None):
+    """Config 3xx (attn_int8.py:50-57): attention_rr whose Q operands and K / V statistics come from
+    cutlass_fp8.int8_gemm_qkv_prep (q8, qs, part: views of its workspace); k, v are that GEMM's k and v columns
+    ([S, H, 128] bf16 views). The same result as attention_rr with config on that GEMM's q, k, v. The rotate
+    flag must match the one int8_gemm_qkv_prep used."""
+    _production(config, "attention_pre")
+    if q8.untyped_storage().data_ptr() != part.untyped_storage().data_ptr():
+        raise RuntimeError("attention_pre: q8 / qs / part must be the views int8_gemm_qkv_prep returned")
+    ws = torch.empty(0, dtype=torch.uint8, device=q8.device).set_(q8.untyped_storage())
+    scale = k.shape[-1] ** -0.5 if scale is None else scale
+    pp = prepass_qkv(k, v, ws, 1, tab, kw, eps, smooth_k, smooth_v, rotate)
+    return forward_u8(pp, k.shape[0], out=_out(k, out), scale=scale)
+
+
 def prepass_u8(q, k, v, tab=None, qw=None, kw=None, eps=1e-5, smooth_k=True, smooth_v=True, rotate=True):
     """Production pre-pass operands (the reference's int8_prepass, attn_int8.cu:2691-2704, for verification):
     dict of q8 [H, Sqpad, 128] int8, qs [H, Sqpad] fp32, k8, ks, ksb [H, Skpad, 2] fp32, vinit
@@ -228,27 +327,7 @@ def prepass_u8(q, k, v, tab=None, qw=None, kw=None, eps=1e-5, smooth_k=True, smo
              nat.ptr(v), v.stride(0), v.stride(1), sq, sk, h, nat.ptr(tab), rot, nat.ptr(qw), nat.ptr(kw),
              float(eps), int(bool(smooth_k)), int(bool(smooth_v)), int(bool(rotate)), nat.ptr(ws), ws.numel(), ptrs,
              nat.stream(q.device))
-    sqp, skp = (sq + 127) // 128 * 128, (sk + 127) // 128 * 128
-    base = ws.data_ptr()
-
-    def view(i, nbytes):
-        off = ptrs[i] - base
-        return ws[off:off + nbytes]
-
-    side = view(4, h * (skp // 128) * 2048).view(h, skp // 128, 2048)
-    return {
-        "q8": view(0, h * sqp * D).view(torch.int8).view(h, sqp, D),
-        "qs": view(1, h * sqp * 4).view(torch.float32).view(h, sqp),
-        "k8": view(2, h * skp * D).view(torch.int8).view(h, skp, D),
-        "ks": view(3, h * skp * 4).view(torch.float32).view(h, skp),
-        "ksb": side[:, :, :1024].contiguous().view(torch.float32).view(h, skp, 2),
-        "vinit": side[:, :, 1024:1536].contiguous().view(torch.int32).view(h, skp // 128, D),
-        "vt": view(5, h * D * skp).view(torch.int8).view(h, D, skp),
-        "kmean": view(6, h * D * 4).view(torch.float32).view(h, D),
-        "vscale": view(7, h * D * 4).view(torch.float32).view(h, D),
-        "vmean": view(8, h * D * 4).view(torch.float32).view(h, D),
-        "_ws": ws, "_sk": sk,
-    }
+    return _u8_views(ws, ptrs, sq, sk, h)
 
 
 def forward_u8(pp, sq, out=None, scale=None, nbias=0, bias=0.0):

@@ -7,7 +7,7 @@ import os
 
 from . import _native
 from . import attention as _attention
-from .attention import attention_rr, attention_rr_bias, prepass, prepass_u8  # noqa: F401
+from .attention import attention_pre, attention_rr, attention_rr_bias, prepass, prepass_u8  # noqa: F401
 
 _ENV_CONFIG = os.environ.get("RAPIDH3_ATTN_CONFIG")
 CONFIG = None if _ENV_CONFIG is None else int(_ENV_CONFIG)
@@ -27,8 +27,3 @@ def attention_bhsd(q, k, v, scale=None, **kw):
 
 def ext():
     return _native.lib()
-
-
-def attention_pre(*args, **kwargs):
-    """Config 3xx (q8/qs from the qkv GEMM epilogue, attn_int8.py:51-57) is not built for gfx950."""
-    raise NotImplementedError("attention_pre (config 3xx) is not built in rapid_h3 for gfx950")

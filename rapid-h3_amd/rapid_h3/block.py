@@ -6,8 +6,9 @@ int8_rowwise (the same chain without rotation, the configuration the benchmark n
 
     x [S, hidden] bf16 residual stream (updated in place and returned)
     RMSNorm + modulation -> INT8 (one pass)        rh3_quant_norm_mod_i8      / rh3_norm_mod_rot_quant_i8
-    QKV GEMM                                       rh3_gemm_i8
-    q/k RMSNorm + RoPE + INT8 attention            rh3_attention_prepass + rh3_attention_forward (head-major out)
+    QKV GEMM (+ Q operands, K/V statistics)        rh3_gemm_i8_qkv (rh3_gemm_i8 with fuse_qkv=False)
+    q/k RMSNorm + RoPE + INT8 attention            rh3_attention_prepass_qkv + rh3_attention_forward (head-major
+                                                   out; production numerics: the *_u8 entry points)
     head-major gather -> INT8                      rh3_quant_heads_i8         / rh3_rot_quant_heads_i8
     out-proj GEMM + gated residual, per segment    rh3_gemm_i8_gated
     RMSNorm + modulation -> INT8                   rh3_quant_norm_mod_i8      / rh3_norm_mod_rot_quant_i8
@@ -79,7 +80,7 @@ _QUANTIZERS = {
 
 
 def fused_block(x, w: BlockWeights, mod, segments, rope_tab, idx=None, mark=None, trace=None, attn_config=None,
-                text_bias=None):
+                text_bias=None, fuse_qkv=True):
     """One DiT block forward on x [S, hidden] bf16 (modified in place). mod = (shift_msa, scale_msa,
     gate_msa, shift_mlp, scale_mlp, gate_mlp), each [R, hidden]; rope_tab [1, S, 1, rot/2, 2, 2] bf16.
     mark: optional callable, called with each name of PHASES after that phase is enqueued (a timer
@@ -87,7 +88,9 @@ def fused_block(x, w: BlockWeights, mod, segments, rope_tab, idx=None, mark=None
     trace: optional dict that receives every intermediate (a checker's view of each stage).
     attn_config: None runs the per-block bf16 P.V attention; an int runs the reference's production
     numerics with that config (its 1xx presets, __init__.py:274-291). text_bias = (nbias, bias) adds the
-    Jenga text bias (configs 90 / 94 only)."""
+    Jenga text bias (configs 90 / 94 only). fuse_qkv (even head counts): the QKV GEMM's epilogue writes the
+    attention's Q operands and K / V statistics itself (gemm.int8_gemm_qkv, the reference's config 3xx
+    path), so the pre-pass skips its Q pass and statistics passes; the result is the same bit for bit."""
     shift_msa, scale_msa, gate_msa, shift_mlp, scale_mlp, gate_mlp = mod
     tick = mark or (lambda name: None)
     keep = trace.__setitem__ if trace is not None else (lambda k, v: None)
@@ -101,25 +104,38 @@ def fused_block(x, w: BlockWeights, mod, segments, rope_tab, idx=None, mark=None
     xq, xs = norm_mod_q(x, w.norm1_w, w.eps, idx, shift_msa, scale_msa)
     keep("xq1", xq), keep("xs1", xs)
     tick("quant_norm1")
-    qkv = _gemm.int8_gemm(xq, xs, w.qkv.q, w.qkv.scale)
+    numerics = 0 if attn_config is None else 1
+    if attn_config is None:
+        if text_bias is not None:
+            raise RuntimeError("text bias: needs the production attention (attn_config 90 or 94)")
+    else:
+        _attn._production(attn_config, "fused_block")
+        if text_bias is not None and text_bias[0] and int(attn_config) % 100 not in (90, 94):
+            raise RuntimeError("text bias: config 94 or 90 only")
+    fused = fuse_qkv and h % 2 == 0
+    if fused:
+        wsb = (_attn.workspace if numerics == 0 else _attn.workspace_u8)(s, s, h, x.device)
+        qkv = _gemm.int8_gemm_qkv(xq, xs, w.qkv.q, w.qkv.scale, h, wsb, numerics, tab=rope_tab, qw=w.q_norm_w,
+                                  kw=w.k_norm_w, eps=w.qk_eps)
+    else:
+        qkv = _gemm.int8_gemm(xq, xs, w.qkv.q, w.qkv.scale)
     keep("qkv", qkv)
     tick("gemm_qkv")
     q, k, v = (t.view(s, h, D) for t in qkv.split(h * D, dim=-1))
     o = torch.empty(1, h, s, D, dtype=x.dtype, device=x.device)
     # attention_rr = pre-pass (RMSNorm + RoPE + stats + INT8) then the main kernel, as two calls
-    if attn_config is None:
-        if text_bias is not None:
-            raise RuntimeError("text bias: needs the production attention (attn_config 90 or 94)")
+    if fused:
+        pp = _attn.prepass_qkv(k, v, wsb, numerics, rope_tab, w.k_norm_w, w.qk_eps)
+    elif numerics == 0:
         pp = _attn.prepass(q, k, v, rope_tab, w.q_norm_w, w.k_norm_w, w.qk_eps)
-        tick("attn_prepass")
+    else:
+        pp = _attn.prepass_u8(q, k, v, rope_tab, w.q_norm_w, w.k_norm_w, w.qk_eps)
+    keep("q8", pp["q8"]), keep("qs", pp["qs"])
+    tick("attn_prepass")
+    if numerics == 0:
         _attn.forward(pp, s, out=o[0].transpose(0, 1))
     else:
         nbias, bias = text_bias if text_bias is not None else (0, 0.0)
-        _attn._production(attn_config, "fused_block")
-        if nbias and int(attn_config) % 100 not in (90, 94):
-            raise RuntimeError("text bias: config 94 or 90 only")
-        pp = _attn.prepass_u8(q, k, v, rope_tab, w.q_norm_w, w.k_norm_w, w.qk_eps)
-        tick("attn_prepass")
         _attn.forward_u8(pp, s, out=o[0].transpose(0, 1), nbias=nbias, bias=bias)
     keep("o", o)
     tick("attn_main")

@@ -107,3 +107,31 @@ def int8_gemm_swiglu(xq, xs, wq_perm, ws_perm, config=6):
     nat.call("rh3_gemm_i8_swiglu", nat.ptr(xq), xq.stride(0), nat.ptr(xs), nat.ptr(wq_perm), wq_perm.stride(0),
              nat.ptr(ws), nat.ptr(out), out.stride(0), m, n, k, nat.stream(xq.device))
     return out
+
+
+def int8_gemm_qkv(xq, xs, wq, ws, heads, workspace, numerics, tab=None, qw=None, kw=None, eps=1e-6, rotate=True,
+                  bias=None):
+    """The qkv projection with the attention pre-pass fused into its epilogue (rh3_gemm_i8_qkv; the
+    reference's config-3xx visitor, fp8_rowwise.cu:108-272): returns out [M, 3*heads*128] bf16 whose k and v
+    columns hold bf16((acc * xs) * ws [+ bias]) and whose q columns are left unwritten; the Q operands and the
+    K (and, numerics 1, V) statistics are written into workspace, the attention workspace of
+    attention.workspace (numerics 0, per-block) or attention.workspace_u8 (numerics 1, production) for
+    Sq = Sk = M. tab [1, M, 1, rot/2, 2, 2] bf16 with qw / kw [128] bf16 applies the per-head RMSNorm + RoPE."""
+    _check(xq, wq, torch.int8, "int8_gemm_qkv")
+    m, k = xq.shape
+    n = wq.shape[0]
+    if n != 3 * heads * 128:
+        raise RuntimeError(f"int8_gemm_qkv: wq has {n} rows, expected 3 * {heads} * 128")
+    xs, ws = _vec(xs, m, "int8_gemm_qkv xs"), _vec(ws, n, "int8_gemm_qkv ws")
+    if bias is not None:
+        bias = bias.to(torch.bfloat16).contiguous()
+    rot = 0
+    if tab is not None:
+        rot = tab.shape[-3] * 2
+        tab, qw, kw = tab.contiguous(), qw.contiguous(), kw.contiguous()
+    out = torch.empty((m, n), device=xq.device, dtype=torch.bfloat16)
+    nat.call("rh3_gemm_i8_qkv", nat.ptr(xq), xq.stride(0), nat.ptr(xs), nat.ptr(wq), wq.stride(0), nat.ptr(ws),
+             nat.ptr(bias), nat.ptr(out), out.stride(0), m, heads, k, nat.ptr(tab), rot, nat.ptr(qw), nat.ptr(kw),
+             float(eps), int(numerics), int(bool(rotate)), nat.ptr(workspace), workspace.numel(),
+             nat.stream(xq.device))
+    return out

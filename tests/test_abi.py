@@ -123,3 +123,18 @@ def test_override_host_logic():
     assert override.make_override(290).rapidh3_rrcheck is True
     assert not hasattr(override.make_override(194, exact_rows="text"), "rapidh3_rmsrope")
     assert not hasattr(override.make_override(94), "rapidh3_rmsrope")
+
+
+def test_workspace_layout_offsets():
+    """rh3_attention_workspace_layout agrees with the workspace sizes and orders the arrays as declared."""
+    from rapid_h3 import _native as nat
+    from rapid_h3 import attention
+    for numerics, size_fn in ((0, "rh3_attention_workspace_bytes"), (1, "rh3_attention_u8_workspace_bytes")):
+        for sq, sk, h in ((300, 300, 2), (1, 129, 3), (145152, 145152, 24)):
+            o = attention.workspace_offsets(numerics, sq, sk, h)
+            vals = list(o.values())
+            assert vals == sorted(vals) and vals[0] == 0 and all(v % 256 == 0 for v in vals)
+            assert o["bytes"] == getattr(nat.lib(), size_fn)(sq, sk, h)
+    o = attention.workspace_offsets(1, 300, 300, 2)          # Spad 384, 2 statistics chunks
+    assert o["qs"] == 2 * 384 * 128 and o["k8"] - o["qs"] == 2 * 384 * 4
+    assert o["vt"] - o["side"] == 2 * 3 * 2048 and o["vmin"] - o["vmax"] == 2 * 2 * 128 * 4

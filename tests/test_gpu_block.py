@@ -36,8 +36,8 @@ def _setup(rng):
     return _bf(x), ws, norms, mod, tab
 
 
-@pytest.mark.parametrize("recipe", ["int8_rowwise", "int8_rot"])
-def test_fused_block_chain(dev, recipe):
+@pytest.mark.parametrize("recipe,fuse_qkv", [("int8_rowwise", True), ("int8_rot", True), ("int8_rowwise", False)])
+def test_fused_block_chain(dev, recipe, fuse_qkv):
     from rapid_h3 import gemm, kernels
     from rapid_h3.block import BlockWeights, fused_block
     rng = np.random.default_rng(21 if recipe == "int8_rot" else 20)
@@ -57,7 +57,7 @@ def test_fused_block_chain(dev, recipe):
     modd = tuple(to_dev(m, dev) for m in mod)
     x = to_dev(x0, dev)
     tr = {}
-    out = fused_block(x, w, modd, SEGMENTS, to_dev(tab, dev).view(1, S, 1, 48, 2, 2), trace=tr)
+    out = fused_block(x, w, modd, SEGMENTS, to_dev(tab, dev).view(1, S, 1, 48, 2, 2), trace=tr, fuse_qkv=fuse_qkv)
     T = {k: to_np(v) for k, v in tr.items()}
 
     rot = recipe == "int8_rot"
@@ -70,11 +70,14 @@ def test_fused_block_chain(dev, recipe):
     # 1. RMSNorm + modulation quantizer
     q1, s1 = norm_q(x0, norms["norm1"], 1e-6, idx, shift_msa, scale_msa)
     assert np.array_equal(T["xq1"], q1) and np.array_equal(T["xs1"], s1)
-    # 2. QKV GEMM
-    assert np.array_equal(T["qkv"], og.int8_gemm(T["xq1"], T["xs1"], *oqw["qkv"]))
+    # 2. QKV GEMM (the fused epilogue leaves the q columns unwritten: k and v are compared, Q via its codes)
+    qkv_ref = og.int8_gemm(T["xq1"], T["xs1"], *oqw["qkv"])
+    lo = HID if fuse_qkv else 0
+    assert np.array_equal(T["qkv"][:, lo:], qkv_ref[:, lo:])
     # 3. q/k RMSNorm + RoPE + INT8 attention (head-major output)
-    qkv = T["qkv"].reshape(S, 3, HEADS, 128)
+    qkv = qkv_ref.reshape(S, 3, HEADS, 128)
     q8, qs, k8, ks, _ = oa.prepass(qkv[:, 0], qkv[:, 1], rr=(tab, norms["qn"], norms["kn"], 1e-6))
+    assert np.array_equal(T["q8"], q8) and np.array_equal(T["qs"], qs)
     att = oa.attention_from_codes(q8, qs, k8, ks, qkv[:, 2], 128 ** -0.5)[:S]        # [S, H, D]
     o = T["o"][0]                                                                       # [H, S, D] bf16
     assert rel_l2(bf16_to_f32(o).transpose(1, 0, 2), att) < 1e-2
@@ -124,8 +127,11 @@ def test_fused_block_production_attention(dev, text_bias):
     fused_block(to_dev(x0, dev), w, tuple(to_dev(m, dev) for m in mod), SEGMENTS,
                 to_dev(tab, dev).view(1, S, 1, 48, 2, 2), trace=tr, attn_config=94, text_bias=text_bias)
     T = {k: to_np(v) for k, v in tr.items()}
-    qkv = T["qkv"].reshape(S, 3, HEADS, 128)
+    qkv_ref = og.int8_gemm(T["xq1"], T["xs1"], *[o for o in (to_np(qw["qkv"].q), to_np(qw["qkv"].scale))])
+    assert np.array_equal(T["qkv"][:, HID:], qkv_ref[:, HID:])
+    qkv = qkv_ref.reshape(S, 3, HEADS, 128)
     pp = oa.prepass_u8(qkv[:, 0], qkv[:, 1], qkv[:, 2], rr=(tab, norms["qn"], norms["kn"], 1e-6))
+    assert np.array_equal(T["q8"], pp["q8"]) and np.array_equal(T["qs"], pp["qs"])
     nb, bias = text_bias if text_bias is not None else (0, 0.0)
     att = oa.attention_u8_from_codes(pp, 128 ** -0.5, nbias=nb, bias=bias)[:S]
     o = T["o"][0]
