@@ -173,6 +173,9 @@ def main():
     ap.add_argument("--attn-config", type=int, default=None,
                     help="run the attention with the reference's production numerics (config 80-99, e.g. 94) "
                          "instead of the per-block bf16 P.V recipe the metric names")
+    ap.add_argument("--fuse-qkv", type=int, default=None, choices=(0, 1),
+                    help="1: the QKV GEMM epilogue writes the attention's Q operands and K/V statistics "
+                         "(gemm.int8_gemm_qkv); 0: plain QKV GEMM + the full pre-pass; default: the block's")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="run only the attention kernel + a 1 GiB copy (workload of the --pmc passes)")
     a = ap.parse_args()
@@ -190,8 +193,9 @@ def main():
     x, w, mod, segments, tab = setup(m, dev, a.recipe)
 
     ac = a.attn_config
+    fq = {} if a.fuse_qkv is None else {"fuse_qkv": bool(a.fuse_qkv)}
     for _ in range(a.warmup):
-        fused_block(x, w, mod, segments, tab, attn_config=ac)
+        fused_block(x, w, mod, segments, tab, attn_config=ac, **fq)
     torch.cuda.synchronize()
 
     events = []
@@ -210,7 +214,7 @@ def main():
         b = torch.cuda.Event(enable_timing=True)
         b.record()
         events.append([("begin", b)])
-        fused_block(x, w, mod, segments, tab, mark=mark, attn_config=ac)
+        fused_block(x, w, mod, segments, tab, mark=mark, attn_config=ac, **fq)
     end.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0

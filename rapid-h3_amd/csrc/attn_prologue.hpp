@@ -64,6 +64,55 @@ __device__ __forceinline__ void rms_rope8(float* x, int lane, const RR& rr, int6
   }
 }
 
+// The two halves of rms_rope8 for callers that issue the loads of several rows before computing: the rope-table
+// values of the lane's 8 channels for token s (lanes past rot load nothing), and the arithmetic with the norm
+// weights w and those table values already in registers (the same operations in the same order).
+__device__ __forceinline__ void rope_tab8(const RR& rr, int l16, int64_t s, float* tv) {
+  const int hr = rr.rot >> 1, c0 = 8 * l16;
+  if (c0 < rr.rot) {
+    const int i0 = c0 < hr ? c0 : c0 - hr;
+    const uint16_t* t = rr.tab + (s * hr + i0) * 4;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) load8(t + 8 * q, tv + 8 * q);
+  }
+}
+
+__device__ __forceinline__ void rms_rope8_pre(float* x, int lane, const RR& rr, const float* w, const float* tv) {
+  const int l16 = lane & 15;
+  float ss = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ss = ss + x[e] * x[e];
+  ss = ss + __shfl_xor(ss, 8, 64);
+  ss = ss + __shfl_xor(ss, 4, 64);
+  ss = ss + __shfl_xor(ss, 2, 64);
+  ss = ss + __shfl_xor(ss, 1, 64);
+  const float r = 1.0f / sqrtf(ss / 128.0f + rr.eps);
+  float y[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) y[e] = round_bf((r * x[e]) * w[e]);
+  const int hr = rr.rot >> 1, step = hr >> 3;
+  const int c0 = 8 * l16;
+  int src = l16;
+  if (c0 < hr) src = l16 + step;
+  else if (c0 < rr.rot) src = l16 - step;
+  float py[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) py[e] = __shfl(y[e], (lane & ~15) + src, 64);
+  if (c0 < rr.rot) {
+    const bool first = c0 < hr;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float a = first ? y[e] : py[e];
+      const float b = first ? py[e] : y[e];
+      x[e] = first ? round_bf((a * tv[4 * e + 0]) + (b * tv[4 * e + 1]))
+                   : round_bf((a * tv[4 * e + 2]) + (b * tv[4 * e + 3]));
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = y[e];
+  }
+}
+
 // Normalized Walsh-Hadamard transform of the 16-lane row (attn_int8.cu:113-128): stages at channel strides 1,
 // 2, 4 inside the lane, then 8, 16, 32, 64 (lane distances 1, 2, 4, 8), (lo, hi) -> (lo + hi, lo - hi), each
 // rounded to fp32 (the reference's order), then * fp32(1 / sqrt(128)).

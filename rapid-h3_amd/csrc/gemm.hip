@@ -351,41 +351,70 @@ __global__ void __launch_bounds__(RH3_GEMM_NW * 64, RH3_GEMM_NW / 4) gemm_kernel
     auto load_row = [&](int row, float* v) __attribute__((always_inline)) {
       unpack8(*reinterpret_cast<const uint4*>(tp(row, hh * 16 + l16)), v);
     };
+    // rows are taken 4 at a time per group, all their loads (tile values, rope-table values) issued before any
+    // arithmetic, so the table latency is paid once per 4 rows; the norm weights are loaded once
+    constexpr int R = 4;
+    const attn::RR& rr = role == 0 ? qp.rq : qp.rk;
+    float wn8[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (rr.tab) attn::load8(rr.w + 8 * l16, wn8);
+    auto load_batch = [&](int it0, float (*v)[8], float (*tv)[32]) __attribute__((always_inline)) {
+#pragma unroll
+      for (int u = 0; u < R; ++u) {
+        const int row = (it0 + u) * 16 + (grp >> 1);
+        const int64_t s = m0 + row;
+        load_row(row, v[u]);
+        if (rr.tab) attn::rope_tab8(rr, l16, s < a.M ? s : a.M - 1, tv[u]);
+      }
+    };
     if (role == 0 && qp.mode == 1) {
-      for (int it = 0; it < 16; ++it) {
-        const int row = it * 16 + (grp >> 1);
-        const int64_t s = m0 + row, h = hb + hh;
-        if (s >= qp.Spad) continue;  // uniform per row group
-        int8_t* co = qp.q8 + (h * qp.Spad + s) * 128 + 8 * l16;
-        if (s >= a.M) {
-          *reinterpret_cast<uint2*>(co) = make_uint2(0, 0);
-          if (l16 == 0) qp.qs[h * qp.Spad + s] = 0.0f;
-          continue;
+      for (int it0 = 0; it0 < 16; it0 += R) {
+        float v[R][8], tv[R][32];
+        load_batch(it0, v, tv);
+#pragma unroll
+        for (int u = 0; u < R; ++u) {
+          const int row = (it0 + u) * 16 + (grp >> 1);
+          const int64_t s = m0 + row, h = hb + hh;
+          if (s >= qp.Spad) continue;  // uniform per row group
+          int8_t* co = qp.q8 + (h * qp.Spad + s) * 128 + 8 * l16;
+          if (s >= a.M) {
+            *reinterpret_cast<uint2*>(co) = make_uint2(0, 0);
+            if (l16 == 0) qp.qs[h * qp.Spad + s] = 0.0f;
+            continue;
+          }
+          if (rr.tab) attn::rms_rope8_pre(v[u], lane, rr, wn8, tv[u]);
+          if (qp.rotate) attn::wht128_row(v[u], l16);
+          uint2 codes;
+          const float sc = attn::token_quant_row(v[u], codes);
+          *reinterpret_cast<uint2*>(co) = codes;
+          if (l16 == 0) qp.qs[h * qp.Spad + s] = sc;
         }
-        float v[8];
-        load_row(row, v);
-        if (qp.rq.tab) attn::rms_rope8(v, lane, qp.rq, s);
-        if (qp.rotate) attn::wht128_row(v, l16);
-        uint2 codes;
-        const float sc = attn::token_quant_row(v, codes);
-        *reinterpret_cast<uint2*>(co) = codes;
-        if (l16 == 0) qp.qs[h * qp.Spad + s] = sc;
       }
     } else if (role == 0) {
-      // one scale per (head, 128-token block): absmax pass, block reduction, then the codes from the same
-      // values recomputed (rows past M count as 0, as in the pre-pass quantizer)
+      // one scale per (head, 128-token block): the RMSNorm + RoPE'd rows (bf16 values) go back into the tile
+      // while the block absmax accumulates, then the codes are made from them (rows past M count as 0, as in
+      // the pre-pass quantizer)
       float bmax[2] = {0.0f, 0.0f};
-      for (int it = 0; it < 16; ++it) {
-        const int row = it * 16 + (grp >> 1);
-        const int64_t s = m0 + row;
-        if (s >= a.M) continue;
-        float v[8];
-        load_row(row, v);
-        if (qp.rq.tab) attn::rms_rope8(v, lane, qp.rq, s);
-        float am = 0.0f;
+      for (int it0 = 0; it0 < 16; it0 += R) {
+        float v[R][8], tv[R][32];
+        load_batch(it0, v, tv);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) am = fmaxf(am, fabsf(v[e]));
-        bmax[it >> 3] = fmaxf(bmax[it >> 3], am);
+        for (int u = 0; u < R; ++u) {
+          const int row = (it0 + u) * 16 + (grp >> 1);
+          if (m0 + row >= a.M) continue;
+          if (rr.tab) {
+            attn::rms_rope8_pre(v[u], lane, rr, wn8, tv[u]);
+            uint4 o;
+            o.x = pack_bf2(v[u][0], v[u][1]);
+            o.y = pack_bf2(v[u][2], v[u][3]);
+            o.z = pack_bf2(v[u][4], v[u][5]);
+            o.w = pack_bf2(v[u][6], v[u][7]);
+            *reinterpret_cast<uint4*>(tp(row, hh * 16 + l16)) = o;
+          }
+          float am = 0.0f;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) am = fmaxf(am, fabsf(v[u][e]));
+          bmax[(it0 + u) >> 3] = fmaxf(bmax[(it0 + u) >> 3], am);
+        }
       }
 #pragma unroll
       for (int b = 0; b < 2; ++b) {
@@ -417,10 +446,7 @@ __global__ void __launch_bounds__(RH3_GEMM_NW * 64, RH3_GEMM_NW / 4) gemm_kernel
         const int64_t s = m0 + row, h = hb + hh;
         if (s >= qp.Spad) continue;
         float v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-        if (s < a.M) {
-          load_row(row, v);
-          if (qp.rq.tab) attn::rms_rope8(v, lane, qp.rq, s);
-        }
+        if (s < a.M) load_row(row, v);
         uint32_t cb[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
@@ -448,17 +474,26 @@ __global__ void __launch_bounds__(RH3_GEMM_NW * 64, RH3_GEMM_NW / 4) gemm_kernel
         float mx[8], mn[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) { mx[e] = -INFINITY; mn[e] = INFINITY; }
-        for (int it = 0; it < 16; ++it) {
-          const int row = it * 16 + (grp >> 1);
-          if (row >= nrows) continue;
-          float v[8];
-          load_row(row, v);
-          if (role == 1 && qp.rk.tab) attn::rms_rope8(v, lane, qp.rk, m0 + row);
+        const bool rope = role == 1 && rr.tab;
+        for (int it0 = 0; it0 < 16; it0 += R) {
+          float v[R][8], tv[R][32];
+          if (rope) {
+            load_batch(it0, v, tv);
+          } else {
 #pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            acc8[e] += static_cast<double>(v[e]);
-            mx[e] = fmaxf(mx[e], v[e]);
-            mn[e] = fminf(mn[e], v[e]);
+            for (int u = 0; u < R; ++u) load_row((it0 + u) * 16 + (grp >> 1), v[u]);
+          }
+#pragma unroll
+          for (int u = 0; u < R; ++u) {
+            const int row = (it0 + u) * 16 + (grp >> 1);
+            if (row >= nrows) continue;
+            if (rope) attn::rms_rope8_pre(v[u], lane, rr, wn8, tv[u]);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              acc8[e] += static_cast<double>(v[u][e]);
+              mx[e] = fmaxf(mx[e], v[u][e]);
+              mn[e] = fminf(mn[e], v[u][e]);
+            }
           }
         }
         __syncthreads();  // the tile is no longer read: stage 0 / 1 take the per-group partials

@@ -6,7 +6,7 @@ int8_rowwise (the same chain without rotation, the configuration the benchmark n
 
     x [S, hidden] bf16 residual stream (updated in place and returned)
     RMSNorm + modulation -> INT8 (one pass)        rh3_quant_norm_mod_i8      / rh3_norm_mod_rot_quant_i8
-    QKV GEMM (+ Q operands, K/V statistics)        rh3_gemm_i8_qkv (rh3_gemm_i8 with fuse_qkv=False)
+    QKV GEMM                                       rh3_gemm_i8 (fuse_qkv: rh3_gemm_i8_qkv, + Q operands, K/V stats)
     q/k RMSNorm + RoPE + INT8 attention            rh3_attention_prepass_qkv + rh3_attention_forward (head-major
                                                    out; production numerics: the *_u8 entry points)
     head-major gather -> INT8                      rh3_quant_heads_i8         / rh3_rot_quant_heads_i8
@@ -80,7 +80,7 @@ _QUANTIZERS = {
 
 
 def fused_block(x, w: BlockWeights, mod, segments, rope_tab, idx=None, mark=None, trace=None, attn_config=None,
-                text_bias=None, fuse_qkv=True):
+                text_bias=None, fuse_qkv=False):
     """One DiT block forward on x [S, hidden] bf16 (modified in place). mod = (shift_msa, scale_msa,
     gate_msa, shift_mlp, scale_mlp, gate_mlp), each [R, hidden]; rope_tab [1, S, 1, rot/2, 2, 2] bf16.
     mark: optional callable, called with each name of PHASES after that phase is enqueued (a timer
@@ -90,7 +90,9 @@ def fused_block(x, w: BlockWeights, mod, segments, rope_tab, idx=None, mark=None
     numerics with that config (its 1xx presets, __init__.py:274-291). text_bias = (nbias, bias) adds the
     Jenga text bias (configs 90 / 94 only). fuse_qkv (even head counts): the QKV GEMM's epilogue writes the
     attention's Q operands and K / V statistics itself (gemm.int8_gemm_qkv, the reference's config 3xx
-    path), so the pre-pass skips its Q pass and statistics passes; the result is the same bit for bit."""
+    path), so the pre-pass skips its Q pass and statistics passes; the result is the same bit for bit. Off by
+    default: at the benchmark shape the longer GEMM epilogue costs 0.4-0.6 ms more than the pre-pass passes it
+    removes."""
     shift_msa, scale_msa, gate_msa, shift_mlp, scale_mlp, gate_mlp = mod
     tick = mark or (lambda name: None)
     keep = trace.__setitem__ if trace is not None else (lambda k, v: None)
