@@ -146,8 +146,8 @@ constexpr int FWD_WAVES = 12, FWD_NT = FWD_WAVES * 64, FWD_BQ = FWD_WAVES * 32;
 constexpr int MAGIC_I = 0x4B400000;  // bits of 1.5 * 2^23
 constexpr float MAGIC_F = 12582912.0f;
 constexpr int STEP = 64;  // keys per step
-#ifndef LAG_MASK
-#define LAG_MASK 2  // bit i set: waves 4i..4i+3 (one per SIMD) run half a step behind
+#ifndef ATT_PHASES
+#define ATT_PHASES 0x010  // nibble i: the barrier phase of waves 4i..4i+3 (one per SIMD), see the main loop
 #endif
 // lazy rescale: the reference max moves only when a step max exceeds it by more than 2^8 (P <= 256)
 constexpr float RESCALE_LOG2 = 8.0f;
@@ -276,12 +276,9 @@ __global__ void __launch_bounds__(FWD_NT, 1) attn_fwd_kernel(const FwdArgs a) {
 #endif
   };
   // online softmax of step j's scores and O^T += V^T(j) . P^T; TAIL steps hold 1..63 keys below Sk
-  auto softmax_pv = [&](const int j, auto tail) __attribute__((always_inline)) {
+  uint32_t pk[2][8];  // P of the current step, bf16 pairs, the B operand of the P.V MFMAs
+  auto softmax = [&](const int j, auto tail) __attribute__((always_inline)) {
     constexpr bool TAIL = decltype(tail)::value;
-    const uint32_t so = static_cast<uint32_t>(j & 3) * SLOT;
-    uint32_t va[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) va[i] = voff[i] + so;
     // c > 0, so the step's max score is c * (max int32 accumulator over the valid keys); a tail step
     // holds key j*64, so every query's max covers at least one key
     const int nvalid = TAIL ? static_cast<int>(a.Sk - static_cast<int64_t>(j) * STEP) : STEP;
@@ -308,7 +305,6 @@ __global__ void __launch_bounds__(FWD_NT, 1) attn_fwd_kernel(const FwdArgs a) {
     // nb = -1.5*2^23 c - mref rounded once: the same rounding error for every score of this query and step
     const float nb = fmaf(-MAGIC_F, c, -mref);
     // P = 2^(t - mref) in bf16 (P <= 2^8); keys past Sk get P = 0 (lane mask on the packed words)
-    uint32_t pk[2][8];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -333,7 +329,13 @@ __global__ void __launch_bounds__(FWD_NT, 1) attn_fwd_kernel(const FwdArgs a) {
 #pragma unroll
       for (int w = 0; w < 8; ++w)
         lrow = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2bf, pk[kb][w]), ones, lrow, false);
-    // O^T[d][query] += V^T . P^T
+  };
+  // O^T[d][query] += V^T(j) . P^T
+  auto pv = [&](const int j) __attribute__((always_inline)) {
+    const uint32_t so = static_cast<uint32_t>(j & 3) * SLOT;
+    uint32_t va[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) va[i] = voff[i] + so;
 #ifdef RH3_SETPRIO
     __builtin_amdgcn_s_setprio(1);
 #endif
@@ -356,27 +358,34 @@ __global__ void __launch_bounds__(FWD_NT, 1) attn_fwd_kernel(const FwdArgs a) {
 #endif
   };
 
-  // Barrier B_j ends the use of ring slot j. Every wave runs qk(0), softmax_pv(0), qk(1), ...; leading
-  // waves reach B_j after softmax_pv(j), lagging waves after qk(j), so between B_(j-1) and B_j a lagging
-  // wave runs softmax_pv(j-1) (VALU, then MFMA) while a leading wave runs qk(j) (MFMA, then VALU). Each
-  // wave issues the two loads of step j+2 right after B_(j-1), into slot (j+2) % 4, whose last reader
-  // (softmax_pv(j-2) of a lagging wave) ran before B_(j-1); before B_j it waits for its loads of step
-  // j+1 (vmcnt(2) leaves the two issued after B_(j-1) in flight), so slot j+1 is complete past B_j.
-  const bool lag = (LAG_MASK >> (wave >> 2)) & 1;
+  // Barrier B_j ends the use of ring slot j. Every wave runs qk(0), softmax(0), pv(0), qk(1), ... and meets
+  // B_j at one of three places, by phase: 0 after pv(j), 1 after qk(j), 2 after softmax(j). Between B_(j-1)
+  // and B_j a phase-0 wave runs qk(j) softmax(j) pv(j), a phase-1 wave softmax(j-1) pv(j-1) qk(j), a phase-2
+  // wave pv(j-1) qk(j) softmax(j): the three waves of a SIMD (one of each) rotate through MFMA, VALU, MFMA
+  // work, so one of them is on the VALU while the other two feed the MFMA pipe. Each wave issues the two
+  // loads of step j+2 right after B_(j-1), into slot (j+2) % 4, whose last readers (pv(j-2) of phases 1
+  // and 2) ran before B_(j-1); before B_j it waits for its loads of step j+1 (vmcnt(2) leaves the two
+  // issued after B_(j-1) in flight), so slot j+1 is complete past B_j.
+  const int phase = (ATT_PHASES >> (4 * (wave >> 2))) & 0xF;
   auto barrier = [&]() __attribute__((always_inline)) {
     asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
   };
   auto step = [&](const int j, auto tail) __attribute__((always_inline)) {
-    if (!lag) load_step(j + 2);
+    if (phase == 0) load_step(j + 2);
     qk(j);
-    if (lag) {
+    if (phase == 1) {
       barrier();
       load_step(j + 3);
     }
-    softmax_pv(j, tail);
-    if (!lag) barrier();
+    softmax(j, tail);
+    if (phase == 2) {
+      barrier();
+      load_step(j + 3);
+    }
+    pv(j);
+    if (phase == 0) barrier();
   };
 
   load_step(0);
@@ -385,7 +394,7 @@ __global__ void __launch_bounds__(FWD_NT, 1) attn_fwd_kernel(const FwdArgs a) {
   // wait of its own inside the loop (gfx9 s_waitcnt: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8])
   __builtin_amdgcn_s_waitcnt(0x0f70);
   __syncthreads();
-  if (lag) load_step(2);
+  if (phase != 0) load_step(2);
   for (int j = 0; j < nfull; ++j) step(j, std::false_type{});
   if (rem > 0) step(nfull, std::true_type{});
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no global->LDS load outlives the workgroup
