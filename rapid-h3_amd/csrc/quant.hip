@@ -220,19 +220,25 @@ __global__ void __launch_bounds__(256) quant_normmod_lds_kernel(const QuantArgs 
   }
   for (int64_t c = threadIdx.x * 8; c < a.K; c += 256 * 8)
     *reinterpret_cast<uint4*>(w_s + c) = a.w ? *reinterpret_cast<const uint4*>(a.w + c) : make_uint4(0, 0, 0, 0);
+  auto load_raw = [&](int64_t m, uint4* raw) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      const int64_t c = 512 * j + 8 * lane;
+      raw[j] = c < a.K ? *reinterpret_cast<const uint4*>(a.x + m * a.ldx + c) : make_uint4(0, 0, 0, 0);
+    }
+  };
+  uint4 raw[NCH];
+  load_raw(r0 + wave < a.M ? r0 + wave : a.M - 1, raw);
   __syncthreads();
   for (int i = 0; i < NM_RPW; ++i) {
     const int64_t m = r0 + static_cast<int64_t>(i) * 4 + wave;
     if (m >= a.M) break;
     float v[NCH][8];
 #pragma unroll
-    for (int j = 0; j < NCH; ++j) {
-      const int64_t c = 512 * j + 8 * lane;
-      if (c < a.K) unpack8(*reinterpret_cast<const uint4*>(a.x + m * a.ldx + c), v[j]);
-      else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[j][e] = 0.0f;
-      }
+    for (int j = 0; j < NCH; ++j) unpack8(raw[j], v[j]);
+    if (i + 1 < NM_RPW) {  // the wavefront's next row is in flight while this one is reduced and written
+      const int64_t mn = m + 4;
+      load_raw(mn < a.M ? mn : a.M - 1, raw);
     }
     float ss = 0.0f;
 #pragma unroll
