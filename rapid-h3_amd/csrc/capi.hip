@@ -27,6 +27,17 @@ int launch_status(const char* what) {
   return RH3_OK;
 }
 
+int device_cus() {
+  static int cached[64] = {0};  // per device; a race only repeats the same query
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
+  if (dev < 64 && cached[dev] > 0) return cached[dev];
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+  if (dev < 64) cached[dev] = n;
+  return n;
+}
+
 }  // namespace rh3
 
 extern "C" const char* rh3_last_error(void) { return rh3::g_error.c_str(); }

@@ -136,6 +136,9 @@ struct Mma<true> {  // e4m3: 1 MFMA of k = 64 per step, 32-byte fragments (two 1
 #ifndef RH3_GEMM_NW
 #define RH3_GEMM_NW 8
 #endif
+#ifndef RH3_GEMM_PERSIST
+#define RH3_GEMM_PERSIST 1  // 0: one workgroup per tile for every epilogue
+#endif
 
 template <bool FP8, int EPI, int NW>
 __global__ void __launch_bounds__(RH3_GEMM_NW * 64, RH3_GEMM_NW / 4) gemm_kernel(const GemmArgs a) {
@@ -609,6 +612,298 @@ __global__ void __launch_bounds__(RH3_GEMM_NW * 64, RH3_GEMM_NW / 4) gemm_kernel
   }
 }
 
+// Persistent form of gemm_kernel (every epilogue but EPI_QKV; K a multiple of 4 k-steps, at least 8): one workgroup
+// per CU walks a strided share of its XCD's tile range, in the same grouped order. The k-loop runs on
+// across tile boundaries: the loads of the next tile's first three k-steps are issued by the current
+// tile's last three steps into the ring stages those steps free, so a new tile starts with its operands
+// already in LDS. The epilogue no longer owns the ring: it stages one 32 x 32 bf16 block at a time through
+// a 2 KiB per-wave LDS area and its global stores drain while the next tile's MFMAs run. The row scales,
+// column scales and bias / gate of a tile are loaded into registers at the tile start and parked in LDS
+// after its first four k-steps. Same arithmetic as gemm_kernel, element for element.
+template <bool FP8, int EPI>
+__global__ void __launch_bounds__(512, 2) gemm_persistent_kernel(const GemmArgs a) {
+  static_assert(EPI != EPI_QKV, "the qkv epilogue stages the whole tile in the ring");
+  constexpr int NW = 8;
+  using MM = Mma<FP8>;
+  using acc_t = typename MM::acc_t;
+  constexpr int WM = Cfg<NW>::WM, WN = Cfg<NW>::WN, TI = Cfg<NW>::TI, TJ = Cfg<NW>::TJ;
+  constexpr int NL = (BM * BK / 16) / (NW * 64);
+  static_assert(NL == 2 && WM == 128 && WN == 64 && TI == 2 && TJ == 4, "layout below");
+  __shared__ __attribute__((aligned(16))) int8_t st0[2 * TILE_BYTES], st1[2 * TILE_BYTES], st2[2 * TILE_BYTES],
+      st3[2 * TILE_BYTES];
+  __shared__ __attribute__((aligned(16))) int8_t ep_lds[NW * 2048];  // per-wave 32 x 32 bf16 staging block
+  __shared__ __attribute__((aligned(16))) float rec[3 * BM];         // xs[256], ws[256], bias / gate[256]
+
+  // XCD-aware share: workgroup b runs on XCD b % 8; XCD x owns the logical tiles [lo, hi) and its nslot
+  // workgroups take them round robin, so the ~32 tiles in flight on an XCD are consecutive in the grouped
+  // order (shared activation and weight panels in that XCD's L2)
+  const int nb = a.tiles_m * a.tiles_n;
+  const int b = blockIdx.x, xcd = b % 8, slot = b / 8;
+  const int nslot = (static_cast<int>(gridDim.x) - xcd + 7) / 8;
+  const int lo = xcd * (nb / 8) + min(xcd, nb % 8);
+  const int hi = lo + nb / 8 + (xcd < nb % 8 ? 1 : 0);
+  int lt = lo + slot;
+  if (lt >= hi) return;  // whole workgroup: no tile here
+  auto tile_origin = [&](int t, int64_t& m0, int64_t& n0) __attribute__((always_inline)) {
+    const int group = t / (GROUP_M * a.tiles_n), first_m = group * GROUP_M;
+    const int gsz = min(a.tiles_m - first_m, GROUP_M);
+    const int r = t % (GROUP_M * a.tiles_n);
+    m0 = static_cast<int64_t>(first_m + r % gsz) * BM;
+    n0 = static_cast<int64_t>(r / gsz) * BN;
+  };
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / (NW / 2), wn = wave % (NW / 2);
+  const int l32 = lane & 31, g = lane >> 5;
+
+  // global -> LDS copy geometry as in gemm_kernel (swizzle applied on the global side)
+  const int8_t* xp[NL];
+  const int8_t* wp[NL];
+  auto tile_ptrs = [&](int64_t m0, int64_t n0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      const int p = (NL * wave + i) * 64 + lane, r = p >> 2;
+      const int c = (p & 3) ^ (((r >> 1) & 3) ^ ((r >> 3) & 1));
+      int64_t mr = m0 + r, nr = n0 + r;
+      mr = mr < a.M ? mr : a.M - 1;
+      nr = nr < a.N ? nr : a.N - 1;
+      xp[i] = a.x + mr * a.ldx + c * 16;
+      wp[i] = a.w + nr * a.ldw + c * 16;
+    }
+  };
+  const int nk = static_cast<int>(a.K / BK);
+  auto gload = [&](int kt, int8_t* stg) __attribute__((always_inline)) {
+    const int64_t k0 = static_cast<int64_t>(kt) * BK;
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      __builtin_amdgcn_global_load_lds(xp[i] + k0, stg + (NL * wave + i) * 1024, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(wp[i] + k0, stg + TILE_BYTES + (NL * wave + i) * 1024, 16, 0, 0);
+    }
+  };
+
+  acc_t acc[TI][TJ];
+  auto zero_acc = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+      for (int j = 0; j < TJ; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+  };
+  // vmcnt(8): the loads of the next k-step have landed, the two k-steps after it stay in flight (loads
+  // or stores issued in between only make the wait stronger)
+  auto sync_next = [&]() __attribute__((always_inline)) {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0x0078);
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+  typename MM::frag_t fa0[TI], fb0[TJ], fa1[TI], fb1[TJ];
+  auto load_frags = [&](const int8_t* stg, const int ks, typename MM::frag_t* fa, typename MM::frag_t* fb)
+      __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < TI; ++i) fa[i] = MM::load(stg + TILE_BYTES, wn * WN + i * 32 + l32, ks, g);
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) fb[j] = MM::load(stg, wm * WM + j * 32 + l32, ks, g);
+  };
+  auto mma_all = [&](const typename MM::frag_t* fa, const typename MM::frag_t* fb) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+      for (int j = 0; j < TJ; ++j) acc[i][j] = MM::mma(fa[i], fb[j], acc[i][j]);
+  };
+  // one k-step reading stage cur, after first loading k-step kload of the current pointers into nxt3 (the
+  // stage of the previous k-step, whose readers all passed the previous barrier); as in gemm_kernel
+  auto step = [&](const int kload, const int8_t* cur, const int8_t* nxt1, int8_t* nxt3) __attribute__((always_inline)) {
+    gload(kload, nxt3);
+    if constexpr (MM::KSUB == 2) {
+      load_frags(cur, 1, fa1, fb1);
+      mma_all(fa0, fb0);
+      sync_next();
+      load_frags(nxt1, 0, fa0, fb0);
+      mma_all(fa1, fb1);
+    } else {
+      load_frags(cur, 0, fa1, fb1);
+      mma_all(fa1, fb1);
+      sync_next();
+    }
+  };
+
+  int64_t m0, n0;
+  tile_origin(lt, m0, n0);
+  tile_ptrs(m0, n0);
+  zero_acc();
+  gload(0, st0);
+  gload(1, st1);
+  gload(2, st2);
+  __builtin_amdgcn_s_waitcnt(0x0078);  // k-step 0 has landed
+  __syncthreads();
+  if constexpr (MM::KSUB == 2) load_frags(st0, 0, fa0, fb0);
+
+  constexpr bool HAS_BG = EPI == EPI_PLAIN || EPI == EPI_GATED;
+  const uint16_t* bg = EPI == EPI_GATED ? a.gate : a.bias;
+  while (true) {
+    // this tile's scales (and bias / gate) into registers now, into LDS before the last k-step
+    float rv0 = 0.0f, rv1 = 0.0f;
+    if constexpr (EPI != EPI_ACC) {
+      if (tid < BM) {
+        const int64_t m = m0 + tid;
+        if (m < a.M) rv0 = a.xs[m];
+      } else {
+        const int64_t n = n0 + (tid - BM);
+        if (n < a.N) {
+          rv0 = a.ws[n];
+          if (HAS_BG && bg) rv1 = bf2f(bg[n]);
+        }
+      }
+    }
+    const int ltn = lt + nslot;
+    const bool more = ltn < hi;
+    int64_t m0n = m0, n0n = n0;
+    if (more) tile_origin(ltn, m0n, n0n);
+
+    // k-steps 0..3, then the record goes to LDS: every wave has finished the previous tile's epilogue (it
+    // passed this tile's barriers since), and the barriers of the k-steps left publish it to this tile's
+    step(3, st0, st1, st3);
+    step(4, st1, st2, st0);
+    step(5, st2, st3, st1);
+    step(6, st3, st0, st2);
+    if constexpr (EPI != EPI_ACC) {
+      rec[tid] = rv0;
+      if (tid >= BM) rec[BM + tid] = rv1;
+    }
+    for (int kt = 4; kt + 4 < nk; kt += 4) {
+      step(kt + 3, st0, st1, st3);
+      step(kt + 4, st1, st2, st0);
+      step(kt + 5, st2, st3, st1);
+      step(kt + 6, st3, st0, st2);
+    }
+    // the last four k-steps; the three after them are the next tile's k-steps 0..2 (with no next tile:
+    // the current tile's last k-step again, into stages nobody reads)
+    step(nk - 1, st0, st1, st3);
+    if (more) tile_ptrs(m0n, n0n);
+    const int k0n = more ? 0 : nk - 1, k1n = more ? 1 : nk - 1, k2n = more ? 2 : nk - 1;
+    step(k0n, st1, st2, st0);
+    step(k1n, st2, st3, st1);
+    step(k2n, st3, st0, st2);
+
+    // epilogue: acc[i][j] register r holds m = m0 + wm*128 + j*32 + l32,
+    //           n = n0 + wn*64 + i*32 + 8*(r/4) + 4*g + (r%4)
+    if constexpr (EPI == EPI_ACC) {
+      static_assert(!FP8, "raw accumulators are an int8 feature");
+#pragma unroll
+      for (int j = 0; j < TJ; ++j) {
+        const int64_t m = m0 + wm * WM + j * 32 + l32;
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+          for (int rq = 0; rq < 4; ++rq) {
+            const int64_t n = n0 + wn * WN + i * 32 + 8 * rq + 4 * g;
+            if (m < a.M && n < a.N) {
+              int4 v;
+              v.x = acc[i][j][4 * rq + 0];
+              v.y = acc[i][j][4 * rq + 1];
+              v.z = acc[i][j][4 * rq + 2];
+              v.w = acc[i][j][4 * rq + 3];
+              *reinterpret_cast<int4*>(static_cast<int32_t*>(a.out) + m * a.ldo + n) = v;
+            }
+          }
+      }
+    } else {
+      // block (j, i) = rows j*32.., columns i*32.. of the wave's 128 x 64: bf16(y) (plain: bf16(y + bias))
+      // staged with row r at r * 64 B, 16-byte chunk c at c ^ ((r >> 2) & 3), then lane l handles row
+      // 16*it + l/4, columns 8*(l%4)..+7, so global accesses are 64-byte row segments
+      int8_t* const ep = ep_lds + wave * 2048;
+      const float* xs_s = rec;
+      const float* ws_s = rec + BM;
+      const float* bg_s = rec + 2 * BM;
+      const int chr = lane & 3;
+#pragma unroll
+      for (int j = 0; j < TJ; ++j) {
+        const int row = j * 32 + l32;
+        const float xsm = xs_s[wm * WM + row];
+        // the residual segments of this row block (gated): issued before the staging so their latency
+        // runs under it
+        uint4 rres[TI][2];
+        if constexpr (EPI == EPI_GATED) {
+#pragma unroll
+          for (int i = 0; i < TI; ++i)
+#pragma unroll
+            for (int it = 0; it < 2; ++it) {
+              const int64_t m = m0 + wm * WM + j * 32 + it * 16 + (lane >> 2);
+              const int64_t n = n0 + wn * WN + i * 32 + chr * 8;
+              rres[i][it] = (m < a.M && n < a.N)
+                                ? *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.out) + m * a.ldo + n)
+                                : make_uint4(0, 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < TI; ++i) {
+#pragma unroll
+          for (int rq = 0; rq < 4; ++rq) {
+            const int col = wn * WN + i * 32 + 8 * rq + 4 * g;  // tile column of acc register 4*rq
+            const float4 wsn = *reinterpret_cast<const float4*>(ws_s + col);
+            float y[4] = {(MM::val(acc[i][j], 4 * rq + 0) * xsm) * wsn.x, (MM::val(acc[i][j], 4 * rq + 1) * xsm) * wsn.y,
+                          (MM::val(acc[i][j], 4 * rq + 2) * xsm) * wsn.z, (MM::val(acc[i][j], 4 * rq + 3) * xsm) * wsn.w};
+            if constexpr (EPI == EPI_PLAIN) {
+              if (a.bias) {
+                const float4 bb = *reinterpret_cast<const float4*>(bg_s + col);
+                y[0] = y[0] + bb.x;
+                y[1] = y[1] + bb.y;
+                y[2] = y[2] + bb.z;
+                y[3] = y[3] + bb.w;
+              }
+            }
+            uint2 o;
+            o.x = pack_bf2(y[0], y[1]);
+            o.y = pack_bf2(y[2], y[3]);
+            *reinterpret_cast<uint2*>(ep + l32 * 64 + ((rq ^ ((l32 >> 2) & 3)) << 4) + 8 * g) = o;
+          }
+          // each lane reads back what other lanes of its own wave wrote: LDS executes a wave's accesses
+          // in order, and the compiler keeps the reads after the writes (same array)
+#pragma unroll
+          for (int it = 0; it < 2; ++it) {
+            const int r = it * 16 + (lane >> 2);
+            const uint4 v = *reinterpret_cast<const uint4*>(ep + r * 64 + ((chr ^ ((r >> 2) & 3)) << 4));
+            const int64_t m = m0 + wm * WM + j * 32 + r;
+            const int64_t n = n0 + wn * WN + i * 32 + chr * 8;
+            if (m < a.M && n < a.N) {
+              if constexpr (EPI == EPI_PLAIN) {
+                *reinterpret_cast<uint4*>(static_cast<uint16_t*>(a.out) + m * a.ldo + n) = v;
+              } else if constexpr (EPI == EPI_GATED) {
+                const float4 g0 = *reinterpret_cast<const float4*>(bg_s + (n - n0));
+                const float4 g1 = *reinterpret_cast<const float4*>(bg_s + (n - n0) + 4);
+                float yv[8], rv[8];
+                unpack8(v, yv);
+                unpack8(rres[i][it], rv);
+                uint4 o;
+                o.x = pack_bf2(fmaf(yv[0], g0.x, rv[0]), fmaf(yv[1], g0.y, rv[1]));
+                o.y = pack_bf2(fmaf(yv[2], g0.z, rv[2]), fmaf(yv[3], g0.w, rv[3]));
+                o.z = pack_bf2(fmaf(yv[4], g1.x, rv[4]), fmaf(yv[5], g1.y, rv[5]));
+                o.w = pack_bf2(fmaf(yv[6], g1.z, rv[6]), fmaf(yv[7], g1.w, rv[7]));
+                *reinterpret_cast<uint4*>(static_cast<uint16_t*>(a.out) + m * a.ldo + n) = o;
+              } else {  // EPI_SWIGLU: the 8 columns are one [gate 4j..4j+3 | up 4j..4j+3] group of swiglu_perm
+                float yv[8];
+                unpack8(v, yv);
+                uint2 o;
+                o.x = pack_bf2(silu_mul(yv[0], yv[4]), silu_mul(yv[1], yv[5]));
+                o.y = pack_bf2(silu_mul(yv[2], yv[6]), silu_mul(yv[3], yv[7]));
+                *reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.out) + m * a.ldo + n / 2) = o;
+              }
+            }
+          }
+        }
+      }
+    }
+    if (!more) break;
+    lt = ltn;
+    m0 = m0n;
+    n0 = n0n;
+    zero_acc();
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no global->LDS load outlives the workgroup
+}
+
 template <bool FP8, int EPI>
 int run(GemmArgs a, hipStream_t st, const char* name) {
   if (a.M == 0 || a.N == 0) return RH3_OK;
@@ -616,6 +911,15 @@ int run(GemmArgs a, hipStream_t st, const char* name) {
   a.tiles_n = static_cast<int>((a.N + BN - 1) / BN);
   const int64_t nb = static_cast<int64_t>(a.tiles_m) * a.tiles_n;
   RH3_REQUIRE(nb < (1ll << 31), "%s: too many tiles", name);
+  if constexpr (EPI != EPI_QKV && RH3_GEMM_NW == 8) {
+    const int64_t nk = a.K / BK;
+    const int cus = device_cus();
+    if (RH3_GEMM_PERSIST && nk % 4 == 0 && nk >= 8 && cus > 0) {
+      const int64_t grid = nb < cus ? nb : cus;  // one workgroup per CU (the LDS use admits no second)
+      hipLaunchKernelGGL((gemm_persistent_kernel<FP8, EPI>), dim3(static_cast<unsigned>(grid)), dim3(512), 0, st, a);
+      return launch_status(name);
+    }
+  }
   hipLaunchKernelGGL((gemm_kernel<FP8, EPI, RH3_GEMM_NW>), dim3(static_cast<unsigned>(nb)), dim3(RH3_GEMM_NW * 64), 0,
                      st, a);
   return launch_status(name);

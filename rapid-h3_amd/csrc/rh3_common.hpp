@@ -30,20 +30,22 @@ int launch_status(const char* what);
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
+// compute units of the current device (0 if the query fails), cached per device
+int device_cus();
+
 // ---------------------------------------------------------------- device: number formats
 __device__ __forceinline__ float bf2f(uint16_t h) { return __uint_as_float(static_cast<uint32_t>(h) << 16); }
 
-// fp32 -> bf16 bits, round to nearest even (inputs here are finite or +-inf; NaN maps to a quiet NaN)
-__device__ __forceinline__ uint16_t f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<uint16_t>(u >> 16);
-}
+// fp32 -> bf16 bits, round to nearest even, by the hardware conversion (v_cvt_pk_bf16_f32); the same bits as
+// adding 0x7fff + lsb to the fp32 pattern for every finite value and +-inf (overflow rounds to inf); NaN maps
+// to a quiet NaN
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint16_t f2bf(float f) { return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f)); }
 __device__ __forceinline__ float round_bf(float f) { return bf2f(f2bf(f)); }
 
 __device__ __forceinline__ uint32_t pack_bf2(float a, float b) {
-  return static_cast<uint32_t>(f2bf(a)) | (static_cast<uint32_t>(f2bf(b)) << 16);
+  const bf16x2_t v = {static_cast<__bf16>(a), static_cast<__bf16>(b)};
+  return __builtin_bit_cast(uint32_t, v);
 }
 
 // 8 bf16 in a uint4 -> 8 floats

@@ -77,6 +77,44 @@ def test_gemm_shapes(dev, m, n, k):
     assert np.array_equal(to_np(out), og.int8_gemm(xq, xs, wq, ws))
 
 
+@pytest.mark.parametrize("m,n,k", [(4500, 4112, 512), (700, 784, 1024)])
+def test_gemm_persistent_epilogues(dev, m, n, k):
+    """Shapes on the persistent kernel (K a multiple of 256, at least 512): 18 x 17 = 306 tiles give some
+    workgroups two tiles, so a tile boundary falls inside the cross-tile k-loop; ragged last tile row and
+    column. Every epilogue against the oracle: int32 accumulators, plain and bias outputs, the gated residual
+    bit-exact, SwiGLU within one bf16 ulp, FP8 within rel-L2 1e-2."""
+    from rapid_h3 import gemm
+    rng = np.random.default_rng(m + n + k)
+    xq = np.clip(np.rint(rng.standard_normal((m, k)) * 30), -127, 127).astype(np.int8)
+    wq = np.clip(np.rint(rng.standard_normal((n, k)) * 30), -127, 127).astype(np.int8)
+    xs = (rng.random((m, 1)) * 1e-3 + 1e-4).astype(np.float32)
+    ws = (rng.random((1, n)) * 1e-3 + 1e-4).astype(np.float32)
+    bias = _bf(rng.standard_normal(n))
+    gate = _bf(rng.standard_normal(n))
+    resid = _bf(rng.standard_normal((m, n)))
+    xt, wt, xst, wst = to_dev(xq, dev), to_dev(wq, dev), to_dev(xs, dev), to_dev(ws, dev)
+    acc = og.int8_acc(xq, wq)
+    assert np.array_equal(to_np(gemm.int8_gemm_acc(xt, wt)), acc)
+    y = og.dequant(acc, xs, ws)
+    assert np.array_equal(to_np(gemm.int8_gemm(xt, xst, wt, wst)), f32_to_bf16(y))
+    yb = (y + bf16_to_f32(bias).reshape(1, -1)).astype(np.float32)
+    assert np.array_equal(to_np(gemm.int8_gemm(xt, xst, wt, wst, bias=to_dev(bias, dev))), f32_to_bf16(yb))
+    rt = to_dev(resid, dev)
+    gemm.int8_gemm_gated_residual(xt, xst, wt, wst, to_dev(gate, dev), rt)
+    want = f32_to_bf16(og.fma_f32(bf16_to_f32(f32_to_bf16(y)), np.broadcast_to(bf16_to_f32(gate).reshape(1, -1), y.shape),
+                                  bf16_to_f32(resid)))
+    assert np.array_equal(to_np(rt), want)
+    h = to_np(gemm.int8_gemm_swiglu(xt, xst, wt, wst))
+    d = _bf16_ulps(h, og.swiglu_from_interleaved(f32_to_bf16(y)))
+    assert d.max() <= 1 and (d > 0).mean() < 0.01
+    fq = rng.integers(0, 256, size=(m, k), dtype=np.uint8)
+    fwq = rng.integers(0, 256, size=(n, k), dtype=np.uint8)
+    fq[(fq & 0x7F) == 0x7F] = 0  # no NaN codes
+    fwq[(fwq & 0x7F) == 0x7F] = 0
+    got = bf16_to_f32(to_np(gemm.fp8_gemm(to_dev(fq, dev, "fp8"), xst, to_dev(fwq, dev, "fp8"), wst)))
+    assert og.rel_l2(got, bf16_to_f32(og.fp8_gemm(fq, xs, fwq, ws))) < 1e-2
+
+
 def test_gemm_rejects_bad_shapes(dev):
     import torch
     from rapid_h3 import gemm
