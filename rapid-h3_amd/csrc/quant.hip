@@ -79,20 +79,27 @@ __device__ __forceinline__ uint32_t fp8_e4m3(float t) {
   return code | sign;
 }
 
-template <int KIND>
+// 16-byte row loads; STREAM: the row is read once (streaming hint), else it may be read again from L2
+template <bool STREAM>
+__device__ __forceinline__ uint4 ld_row16(const uint16_t* p) {
+  if constexpr (STREAM) return ld_stream16(p);
+  else return *reinterpret_cast<const uint4*>(p);
+}
+
+template <int KIND, bool STREAM = false>
 __device__ __forceinline__ void load_chunk(const QuantArgs& a, int64_t m, int64_t c, float* v) {
   if (KIND == KIND_HEADS) {
     const uint16_t* p = a.x + (c >> 7) * a.ld_head + m * a.ldx + (c & 127);
-    unpack8(*reinterpret_cast<const uint4*>(p), v);
+    unpack8(ld_row16<STREAM>(p), v);
   } else if (KIND == KIND_SWIGLU) {
     const uint16_t* p = a.x + m * a.ldx + c;
     float g[8], u[8];
-    unpack8(*reinterpret_cast<const uint4*>(p), g);
-    unpack8(*reinterpret_cast<const uint4*>(p + a.K), u);
+    unpack8(ld_row16<STREAM>(p), g);
+    unpack8(ld_row16<STREAM>(p + a.K), u);
 #pragma unroll
     for (int e = 0; e < 8; ++e) v[e] = silu_mul(g[e], u[e]);
   } else {
-    unpack8(*reinterpret_cast<const uint4*>(a.x + m * a.ldx + c), v);
+    unpack8(ld_row16<STREAM>(a.x + m * a.ldx + c), v);
   }
 }
 
@@ -113,12 +120,12 @@ __global__ void __launch_bounds__(256) quant_rows_kernel(const QuantArgs a) {
     if (RAW) {
       if (c < a.K) {
         const uint16_t* p = KIND == KIND_HEADS ? a.x + (c >> 7) * a.ld_head + m * a.ldx + (c & 127) : a.x + m * a.ldx + c;
-        raw[j] = *reinterpret_cast<const uint4*>(p);
+        raw[j] = ld_stream16(p);
       } else {
         raw[j] = make_uint4(0, 0, 0, 0);
       }
     } else if (c < a.K) {
-      load_chunk<KIND>(a, m, c, v[j]);
+      load_chunk<KIND, true>(a, m, c, v[j]);
     } else {
 #pragma unroll
       for (int e = 0; e < 8; ++e) v[j][e] = 0.0f;
@@ -192,7 +199,7 @@ __global__ void __launch_bounds__(256) quant_rows_kernel(const QuantArgs a) {
     } else {
       out = quant8_i8(x, s, inv);
     }
-    *reinterpret_cast<uint2*>(static_cast<int8_t*>(a.q) + m * a.ldq + c) = out;
+    st_stream8(static_cast<int8_t*>(a.q) + m * a.ldq + c, out);
   }
 }
 
@@ -200,7 +207,10 @@ __global__ void __launch_bounds__(256) quant_rows_kernel(const QuantArgs a) {
 // the same table row, so a workgroup copies the row of its first token once (as fp32, plus the weight) and
 // each wavefront then quantizes RPW rows from LDS; a row with another table index reads its values from
 // global memory. Same arithmetic and order as quant_rows_kernel<NCH, KIND_NORMMOD>.
-constexpr int NM_RPW = 8;  // rows per wavefront
+constexpr int NM_RPW = 8;
+#ifndef RH3_QUANT_SPLIT
+#define RH3_QUANT_SPLIT 1  // 0: rows wider than 4096 on quant_rows_kernel (one wavefront per row)
+#endif  // rows per wavefront
 template <int NCH, typename TabT>
 __global__ void __launch_bounds__(256) quant_normmod_lds_kernel(const QuantArgs a) {
   extern __shared__ float4 nm_lds[];   // [K/4] scale, [K/4] shift, [K/8] weight (bf16 x 8 per uint4)
@@ -224,7 +234,7 @@ __global__ void __launch_bounds__(256) quant_normmod_lds_kernel(const QuantArgs 
 #pragma unroll
     for (int j = 0; j < NCH; ++j) {
       const int64_t c = 512 * j + 8 * lane;
-      raw[j] = c < a.K ? *reinterpret_cast<const uint4*>(a.x + m * a.ldx + c) : make_uint4(0, 0, 0, 0);
+      raw[j] = c < a.K ? ld_stream16(a.x + m * a.ldx + c) : make_uint4(0, 0, 0, 0);
     }
   };
   uint4 raw[NCH];
@@ -289,7 +299,7 @@ __global__ void __launch_bounds__(256) quant_normmod_lds_kernel(const QuantArgs 
     for (int j = 0; j < NCH; ++j) {
       const int64_t c = 512 * j + 8 * lane;
       if (c >= a.K) continue;
-      *reinterpret_cast<uint2*>(static_cast<int8_t*>(a.q) + m * a.ldq + c) = quant8_i8(v[j], s, inv);
+      st_stream8(static_cast<int8_t*>(a.q) + m * a.ldq + c, quant8_i8(v[j], s, inv));
     }
   }
 }
@@ -381,9 +391,68 @@ void launch_vec(const QuantArgs& a, hipStream_t st) {
   else hipLaunchKernelGGL((quant_rows_wide_kernel<KIND, FP8, TabT, VEC>), grid, block, 0, st, a);
 }
 
+// Plain rows wider than 4096 columns: one workgroup per row, its 4 wavefronts taking every 4th 512-column
+// chunk (at most 8 each, so the row stays in 32 VGPRs per lane and occupancy stays high); the row absmax
+// goes through LDS. Same arithmetic as quant_rows_kernel<NCH, KIND_PLAIN, FP8> (max is order-free).
+template <int NCHW, bool FP8>
+__global__ void __launch_bounds__(256) quant_rows_split_kernel(const QuantArgs a) {
+  __shared__ float wmax[4];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t m = blockIdx.x;
+  uint4 raw[NCHW];
+#pragma unroll
+  for (int i = 0; i < NCHW; ++i) {
+    const int64_t c = 512 * (4 * i + wave) + 8 * lane;
+    raw[i] = c < a.K ? ld_stream16(a.x + m * a.ldx + c) : make_uint4(0, 0, 0, 0);
+  }
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NCHW; ++i) {
+    float x[8];
+    unpack8(raw[i], x);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(x[e]));
+  }
+  amax = wave_max(amax);
+  if (lane == 0) wmax[wave] = amax;
+  // the raw words are unpacked again below rather than kept as floats
+#pragma unroll
+  for (int i = 0; i < NCHW; ++i) asm volatile("" : "+v"(raw[i].x), "+v"(raw[i].y), "+v"(raw[i].z), "+v"(raw[i].w));
+  __syncthreads();
+  amax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+  const float qmax = FP8 ? 448.0f : 127.0f;
+  const float s = fmaxf(amax / qmax, 1e-12f);
+  const float inv = 1.0f / s;
+  if (threadIdx.x == 0) a.s[m] = s;
+#pragma unroll
+  for (int i = 0; i < NCHW; ++i) {
+    const int64_t c = 512 * (4 * i + wave) + 8 * lane;
+    if (c >= a.K) continue;
+    float x[8];
+    unpack8(raw[i], x);
+    uint2 out;
+    if (FP8) {
+      uint32_t b[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) b[e] = fp8_e4m3(fminf(fmaxf(x[e] / s, -448.0f), 448.0f));
+      out.x = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
+      out.y = b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24);
+    } else {
+      out = quant8_i8(x, s, inv);
+    }
+    st_stream8(static_cast<int8_t*>(a.q) + m * a.ldq + c, out);
+  }
+}
+
 template <int KIND, bool FP8, typename TabT>
 int launch(const QuantArgs& a, hipStream_t st, const char* name) {
   if (a.M == 0) return RH3_OK;
+  if (KIND == KIND_PLAIN && a.K > 4096 && a.K <= 16384 && a.M < (1ll << 31) && RH3_QUANT_SPLIT) {
+    const dim3 grid(static_cast<unsigned>(a.M)), block(256);
+    if (a.K <= 8192) hipLaunchKernelGGL((quant_rows_split_kernel<4, FP8>), grid, block, 0, st, a);
+    else hipLaunchKernelGGL((quant_rows_split_kernel<8, FP8>), grid, block, 0, st, a);
+    return launch_status(name);
+  }
   // up to 6144 columns the staged rows fit in 60 KB of LDS
   if (KIND == KIND_NORMMOD && !FP8 && a.K <= 6144 && a.K % 8 == 0) {
     const dim3 grid(static_cast<unsigned>((a.M + 4 * NM_RPW - 1) / (4 * NM_RPW))), block(256);

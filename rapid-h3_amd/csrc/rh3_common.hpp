@@ -48,6 +48,19 @@ __device__ __forceinline__ uint32_t pack_bf2(float a, float b) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
+// Streaming global accesses (the nontemporal hint): for data a kernel touches exactly once, so that it
+// does not displace reused lines in L2 / MALL
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint4 ld_stream16(const void* p) {
+  const u32x4_t t = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+  return make_uint4(t[0], t[1], t[2], t[3]);
+}
+__device__ __forceinline__ void st_stream8(void* p, uint2 v) {
+  const u32x2_t t = {v.x, v.y};
+  __builtin_nontemporal_store(t, reinterpret_cast<u32x2_t*>(p));
+}
+
 // 8 bf16 in a uint4 -> 8 floats
 __device__ __forceinline__ void unpack8(const uint4 r, float* v) {
   const uint32_t w[4] = {r.x, r.y, r.z, r.w};

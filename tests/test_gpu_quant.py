@@ -30,7 +30,8 @@ def test_quant_rows_golden(dev, golden):
     assert np.array_equal(to_np(s), g["s_fp8"])
 
 
-@pytest.mark.parametrize("m,k", [(1, 8), (7, 520), (33, 1024), (5, 8192), (9, 9216), (130, 3072)])
+@pytest.mark.parametrize("m,k", [(1, 8), (7, 520), (33, 1024), (5, 8192), (9, 9216), (130, 3072), (3, 4104), (2, 12296),
+                                 (4, 16384)])
 def test_quant_rows_shapes(dev, m, k):
     rng = np.random.default_rng(m * 131 + k)
     x = _bf(rng.standard_normal((m, k)) * np.exp(rng.standard_normal((1, k))))
