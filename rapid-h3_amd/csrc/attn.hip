@@ -9,13 +9,13 @@
 //                  bench/attn_emulate.py:10-18) -> codes [H][Spad][128] int8, scales [H][Spad/128]
 //   vt_kernel      V [S][H][128] bf16 -> Vt [H][128][Skpad] bf16, keys permuted inside 32-key groups
 //                  so that the P.V operand of each lane is one 16-byte LDS read
-// Main kernel: per (128-query block, head) workgroup of 4 waves, 32 queries per wave.
+// Main kernel: per (384-query block, head) workgroup of 12 waves, 32 queries per wave, 64-key steps.
 //   S^T = K8 . Q8^T on v_mfma_i32_32x32x32_i8 (keys on rows, queries on lanes), one fp32 dequant
 //   multiply per score c = qs[qblock] * ks[kblock] * scale * log2(e) (the 128x128 tile shares both
 //   block scales), online softmax in the exp2 domain, P rounded to bf16, and O^T += Vt . P^T on
 //   v_mfma_f32_32x32x16_bf16 (D on rows, queries on lanes, so the per-query rescale is per lane).
 //   The row sum l adds the same bf16-rounded P the MFMA consumes (attn_int8.cu:8-10, :652-656).
-//   K and Vt tiles (16 + 32 KiB) are double-buffered in LDS with XOR-swizzled 16-byte chunks.
+//   K and Vt tiles (8 + 16 KiB per step) go through a 4-slot LDS ring with XOR-swizzled 16-byte chunks.
 #include <type_traits>
 
 #include "attn_common.hpp"
