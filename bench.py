@@ -10,7 +10,11 @@ TOPS, inputs and weights resident in HBM before the timed region. Synthetic data
 with 1 % of channels x20, weights N(0, 0.02) random init, modulation and norm weights random.
 
     python bench.py [--gpus 1] [--steps 3] [--warmup 1] [--tokens 145152] [--no-cpu] [--recipe int8_rot]
-                    [--attn-config 94]
+                    [--attn-config 94] [--model h3]
+
+--model h3 runs the same block at MiniMax-H3's own shapes (hidden 5376, 56 x 128 heads, FFN 14336,
+S = 44,992 by default), the shapes of the reference's published GB10 numbers; the default (c2) is the
+configuration the metric names.
 """
 import argparse
 import json
@@ -27,7 +31,12 @@ METRIC = "INT8 attn + W8A8 GEMM TOPS (frac of MFMA peak) at 145k tokens; ms/DiT 
 PEAK_INT8_TOPS = 5033.0        # MI355X dense int8 MFMA
 PEAK_BF16_TFLOPS = 2517.0      # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
-HIDDEN, HEADS, D, FFN = 3072, 24, 128, 8192
+D = 128
+MODELS = {  # hidden, heads, FFN width, default tokens
+    "c2": (3072, 24, 8192, 145152),    # BASELINE configs C2 / C4: 36 x 48 x 84 latent patches
+    "h3": (5376, 56, 14336, 44992),    # MiniMax-H3 (the reference's bench/microbench.py:15, docs/kernels.md:405)
+}
+HIDDEN, HEADS, FFN, _ = MODELS["c2"]
 GRID = (36, 48, 84)            # latent frames x patch rows x patch columns = 145,152 tokens
 
 
@@ -45,14 +54,14 @@ def rope_table(s, device):
 
 
 def block_ops(m):
-    gemms = {"gemm_qkv": 2 * m * 3 * HIDDEN * HIDDEN, "gemm_out_gated": 2 * m * HIDDEN * HIDDEN,
+    gemms = {"gemm_qkv": 2 * m * 3 * HEADS * D * HIDDEN, "gemm_out_gated": 2 * m * HIDDEN * HEADS * D,
              "gemm_up_swiglu": 2 * m * 2 * FFN * HIDDEN, "gemm_down_gated": 2 * m * HIDDEN * FFN}
     return gemms, 4 * m * m * D * HEADS
 
 
 def quant_bytes(m):
     """Algorithmic HBM bytes of each quantizer phase: input read once, int8 codes + fp32 scale written."""
-    k_in = {"quant_norm1": HIDDEN, "quant_heads": HIDDEN, "quant_norm2": HIDDEN, "quant_h": FFN}
+    k_in = {"quant_norm1": HIDDEN, "quant_heads": HEADS * D, "quant_norm2": HIDDEN, "quant_h": FFN}
     return {n: m * k * 2 + m * k + 4 * m for n, k in k_in.items()}
 
 
@@ -69,7 +78,7 @@ def setup(m, device, recipe="int8_rowwise"):
     x[:, torch.randperm(HIDDEN, generator=g, device=device)[:HIDDEN // 100]] *= 20
     x = x.to(torch.bfloat16)
     qw = {}
-    for name, n, k in (("qkv", 3 * HIDDEN, HIDDEN), ("out", HIDDEN, HIDDEN), ("fc1", 2 * FFN, HIDDEN),
+    for name, n, k in (("qkv", 3 * HEADS * D, HIDDEN), ("out", HIDDEN, HEADS * D), ("fc1", 2 * FFN, HIDDEN),
                        ("fc2", HIDDEN, FFN)):
         qw[name] = kernels.quantize_weight(randn(n, k, std=0.02).to(torch.bfloat16), recipe)
     perm = gemm.swiglu_perm(2 * FFN, device)
@@ -105,7 +114,7 @@ def cpu_baseline(m):
     ms = 16384
     t_gemm = 0.0
     x = f32_to_bf16(rng.standard_normal((ms, HIDDEN)).astype(np.float32))
-    for n, k in ((3 * HIDDEN, HIDDEN), (HIDDEN, HIDDEN), (2 * FFN, HIDDEN), (HIDDEN, FFN)):
+    for n, k in ((3 * HEADS * D, HIDDEN), (HIDDEN, HEADS * D), (2 * FFN, HIDDEN), (HIDDEN, FFN)):
         a = x if k == HIDDEN else f32_to_bf16(rng.standard_normal((ms, k)).astype(np.float32))
         wq, ws = oq.quantize_weight(f32_to_bf16((0.02 * rng.standard_normal((n, k))).astype(np.float32)))
         t0 = time.perf_counter()
@@ -166,7 +175,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=3)
     ap.add_argument("--warmup", type=int, default=1)
-    ap.add_argument("--tokens", type=int, default=GRID[0] * GRID[1] * GRID[2])
+    ap.add_argument("--tokens", type=int, default=None, help="default: the model's (145,152 for c2)")
+    ap.add_argument("--model", default="c2", choices=tuple(MODELS),
+                    help="c2: hidden 3072, 24 heads, FFN 8192 (the metric's); h3: 5376, 56, 14336")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--recipe", default="int8_rowwise", choices=("int8_rowwise", "int8_rot"),
                     help="int8_rowwise (the configuration the metric names) or the reference's int8_rot")
@@ -183,6 +194,10 @@ def main():
         print(f"bench.py: this build runs on one GPU; --gpus {a.gpus} is not supported (no multi-GPU path)",
               file=sys.stderr)
         sys.exit(2)
+    global HIDDEN, HEADS, FFN
+    HIDDEN, HEADS, FFN, m_default = MODELS[a.model]
+    if a.tokens is None:
+        a.tokens = m_default
     if a.traffic_probe:
         traffic_probe(a.tokens)
         return
@@ -246,7 +261,8 @@ def main():
             parts[p] = {"ms": round(t, 3)}
     t_attn = phase_ms["attn_main"]
     achieved = attn_ops / (t_attn * 1e-3) / 1e12
-    traffic = traffic_from_profile() if ac is None else None
+    # the committed counter summary is of the attention at the metric's shape only
+    traffic = traffic_from_profile() if ac is None and a.model == "c2" and m == MODELS["c2"][3] else None
     kname = "attn_fwd_kernel" if ac is None else "attn_u8_kernel"
     attn_recipe = ("per-128-block Q/K, K smoothing, bf16 P.V" if ac is None else
                    f"production attention config {ac}: per-token H128-rotated Q/K, K/V smoothing, int8 V, "
@@ -256,7 +272,9 @@ def main():
         "metric": METRIC, "value": round(value, 2), "unit": "TOPS", "n_gpus": 1, "steps": a.steps,
         "warmup": a.warmup, "ms_per_step": round(ms_step, 3), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "int8", "data": "synthetic",
-        "config": {"workload": "full-size DiT block: fused quantizers + 4 W8A8 GEMMs (C2) + INT8 attention (C4)",
+        "config": {"workload": ("full-size DiT block: fused quantizers + 4 W8A8 GEMMs (C2) + INT8 attention (C4)"
+                                if a.model == "c2" else
+                                "DiT block at MiniMax-H3's own shapes: fused quantizers + 4 W8A8 GEMMs + INT8 attention"),
                    "tokens": m, "hidden": HIDDEN, "heads": HEADS, "head_dim": D, "ffn": FFN,
                    "recipe": f"{a.recipe}, {attn_recipe}", "parallelism": "none"},
         "ms_per_block": round(ms_step, 3),
