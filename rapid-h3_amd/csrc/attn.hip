@@ -442,8 +442,8 @@ int prepass(const uint16_t* q, int64_t q_ss, int64_t q_sh, const uint16_t* k, in
   const int nchunk = static_cast<int>((Sk + CHUNK - 1) / CHUNK);
   const float* mean = nullptr;
   if (smooth_k) {
-    hipLaunchKernelGGL(stats_kernel, dim3(nchunk, H), dim3(256), 0, st, k, k_ss, k_sh, Sk, rk, w.part);
-    hipLaunchKernelGGL(kmean_kernel, dim3(H), dim3(D), 0, st, w.part, nchunk, Sk, w.kmean);
+    hipLaunchKernelGGL(stats_kernel, dim3(nchunk, H), dim3(STATS_NT), 0, st, k, k_ss, k_sh, Sk, rk, w.part);
+    hipLaunchKernelGGL(kmean_kernel, dim3(H), dim3(KMEAN_NT), 0, st, w.part, nchunk, Sk, w.kmean);
     mean = w.kmean;
   } else {
     // a fill kernel, not hipMemsetAsync, so the call stays safe inside a captured HIP graph
@@ -528,7 +528,7 @@ extern "C" int rh3_attention_prepass_qkv(const uint16_t* k, int64_t k_ss, int64_
   const int nchunk = static_cast<int>((S + CHUNK - 1) / CHUNK);
   const float* mean = nullptr;
   if (smooth_k) {
-    hipLaunchKernelGGL(kmean_kernel, dim3(H), dim3(D), 0, stream, w.part, nchunk, S, w.kmean);
+    hipLaunchKernelGGL(kmean_kernel, dim3(H), dim3(KMEAN_NT), 0, stream, w.part, nchunk, S, w.kmean);
     mean = w.kmean;
   } else {
     hipLaunchKernelGGL(zero_kernel, dim3((H * D + 255) / 256), dim3(256), 0, stream, w.kmean, H * D);

@@ -18,8 +18,12 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 
 // ------------------------------------------------------------------ statistics
-// grid (nchunk, H), 256 threads = 16 token slots x 16 lanes
-__global__ void __launch_bounds__(256) stats_kernel(const uint16_t* __restrict__ k, int64_t k_ss, int64_t k_sh,
+// Sums of bf16 values in float64 are exact here (a few hundred thousand values of 8 significant bits within a
+// few dozen binades), so every summation order below gives the same bits.
+//
+// grid (nchunk, H), STATS_NT threads = 16 token slots x 16 lanes
+constexpr int STATS_NT = 256;
+__global__ void __launch_bounds__(STATS_NT) stats_kernel(const uint16_t* __restrict__ k, int64_t k_ss, int64_t k_sh,
                                                     int64_t S, RR rr, double* __restrict__ part) {
   __shared__ double red[16][D];
   const int h = blockIdx.y, c = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
@@ -54,11 +58,29 @@ __global__ void zero_kernel(float* __restrict__ p, int64_t n) {
   if (i < n) p[i] = 0.0f;
 }
 
-__global__ void kmean_kernel(const double* __restrict__ part, int nchunk, int64_t S, float* __restrict__ kmean) {
-  const int h = blockIdx.x, d = threadIdx.x;
-  double t = 0.0;
-  for (int c = 0; c < nchunk; ++c) t += part[(static_cast<int64_t>(h) * nchunk + c) * D + d];
-  kmean[h * D + d] = static_cast<float>(t / static_cast<double>(S));
+// grid (H), KMEAN_NT threads: group j of 128 channels sums chunks j, j + 8, ..., then the 8 groups
+constexpr int KMEAN_NT = 1024;
+__global__ void __launch_bounds__(KMEAN_NT) kmean_kernel(const double* __restrict__ part, int nchunk, int64_t S,
+                                                         float* __restrict__ kmean) {
+  constexpr int G = KMEAN_NT / D;
+  __shared__ double red[G][D];
+  const int h = blockIdx.x, d = threadIdx.x % D, j = threadIdx.x / D;
+  const double* p = part + static_cast<int64_t>(h) * nchunk * D + d;
+  double t0 = 0.0, t1 = 0.0;
+  int c = j;
+  for (; c + G < nchunk; c += 2 * G) {
+    t0 += p[static_cast<int64_t>(c) * D];
+    t1 += p[static_cast<int64_t>(c + G) * D];
+  }
+  if (c < nchunk) t0 += p[static_cast<int64_t>(c) * D];
+  red[j][d] = t0 + t1;
+  __syncthreads();
+  if (j == 0) {
+    double t = 0.0;
+#pragma unroll
+    for (int i = 0; i < G; ++i) t += red[i][d];
+    kmean[h * D + d] = static_cast<float>(t / static_cast<double>(S));
+  }
 }
 
 typedef __bf16 v2bf __attribute__((ext_vector_type(2)));

@@ -87,18 +87,36 @@ __global__ void __launch_bounds__(256) vstats_kernel(const uint16_t* __restrict_
   }
 }
 
-// grid H, 128 threads
-__global__ void vfinal_kernel(const double* __restrict__ vsum, const float* __restrict__ vmax,
-                              const float* __restrict__ vmin, int nchunk, int64_t S, int smooth_v,
-                              float* __restrict__ vmean, float* __restrict__ vscale) {
-  const int h = blockIdx.x, d = threadIdx.x;
+// grid H, VFINAL_NT threads: group j of 128 channels folds chunks j, j + 8, ..., then the 8 groups (the float64
+// sums of bf16 values are exact and max / min are order-free, so the grouping does not change the result)
+constexpr int VFINAL_NT = 1024;
+__global__ void __launch_bounds__(VFINAL_NT) vfinal_kernel(const double* __restrict__ vsum,
+                                                           const float* __restrict__ vmax,
+                                                           const float* __restrict__ vmin, int nchunk, int64_t S,
+                                                           int smooth_v, float* __restrict__ vmean,
+                                                           float* __restrict__ vscale) {
+  constexpr int G = VFINAL_NT / D;
+  __shared__ double rs[G][D];
+  __shared__ float rmx[G][D], rmn[G][D];
+  const int h = blockIdx.x, d = threadIdx.x % D, j = threadIdx.x / D;
   double t = 0.0;
   float a = -INFINITY, b = INFINITY;
-  for (int c = 0; c < nchunk; ++c) {
+  for (int c = j; c < nchunk; c += G) {
     const int64_t o = (static_cast<int64_t>(h) * nchunk + c) * D + d;
     t += vsum[o];
     a = fmaxf(a, vmax[o]);
     b = fminf(b, vmin[o]);
+  }
+  rs[j][d] = t;
+  rmx[j][d] = a;
+  rmn[j][d] = b;
+  __syncthreads();
+  if (j != 0) return;
+#pragma unroll
+  for (int i = 1; i < G; ++i) {
+    t += rs[i][d];
+    a = fmaxf(a, rmx[i][d]);
+    b = fminf(b, rmn[i][d]);
   }
   const float vm = smooth_v ? static_cast<float>(t / static_cast<double>(S)) : 0.0f;
   vmean[h * D + d] = vm;
@@ -512,15 +530,15 @@ int prepass_u8(const uint16_t* q, int64_t q_ss, int64_t q_sh, const uint16_t* k,
   const int nchunk = static_cast<int>((Sk + CHUNK - 1) / CHUNK);
   const float* mean = nullptr;
   if (smooth_k) {
-    hipLaunchKernelGGL(stats_kernel, dim3(nchunk, H), dim3(256), 0, st, k, k_ss, k_sh, Sk, rk, w.kpart);
-    hipLaunchKernelGGL(kmean_kernel, dim3(H), dim3(D), 0, st, w.kpart, nchunk, Sk, w.kmean);
+    hipLaunchKernelGGL(stats_kernel, dim3(nchunk, H), dim3(STATS_NT), 0, st, k, k_ss, k_sh, Sk, rk, w.kpart);
+    hipLaunchKernelGGL(kmean_kernel, dim3(H), dim3(KMEAN_NT), 0, st, w.kpart, nchunk, Sk, w.kmean);
     mean = w.kmean;
   } else {
     // a fill kernel, not hipMemsetAsync, so the call stays safe inside a captured HIP graph
     hipLaunchKernelGGL(zero_kernel, dim3((H * D + 255) / 256), dim3(256), 0, st, w.kmean, H * D);
   }
   hipLaunchKernelGGL(vstats_kernel, dim3(nchunk, H), dim3(256), 0, st, v, v_ss, v_sh, Sk, w.vsum, w.vmax, w.vmin);
-  hipLaunchKernelGGL(vfinal_kernel, dim3(H), dim3(D), 0, st, w.vsum, w.vmax, w.vmin, nchunk, Sk, smooth_v, w.vmean,
+  hipLaunchKernelGGL(vfinal_kernel, dim3(H), dim3(VFINAL_NT), 0, st, w.vsum, w.vmax, w.vmin, nchunk, Sk, smooth_v, w.vmean,
                      w.vscale);
   hipLaunchKernelGGL(tokq_kernel, dim3(sqp * H / 16), dim3(256), 0, st, q, q_ss, q_sh, Sq, sqp, H, rq,
                      static_cast<const float*>(nullptr), rotate, w.q8, w.qs, static_cast<float*>(nullptr));
@@ -632,12 +650,12 @@ extern "C" int rh3_attention_u8_prepass_qkv(const uint16_t* k, int64_t k_ss, int
   const int nchunk = static_cast<int>((S + CHUNK - 1) / CHUNK);
   const float* mean = nullptr;
   if (smooth_k) {
-    hipLaunchKernelGGL(kmean_kernel, dim3(H), dim3(D), 0, stream, w.kpart, nchunk, S, w.kmean);
+    hipLaunchKernelGGL(kmean_kernel, dim3(H), dim3(KMEAN_NT), 0, stream, w.kpart, nchunk, S, w.kmean);
     mean = w.kmean;
   } else {
     hipLaunchKernelGGL(zero_kernel, dim3((H * D + 255) / 256), dim3(256), 0, stream, w.kmean, H * D);
   }
-  hipLaunchKernelGGL(vfinal_kernel, dim3(H), dim3(D), 0, stream, w.vsum, w.vmax, w.vmin, nchunk, S, smooth_v, w.vmean,
+  hipLaunchKernelGGL(vfinal_kernel, dim3(H), dim3(VFINAL_NT), 0, stream, w.vsum, w.vmax, w.vmin, nchunk, S, smooth_v, w.vmean,
                      w.vscale);
   hipLaunchKernelGGL(tokq_kernel, dim3(skp * H / 16), dim3(256), 0, stream, k, k_ss, k_sh, S, skp, H, rk, mean, rotate,
                      w.k8, w.ks, reinterpret_cast<float*>(w.side));
