@@ -170,7 +170,44 @@ def traffic_probe(m):
     print(f"traffic probe: attn_fwd_kernel S={m} H={HEADS} D={D}; copy 1073741824 B", flush=True)
 
 
+def pmc_summary(path):
+    """Per-kernel table of a rocprofv3 --pmc counter CSV (pmc_counter_collection.csv) holding GRBM_GUI_ACTIVE and
+    SQ_VALU_MFMA_BUSY_CYCLES: average duration, the shader clock the kernel ran at (GRBM_GUI_ACTIVE sums one
+    busy-cycle count per XCD, so clock = GRBM / 8 / duration) and the MFMA pipe's busy share of the SIMD cycles
+    (SQ_VALU_MFMA_BUSY_CYCLES / (1024 SIMDs x GRBM / 8)), the utilisation at the clock actually run."""
+    import collections
+    import csv
+    import re
+    per = collections.defaultdict(dict)
+    meta = {}
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            d = int(r["Dispatch_Id"])
+            per[d][r["Counter_Name"]] = float(r["Counter_Value"])
+            meta[d] = (r["Kernel_Name"], int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
+    rows = collections.OrderedDict()
+    for d in sorted(per):
+        name, dur = meta[d]
+        name = name.replace("(anonymous namespace)::", "")
+        name = name[5:] if name.startswith("void ") else name
+        if not name.startswith("rh3::") or dur <= 0:
+            continue
+        short = re.sub(r"\(.*", "", name)
+        grbm = per[d].get("GRBM_GUI_ACTIVE", 0.0) / 8
+        busy = per[d].get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0) / 1024
+        rows.setdefault(short, []).append((dur * 1e-6, grbm / dur, busy / grbm if grbm else 0.0))
+    print("| kernel | launches | ms / launch | clock GHz | MFMA busy at that clock |")
+    print("|---|---:|---:|---:|---:|")
+    for k, v in rows.items():
+        n = len(v)
+        print(f"| `{k}` | {n} | {sum(x[0] for x in v) / n:.3f} | {sum(x[1] for x in v) / n:.2f} | "
+              f"{sum(x[2] for x in v) / n:.1%} |")
+
+
 def main():
+    if len(sys.argv) == 3 and sys.argv[1] == "--pmc-summary":
+        pmc_summary(sys.argv[2])
+        return
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=3)
