@@ -288,6 +288,42 @@ int rh3_attention_u8_forward(int64_t Sq, int64_t Sk, int64_t H, float scale, int
                              uint16_t* out, int64_t o_ss, int64_t o_sh,
                              void* workspace, int64_t workspace_bytes, hipStream_t stream);
 
+/* ---------------------------------------------------------------------------------------------
+ * INT8 flash attention with one K scale per 128-key block (attn_int8.cu configs 60-61: attn_fwd6
+ * :1786-1962 and quant_k_block :404-443). Q and V as the production numerics above (per-token H128-rotated
+ * Q; per-channel smoothed int8 V). K: mean-smoothed, H128-rotated (rotate), then one scale per (head,
+ * 128-key block) kb = max(amax, 1e-8) / 127, codes rint(x * (1 / kb)). Per tile: integer max ti of the
+ * accumulators, cc = qs * scale * log2(e) * kb, u8 P = rint(2^(fma(acc, cc, log2 255 - ti cc))), int32 P.V and
+ * the same fold. No RMSNorm + RoPE path and no text bias, as in the reference. Workspace as
+ * rh3_attention_u8_workspace_bytes.
+ * ------------------------------------------------------------------------------------------- */
+
+/* replaces attn_int8.attention(..., config=60 or 61) -> int8_attention (attn_int8.py:30-33,
+ * attn_int8.cu:2660-2667, :2812-2813). */
+int rh3_int8_attention_bk(const uint16_t* q, int64_t q_ss, int64_t q_sh,
+                          const uint16_t* k, int64_t k_ss, int64_t k_sh,
+                          const uint16_t* v, int64_t v_ss, int64_t v_sh,
+                          int64_t Sq, int64_t Sk, int64_t H, float scale,
+                          int smooth_k, int smooth_v, int rotate,
+                          uint16_t* out, int64_t o_ss, int64_t o_sh,
+                          void* workspace, int64_t workspace_bytes, hipStream_t stream);
+
+/* Pre-pass operands of configs 60-61 for verification (the reference's int8_prepass with config 60,
+ * attn_int8.cu:2618-2641): ptrs as rh3_attention_u8_prepass, except that ks holds the block scales
+ * [H, Skpad/128] and each side record holds its block scale in its first float (the pair area is otherwise
+ * unused). */
+int rh3_attention_bk_prepass(const uint16_t* q, int64_t q_ss, int64_t q_sh,
+                             const uint16_t* k, int64_t k_ss, int64_t k_sh,
+                             const uint16_t* v, int64_t v_ss, int64_t v_sh,
+                             int64_t Sq, int64_t Sk, int64_t H, int smooth_k, int smooth_v, int rotate,
+                             void* workspace, int64_t workspace_bytes, void** ptrs /* [9] */,
+                             hipStream_t stream);
+
+/* The configs 60-61 main kernel alone, on a workspace rh3_attention_bk_prepass filled for (Sq, Sk, H). */
+int rh3_attention_bk_forward(int64_t Sq, int64_t Sk, int64_t H, float scale,
+                             uint16_t* out, int64_t o_ss, int64_t o_sh,
+                             void* workspace, int64_t workspace_bytes, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -304,3 +304,86 @@ def attention_u8_from_codes(pp, scale, rows=None, heads=None, sk=None, nbias=0, 
             o = o * a + ts * (p @ vp[j0:j0 + TILE].astype(np.float64))
         out[:, hi] = (o / l * pp["vscale"][h][None].astype(np.float64) + pp["vmean"][h][None]).astype(F32)
     return out
+
+
+def block_quant_rot(x, rotate=True):
+    """Per-128-key-block K quantizer of configs 60-61 (attn_int8.cu:404-443, quant_k_block): x [S, H, D] fp32
+    (K - kmean) -> [normalized H128] -> one scale per (head, 128-token block) sc = max(amax, 1e-8) / 127 and
+    q = rint(x * fp32(1 / sc)) (the reference kernel multiplies by the reciprocal) -> (codes [H, Spad, D] int8,
+    kbs [H, Spad / 128] fp32). Rows S..Spad are zero, inside the block max and as codes."""
+    s, h, _ = x.shape
+    y = hadamard128(x) if rotate else np.asarray(x, F32)
+    sp = spad(s)
+    yp = np.zeros((sp, h, D), F32)
+    yp[:s] = y
+    blk = yp.reshape(sp // BLOCK, BLOCK, h, D)
+    amax = np.abs(blk).max(axis=(1, 3))                                   # [nblk, H]
+    sc = (np.maximum(amax, F32(1e-8)) / F32(127.0)).astype(F32)
+    inv = (F32(1.0) / sc).astype(F32)
+    q = np.rint((blk * inv[:, None, :, None]).astype(F32))
+    assert np.abs(q).max() <= 127
+    codes = np.ascontiguousarray(q.reshape(sp, h, D).astype(np.int8).transpose(1, 0, 2))
+    return codes, np.ascontiguousarray(sc.T)
+
+
+def prepass_blockk(q, k, v, smooth_k=True, smooth_v=True, rotate=True):
+    """Pre-pass operands of configs 60-61 (attn_int8.cu:2618-2641 without the RMSNorm + RoPE path, which those
+    configs do not have): dict q8, qs [H, Sqpad] (per token, as prepass_u8), k8 [H, Skpad, D] and kbs
+    [H, Skpad / 128] (one K scale per 128-key block after the smoothing and the H128 rotation), kmean, v8,
+    vscale, vmean, vinit (as prepass_u8)."""
+    qf, kf = _as_f32(q), _as_f32(k)
+    km = kmean(k) if smooth_k else np.zeros((kf.shape[1], D), F32)
+    q8, qs = token_quant(qf, rotate)
+    k8, kbs = block_quant_rot((kf - km[None]).astype(F32), rotate)
+    v8, vs, vm = v_int8(v, smooth_v)
+    sk = kf.shape[0]
+    skp = spad(sk)
+    vpad = np.zeros((skp, v8.shape[1], D), np.int64)
+    vpad[:sk] = v8
+    vsum = vpad.reshape(skp // TILE, TILE, -1, D).sum(axis=1).transpose(1, 0, 2)
+    vinit = (MAGIC_I + 128 * vsum).astype(np.int32)
+    return dict(q8=q8, qs=qs, k8=k8, kbs=kbs, kmean=km, v8=v8, vscale=vs, vmean=vm, vinit=vinit)
+
+
+def attention_blockk_from_codes(pp, scale, rows=None, heads=None, sk=None):
+    """The main kernel of configs 60-61 (attn_fwd6, attn_int8.cu:1786-1962) on prepass_blockk's operands, tile by
+    tile (128 keys). Per query and tile: the accumulator read as the float 1.5*2^23 + acc (keys past Sk forced to
+    1.5*2^23 - 2^22), integer tile max ti, cc = fp32(c * kb) with c = qs * scale * log2(e), tv = (ti - 1.5*2^23) cc,
+    n = max(m, tv), a = 2^(m - n), ts = 2^(tv - n), b = fma(-ti, cc, log2 255), P = rint(2^(fma(acc, cc, b))) in
+    [0, 255], l = l a + ts sum P, O = O a + ts (P . V8) (exact integers per tile), out = O / l * vscale + vmean.
+    2^x in float64 from the fp32 argument (the kernels' exp2 is a hardware approximation); the reference's
+    P = 256 wrap (possible only when cc * 2^23 is large) is a saturation at 255 here. Returns fp32
+    [len(rows), len(heads), D] before the bf16 rounding of the output."""
+    q8, qs, k8, kbs, v8 = pp["q8"], pp["qs"], pp["k8"], pp["kbs"], pp["v8"]
+    sk = v8.shape[0] if sk is None else sk
+    skp = spad(sk)
+    hh = range(q8.shape[0]) if heads is None else heads
+    rows = np.arange(q8.shape[1]) if rows is None else np.asarray(rows)
+    sl2 = F32(F32(scale) * F32(1.4426950408889634))
+    out = np.zeros((len(rows), len(hh), D), F32)
+    for hi, h in enumerate(hh):
+        vp = np.zeros((skp, D), np.int64)
+        vp[:sk] = v8[:, h]
+        acc = q8[h, rows].astype(np.float64) @ k8[h, :skp].astype(np.float64).T
+        bits = (MAGIC + acc).astype(F32)                       # exact: |acc| < 2^21
+        bits[:, sk:] = MAGIC - F32(2 ** 22)
+        c = (qs[h, rows] * sl2).astype(F32)[:, None]
+        m = np.full((len(rows), 1), -np.inf, F32)
+        l = np.zeros((len(rows), 1))
+        o = np.zeros((len(rows), D))
+        for j0 in range(0, skp, TILE):
+            bt = bits[:, j0:j0 + TILE]
+            ti = bt.max(axis=1, keepdims=True)
+            cc = (c * kbs[h, j0 // TILE]).astype(F32)
+            tv = ((ti - MAGIC).astype(F32) * cc).astype(F32)
+            n = np.maximum(m, tv)
+            with np.errstate(invalid="ignore"):
+                a = np.nan_to_num(np.exp2((m - n).astype(F32).astype(np.float64)), nan=0.0)
+            ts = np.exp2((tv - n).astype(F32).astype(np.float64))
+            m = n
+            b = _fma32(-ti, cc, LOG2_255)
+            p = np.clip(np.rint(np.exp2(_fma32(bt, cc, b).astype(np.float64))), 0, 255)
+            l = l * a + ts * p.sum(axis=1, keepdims=True)
+            o = o * a + ts * (p @ vp[j0:j0 + TILE].astype(np.float64))
+        out[:, hi] = (o / l * pp["vscale"][h][None].astype(np.float64) + pp["vmean"][h][None]).astype(F32)
+    return out

@@ -23,6 +23,8 @@
 //   reference's u8 x s8 product exactly); O = fma(ts, acc bits, fma(O, a, -ts * 1.5*2^23)); out =
 //   bf16(fma(O (1 / l), vscale, vmean)). Text bias (attn_cake.cuh:97-99, :210-240): t += bias*log2(e) / c on
 //   keys [0, nbias).
+// Configs 60-61 (attn_fwd6 :1786-1962): the same kernel with BK = true and blockk_kernel (quant_k_block :404-443)
+//   in place of the per-token K quantizer: one K scale per 128-key tile, integer tile max, no per-key dequant.
 #include "attn_common.hpp"
 #include "attn_layout.hpp"
 
@@ -170,6 +172,65 @@ __global__ void __launch_bounds__(256) tokq_kernel(const uint16_t* __restrict__ 
   }
 }
 
+// ------------------------------------------------------------------ per-block K (configs 60-61)
+// grid (Skpad / 128, H), 256 threads: wave w quantizes tokens 32 w .. 32 w + 31 of the block, four 16-lane rows
+// per pass. K - kmean -> [normalized H128] -> one scale per (head, 128-key block) sc = max(amax, 1e-8) / 127,
+// codes rint(x * (1 / sc)) (quant_k_block, attn_int8.cu:404-443); sc goes to kbs [H][Skpad/128] and to the first
+// float of the block's side record, where the main kernel reads it. Padded tokens are zero rows.
+__global__ void __launch_bounds__(256) blockk_kernel(const uint16_t* __restrict__ k, int64_t k_ss, int64_t k_sh,
+                                                     int64_t S, int64_t Spad, const float* __restrict__ mean,
+                                                     int rotate, int8_t* __restrict__ codes,
+                                                     float* __restrict__ kbs, float* __restrict__ side) {
+  __shared__ float wmax[4];
+  const int h = blockIdx.y, blk = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l16 = lane & 15, sub = lane >> 4;
+  float m[8];
+  {
+    const float4 a = *reinterpret_cast<const float4*>(mean + h * D + 8 * l16);
+    const float4 b = *reinterpret_cast<const float4*>(mean + h * D + 8 * l16 + 4);
+    m[0] = a.x; m[1] = a.y; m[2] = a.z; m[3] = a.w; m[4] = b.x; m[5] = b.y; m[6] = b.z; m[7] = b.w;
+  }
+  float v[8][8];
+  float amax = 0.0f;
+#pragma unroll
+  for (int p = 0; p < 8; ++p) {
+    const int64_t s = static_cast<int64_t>(blk) * TILE + wave * 32 + p * 4 + sub;
+    const bool ok = s < S;  // uniform per 16-lane row
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[p][e] = 0.0f;
+    if (ok) {
+      load8(k + s * k_ss + h * k_sh + 8 * l16, v[p]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[p][e] = v[p][e] - m[e];
+    }
+    if (rotate) wht128_row(v[p], l16);  // every lane joins the row shuffles; zero rows stay zero
+#pragma unroll
+    for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[p][e]));
+  }
+  amax = wave_max(amax);
+  if (lane == 0) wmax[wave] = amax;
+  __syncthreads();
+  const float bm = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+  const float sc = fmaxf(bm, 1e-8f) / 127.0f;
+  const float inv = 1.0f / sc;
+  if (tid == 0) {
+    kbs[static_cast<int64_t>(h) * (Spad / TILE) + blk] = sc;
+    side[((static_cast<int64_t>(h) * (Spad / TILE) + blk) * SIDE) / 4] = sc;
+  }
+#pragma unroll
+  for (int p = 0; p < 8; ++p) {
+    const int64_t s = static_cast<int64_t>(blk) * TILE + wave * 32 + p * 4 + sub;
+    uint32_t b[8];
+    // |x * inv| <= 127 (1 + 2^-23): rint stays within the int8 range without a clamp
+#pragma unroll
+    for (int e = 0; e < 8; ++e) b[e] = static_cast<uint32_t>(static_cast<int32_t>(rintf(v[p][e] * inv))) & 0xffu;
+    uint2 o;
+    o.x = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
+    o.y = b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24);
+    *reinterpret_cast<uint2*>(codes + (static_cast<int64_t>(h) * Spad + s) * D + 8 * l16) = o;
+  }
+}
+
 // ------------------------------------------------------------------ V codes, transposed
 // Position p of a 32-key block holds key perm_u8(p): p = 16 g + r <-> key 8 (r / 4) + 4 g + r % 4, the key of
 // register r of lane group g in the S^T accumulator, so that a lane's 16 P bytes are its P.V B operand.
@@ -261,6 +322,7 @@ constexpr int U8_WAVES = 8, U8_NT = U8_WAVES * 64, U8_BQ = U8_WAVES * 32;
 #endif
 
 typedef __attribute__((address_space(3))) const v4i lds_v4i_u8;
+typedef __attribute__((address_space(3))) const float lds_f32_u8;
 
 // max of three floats in one instruction (fmaxf chains get a NaN-quieting max inserted per operand)
 __device__ __forceinline__ float max3f(float a, float b, float c) {
@@ -273,6 +335,11 @@ __device__ __forceinline__ float max3f(float a, float b, float c) {
 // (j + 2) % 4, whose last reader ran before the barrier that ended tile j - 1 (see the barrier comment).
 // A slot holds K: 128 keys x 128 B (chunk c of row r at c ^ ((r ^ (r >> 3)) & 7)), V^T: 128 channels x 128
 // keys (the same swizzle), then the 2 KiB side record. Padded keys carry b = -inf, so every tile runs unmasked.
+// BK (configs 60-61, attn_fwd6 :1786-1962): one K scale kb per 128-key tile (the first float of the side record)
+// instead of the per-key pairs: the tile max is the integer max ti of the raw accumulators (keys past Sk forced to
+// 1.5*2^23 - 2^22 first), cc = c kb, tv = (ti - 1.5*2^23) cc, n = max(m, tv), a = 2^(m - n), ts = 2^(tv - n),
+// P = rint(2^(fma(acc bits, cc, fma(-ti bits, cc, log2 255)))); the P.V, row sums and fold are the same.
+template <bool BK>
 __global__ void __launch_bounds__(U8_NT, 1) attn_u8_kernel(const U8Args a) {
   constexpr int KB = TILE * D, VB = D * TILE, SLOT = KB + VB + SIDE;
   __shared__ __attribute__((aligned(16))) int8_t ring[4 * SLOT];
@@ -364,8 +431,41 @@ __global__ void __launch_bounds__(U8_NT, 1) attn_u8_kernel(const U8Args a) {
 
   auto softmax_pv = [&](const int j) __attribute__((always_inline)) {
     const uint32_t so = static_cast<uint32_t>(j & 3) * SLOT;
-    // t = fma(1.5*2^23 + acc, s_key, b_key), in place over the accumulator registers
+    // exponent of P: 2^(fma(t, cx, bb)); u8: t the dequantized score, cx = c; BK: t the accumulator bits, cx = c kb
     float t[4][16];
+    float cx, bb, al, ts;
+    if constexpr (BK) {
+      if ((j + 1) * TILE > a.Sk) {  // the ragged last tile (uniform branch): padded keys far below every score
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            if (j * TILE + 32 * kb + 8 * (r >> 2) + 4 * g + (r & 3) >= a.Sk) s[kb][r] = MAGIC_I - (1 << 22);
+      }
+      int ti = s[0][0];
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; r += 2) ti = max(ti, max(s[kb][r], s[kb][r + 1]));
+      {
+        const auto sw = __builtin_amdgcn_permlane32_swap(ti, ti, false, false);
+        ti = max(static_cast<int>(sw[0]), static_cast<int>(sw[1]));
+      }
+      const float kbv = *reinterpret_cast<lds_f32_u8*>(static_cast<uintptr_t>(ring_lds + KB + VB + so));
+      cx = c * kbv;
+      const float tif = __int_as_float(ti);
+      const float tv = (tif - MAGIC_F) * cx;
+      const float n = fmaxf(mx, tv);
+      al = __builtin_amdgcn_exp2f(mx - n);
+      ts = __builtin_amdgcn_exp2f(tv - n);
+      mx = n;
+      bb = fmaf(-tif, cx, LOG2_255);
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) t[kb][r] = __int_as_float(s[kb][r]);
+    } else {
+    // t = fma(1.5*2^23 + acc, s_key, b_key), in place over the accumulator registers
     float tm = -INFINITY;
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb)
@@ -398,10 +498,12 @@ __global__ void __launch_bounds__(U8_NT, 1) attn_u8_kernel(const U8Args a) {
       tm = fmaxf(__int_as_float(sw[0]), __int_as_float(sw[1]));
     }
     const float n = fmaxf(mx, tm);
-    const float al = __builtin_amdgcn_exp2f((mx - n) * c);
-    const float ts = __builtin_amdgcn_exp2f((tm - n) * c);
+    al = __builtin_amdgcn_exp2f((mx - n) * c);
+    ts = __builtin_amdgcn_exp2f((tm - n) * c);
     mx = n;
-    const float bb = fmaf(-tm, c, LOG2_255);
+    bb = fmaf(-tm, c, LOG2_255);
+    cx = c;
+    }
     // P = sat_u8(rint(2^x)) with v_cvt_pk_u8_f32 (round to nearest even, saturating at 0 and 255: the
     // reference's cvt.pack.sat.u8 of __float2int_rn), four per word; the signed operand of the MFMA is P - 128
     uint32_t pw[4][4];
@@ -413,7 +515,7 @@ __global__ void __launch_bounds__(U8_NT, 1) attn_u8_kernel(const U8Args a) {
         uint32_t x = 0;
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          x = __builtin_amdgcn_cvt_pk_u8_f32(__builtin_amdgcn_exp2f(fmaf(t[kb][4 * w + e], c, bb)), e, x);
+          x = __builtin_amdgcn_cvt_pk_u8_f32(__builtin_amdgcn_exp2f(fmaf(t[kb][4 * w + e], cx, bb)), e, x);
         rs = __builtin_amdgcn_udot4(x, 0x01010101u, rs, false);
         pw[kb][w] = x ^ 0x80808080u;
       }
@@ -553,8 +655,43 @@ int forward_u8(const WorkU8& w, int64_t Sq, int64_t Sk, int64_t H, float scale, 
                int64_t o_ss, int64_t o_sh, hipStream_t st) {
   U8Args f{w.q8, w.qs, w.k8, w.side, w.vt, w.vscale, w.vmean, out, o_ss, o_sh, Sq, Sk, padk(Sq), padk(Sk),
            scale * 1.4426950408889634f, nbias, static_cast<float>(bias * 1.4426950408889634)};
-  hipLaunchKernelGGL(attn_u8_kernel, dim3((Sq + U8_BQ - 1) / U8_BQ, H), dim3(U8_NT), 0, st, f);
+  hipLaunchKernelGGL(attn_u8_kernel<false>, dim3((Sq + U8_BQ - 1) / U8_BQ, H), dim3(U8_NT), 0, st, f);
   return launch_status("attention_u8 forward");
+}
+
+// configs 60-61: Q per token as prepass_u8 (no RMSNorm + RoPE: the reference has none for these configs), K one
+// scale per 128-key block after the smoothing and the optional H128 (into ks [H][Skpad/128] and the side records),
+// V as prepass_u8 (attn_int8.cu:2618-2641)
+int prepass_bk(const uint16_t* q, int64_t q_ss, int64_t q_sh, const uint16_t* k, int64_t k_ss, int64_t k_sh,
+               const uint16_t* v, int64_t v_ss, int64_t v_sh, int64_t Sq, int64_t Sk, int64_t H, int smooth_k,
+               int smooth_v, int rotate, const WorkU8& w, hipStream_t st) {
+  const int64_t sqp = padk(Sq), skp = padk(Sk);
+  const int nchunk = static_cast<int>((Sk + CHUNK - 1) / CHUNK);
+  const RR none{nullptr, nullptr, 0.f, 0};
+  if (smooth_k) {
+    hipLaunchKernelGGL(stats_kernel, dim3(nchunk, H), dim3(STATS_NT), 0, st, k, k_ss, k_sh, Sk, none, w.kpart);
+    hipLaunchKernelGGL(kmean_kernel, dim3(H), dim3(KMEAN_NT), 0, st, w.kpart, nchunk, Sk, w.kmean);
+  } else {
+    hipLaunchKernelGGL(zero_kernel, dim3((H * D + 255) / 256), dim3(256), 0, st, w.kmean, H * D);
+  }
+  hipLaunchKernelGGL(vstats_kernel, dim3(nchunk, H), dim3(256), 0, st, v, v_ss, v_sh, Sk, w.vsum, w.vmax, w.vmin);
+  hipLaunchKernelGGL(vfinal_kernel, dim3(H), dim3(VFINAL_NT), 0, st, w.vsum, w.vmax, w.vmin, nchunk, Sk, smooth_v,
+                     w.vmean, w.vscale);
+  hipLaunchKernelGGL(tokq_kernel, dim3(sqp * H / 16), dim3(256), 0, st, q, q_ss, q_sh, Sq, sqp, H, none,
+                     static_cast<const float*>(nullptr), rotate, w.q8, w.qs, static_cast<float*>(nullptr));
+  hipLaunchKernelGGL(blockk_kernel, dim3(skp / TILE, H), dim3(256), 0, st, k, k_ss, k_sh, Sk, skp,
+                     static_cast<const float*>(w.kmean), rotate, w.k8, w.ks, reinterpret_cast<float*>(w.side));
+  hipLaunchKernelGGL(vq_kernel, dim3(skp / TILE, H), dim3(256), 0, st, v, v_ss, v_sh, Sk, skp, w.vmean, w.vscale,
+                     w.vt, reinterpret_cast<int32_t*>(w.side));
+  return launch_status("attention_bk prepass");
+}
+
+int forward_bk(const WorkU8& w, int64_t Sq, int64_t Sk, int64_t H, float scale, uint16_t* out, int64_t o_ss,
+               int64_t o_sh, hipStream_t st) {
+  U8Args f{w.q8, w.qs, w.k8, w.side, w.vt, w.vscale, w.vmean, out, o_ss, o_sh, Sq, Sk, padk(Sq), padk(Sk),
+           scale * 1.4426950408889634f, 0, 0.0f};
+  hipLaunchKernelGGL(attn_u8_kernel<true>, dim3((Sq + U8_BQ - 1) / U8_BQ, H), dim3(U8_NT), 0, st, f);
+  return launch_status("attention_bk forward");
 }
 
 int check_out_u8(const char* name, const uint16_t* out, int64_t o_ss, int64_t o_sh) {
@@ -706,4 +843,51 @@ extern "C" int rh3_int8_attention_u8(const uint16_t* q, int64_t q_ss, int64_t q_
                          w, stream))
     return e;
   return forward_u8(w, Sq, Sk, H, scale, nbias, bias, out, o_ss, o_sh, stream);
+}
+
+extern "C" int rh3_attention_bk_prepass(const uint16_t* q, int64_t q_ss, int64_t q_sh, const uint16_t* k,
+                                        int64_t k_ss, int64_t k_sh, const uint16_t* v, int64_t v_ss, int64_t v_sh,
+                                        int64_t Sq, int64_t Sk, int64_t H, int smooth_k, int smooth_v, int rotate,
+                                        void* workspace, int64_t workspace_bytes, void** ptrs, hipStream_t stream) {
+  clear_error();
+  if (int e = check_qkv_u8("attention_bk_prepass", q, q_ss, q_sh, k, k_ss, k_sh, v, v_ss, v_sh, Sq, Sk, H)) return e;
+  RH3_REQUIRE(ptrs, "attention_bk_prepass: ptrs required");
+  const WorkU8 w = layout_u8(workspace, Sq, Sk, H);
+  RH3_REQUIRE(workspace && aligned16(workspace) && workspace_bytes >= w.bytes,
+              "attention_bk_prepass: workspace %lld bytes < required %lld", (long long)workspace_bytes,
+              (long long)w.bytes);
+  if (int e = prepass_bk(q, q_ss, q_sh, k, k_ss, k_sh, v, v_ss, v_sh, Sq, Sk, H, smooth_k, smooth_v, rotate, w, stream))
+    return e;
+  ptrs[0] = w.q8; ptrs[1] = w.qs; ptrs[2] = w.k8; ptrs[3] = w.ks; ptrs[4] = w.side; ptrs[5] = w.vt;
+  ptrs[6] = w.kmean; ptrs[7] = w.vscale; ptrs[8] = w.vmean;
+  return RH3_OK;
+}
+
+extern "C" int rh3_attention_bk_forward(int64_t Sq, int64_t Sk, int64_t H, float scale, uint16_t* out, int64_t o_ss,
+                                        int64_t o_sh, void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+  clear_error();
+  RH3_REQUIRE(Sq > 0 && Sk > 0 && H > 0, "attention_bk_forward: sizes must be positive");
+  if (int e = check_out_u8("attention_bk_forward", out, o_ss, o_sh)) return e;
+  const WorkU8 w = layout_u8(workspace, Sq, Sk, H);
+  RH3_REQUIRE(workspace && aligned16(workspace) && workspace_bytes >= w.bytes,
+              "attention_bk_forward: workspace %lld bytes < required %lld", (long long)workspace_bytes,
+              (long long)w.bytes);
+  return forward_bk(w, Sq, Sk, H, scale, out, o_ss, o_sh, stream);
+}
+
+extern "C" int rh3_int8_attention_bk(const uint16_t* q, int64_t q_ss, int64_t q_sh, const uint16_t* k, int64_t k_ss,
+                                     int64_t k_sh, const uint16_t* v, int64_t v_ss, int64_t v_sh, int64_t Sq,
+                                     int64_t Sk, int64_t H, float scale, int smooth_k, int smooth_v, int rotate,
+                                     uint16_t* out, int64_t o_ss, int64_t o_sh, void* workspace,
+                                     int64_t workspace_bytes, hipStream_t stream) {
+  clear_error();
+  if (int e = check_qkv_u8("int8_attention_bk", q, q_ss, q_sh, k, k_ss, k_sh, v, v_ss, v_sh, Sq, Sk, H)) return e;
+  if (int e = check_out_u8("int8_attention_bk", out, o_ss, o_sh)) return e;
+  const WorkU8 w = layout_u8(workspace, Sq, Sk, H);
+  RH3_REQUIRE(workspace && aligned16(workspace) && workspace_bytes >= w.bytes,
+              "int8_attention_bk: workspace %lld bytes < required %lld", (long long)workspace_bytes,
+              (long long)w.bytes);
+  if (int e = prepass_bk(q, q_ss, q_sh, k, k_ss, k_sh, v, v_ss, v_sh, Sq, Sk, H, smooth_k, smooth_v, rotate, w, stream))
+    return e;
+  return forward_bk(w, Sq, Sk, H, scale, out, o_ss, o_sh, stream);
 }

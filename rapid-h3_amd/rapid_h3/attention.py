@@ -11,8 +11,13 @@ Signatures follow /root/reference/custom_nodes/rapid_h3/attn_int8.py:30-65. Two 
     1xx / 2xx select the same math (the reference's node-level fused-pre-pass and checked variants).
     The reference's other kernel configs run this same arithmetic here; the 64-key-tile configs (0, 1, 4-8,
     10-12, 20-29) and those with the acc * ks dequant (0-12) differ from their own outputs by the tile-max
-    granularity and the rounding of t. Configs 50-69 (FP8 P.V, per-block K) and 3xx (the qkv-GEMM
-    epilogue pre-pass) are not built and raise NotImplementedError.
+    granularity and the rounding of t;
+  * config 60 or 61 (attn_int8.cu attn_fwd6 :1786-1962, quant_k_block :404-443): as the production numerics but
+    with one K scale per 128-key block (after the smoothing and the H128 rotation), an integer tile max over
+    the raw accumulators and no per-key dequantization. No RMSNorm + RoPE path and no text bias (the
+    reference's own limits, attn_int8.cu:2606, :2764).
+Configs 50-59 (FP8 P.V) and 62-69 are not built and raise NotImplementedError. The reference's "config 3xx" is
+attention_pre (Q operands and K / V statistics from the qkv GEMM epilogue) with a kernel config 80-99.
 """
 import torch
 
@@ -64,6 +69,28 @@ def _production(config, name):
     return True
 
 
+def _block_k(config):
+    """True for configs 60 and 61 (one K scale per 128-key block, attn_fwd6); 62-69 do not exist in the
+    reference's dispatch (attn_int8.cu:2812-2813) and raise."""
+    if config is None or not 60 <= int(config) % 100 < 70:
+        return False
+    if int(config) not in (60, 61):
+        raise NotImplementedError(f"config {int(config)}: the per-block-K kernel is configs 60 and 61 only")
+    return True
+
+
+def _attention_bk(q, k, v, scale, smooth_k, smooth_v, rotate, out):
+    sq, h, _ = q.shape
+    sk = k.shape[0]
+    out = _out(q, out)
+    ws = workspace_u8(sq, sk, h, q.device)
+    nat.call("rh3_int8_attention_bk", nat.ptr(q), q.stride(0), q.stride(1), nat.ptr(k), k.stride(0), k.stride(1),
+             nat.ptr(v), v.stride(0), v.stride(1), sq, sk, h, float(scale), int(bool(smooth_k)),
+             int(bool(smooth_v)), int(bool(rotate)), nat.ptr(out), out.stride(0), out.stride(1), nat.ptr(ws),
+             ws.numel(), nat.stream(q.device))
+    return out
+
+
 def workspace_u8(sq, sk, h, device):
     n = nat.lib().rh3_attention_u8_workspace_bytes(sq, sk, h)
     return torch.empty(n, device=device, dtype=torch.uint8)
@@ -89,6 +116,8 @@ def attention(q, k, v, scale=None, config=None, smooth_k=True, smooth_v=True, ro
     rotate do not apply to it); an int config: the production numerics with smooth_v / rotate."""
     _check_qkv(q, k, v, "attention")
     scale = q.shape[-1] ** -0.5 if scale is None else scale
+    if _block_k(config):
+        return _attention_bk(q, k, v, scale, smooth_k, smooth_v, rotate, out)
     if _production(config, "attention"):
         return _attention_u8("attention", q, k, v, None, scale, 0, 0.0, smooth_k, smooth_v, rotate, out)
     out = _out(q, out)
@@ -129,6 +158,8 @@ def attention_rr(q, k, v, tab, qw, kw, eps, scale=None, config=94, smooth_k=True
     pre-pass; q, k untouched. Self-attention only. The default config 94 is the production numerics, as in
     the reference; config=None runs the per-block bf16 P.V recipe."""
     _check_qkv(q, k, v, "attention_rr", self_only=True)
+    if config is not None and 60 <= int(config) % 100 < 70:
+        raise RuntimeError("configs 60-69 have no fused rms/rope path")    # attn_int8.cu:2606
     tab, qw, kw, rot = _check_rr(q, tab, qw, kw)
     scale = q.shape[-1] ** -0.5 if scale is None else scale
     if _production(config, "attention_rr"):
@@ -340,4 +371,38 @@ def forward_u8(pp, sq, out=None, scale=None, nbias=0, bias=0.0):
     ws = pp["_ws"]
     nat.call("rh3_attention_u8_forward", sq, sk, h, float(scale), int(nbias), float(bias), nat.ptr(out),
              out.stride(0), out.stride(1), nat.ptr(ws), ws.numel(), nat.stream(out.device))
+    return out
+
+
+def prepass_bk(q, k, v, smooth_k=True, smooth_v=True, rotate=True):
+    """Pre-pass operands of configs 60-61 (for verification): dict as prepass_u8() with kbs [H, Skpad/128] fp32
+    (one K scale per 128-key block) in place of ks / ksb."""
+    import ctypes
+    _check_qkv(q, k, v, "prepass_bk")
+    sq, h, _ = q.shape
+    sk = k.shape[0]
+    ws = workspace_u8(sq, sk, h, q.device)
+    ptrs = (ctypes.c_void_p * 9)()
+    nat.call("rh3_attention_bk_prepass", nat.ptr(q), q.stride(0), q.stride(1), nat.ptr(k), k.stride(0), k.stride(1),
+             nat.ptr(v), v.stride(0), v.stride(1), sq, sk, h, int(bool(smooth_k)), int(bool(smooth_v)),
+             int(bool(rotate)), nat.ptr(ws), ws.numel(), ptrs, nat.stream(q.device))
+    vw = _u8_views(ws, ptrs, sq, sk, h)
+    skp = (sk + 127) // 128 * 128
+    vw["kbs"] = vw.pop("ks").reshape(-1)[:h * (skp // 128)].view(h, skp // 128)
+    side = _ptr_views(ws, ptrs, {"s": (4, (h, skp // 128, 512), torch.float32)})["s"]
+    vw["side_kb"] = side[:, :, 0]
+    del vw["ksb"]
+    return vw
+
+
+def forward_bk(pp, sq, out=None, scale=None):
+    """The configs 60-61 main kernel alone on operands prepass_bk() produced: out [Sq, H, 128] bf16."""
+    h = pp["q8"].shape[0]
+    sk = pp["_sk"]
+    scale = D ** -0.5 if scale is None else scale
+    if out is None:
+        out = torch.empty((sq, h, D), device=pp["q8"].device, dtype=torch.bfloat16)
+    ws = pp["_ws"]
+    nat.call("rh3_attention_bk_forward", sq, sk, h, float(scale), nat.ptr(out), out.stride(0), out.stride(1),
+             nat.ptr(ws), ws.numel(), nat.stream(out.device))
     return out

@@ -183,12 +183,32 @@ def attn_u8_case(rng):
     np.savez_compressed(os.path.join(HERE, "attention_u8.npz"), q=q, k=k, v=v, tab=tab, qw=qw, kw=kw, **out)
 
 
-CASES = ("quant", "norm_mod", "heads", "gemm", "attn", "rot", "attn_u8")
+def attn_bk_case(rng):
+    """Per-block-K attention (configs 60-61): plain (300 tokens, a ragged last key tile), without rotation and V
+    smoothing, and cross-attention (300 queries over 200 keys). Outputs rounded to bf16."""
+    s, h = 300, 2
+    q = bf16(rng.standard_normal((s, h, 128)))
+    k = bf16(rng.standard_normal((s, h, 128)) + 2.0 * rng.standard_normal((1, h, 128)))
+    v = bf16(rng.standard_normal((s, h, 128)) + 0.5 * rng.standard_normal((1, h, 128)))
+    sc = 128 ** -0.5
+    keys = ("q8", "qs", "k8", "kbs", "vinit", "v8", "vscale", "vmean", "kmean")
+    out = {}
+    for pre, kw_ in (("", {}), ("n", {"rotate": False, "smooth_v": False})):
+        pp = oa.prepass_blockk(q, k, v, **kw_)
+        out.update({pre + n: pp[n] for n in keys})
+        out[pre + "out"] = bf16(oa.attention_blockk_from_codes(pp, sc)[:s])
+    pp = oa.prepass_blockk(q, k[:200], v[:200])
+    out.update({"c" + n: pp[n] for n in keys if n not in ("q8", "qs")})
+    out["cout"] = bf16(oa.attention_blockk_from_codes(pp, sc)[:s])
+    np.savez_compressed(os.path.join(HERE, "attention_bk.npz"), q=q, k=k, v=v, **out)
+
+
+CASES = ("quant", "norm_mod", "heads", "gemm", "attn", "rot", "attn_u8", "attn_bk")
 
 
 def main(which=CASES):
     """Each group draws from its own fixed stream: the first five share seed 0 in this order, rot uses
-    seed 1 and attn_u8 seed 2, so regenerating one file leaves the others' inputs unchanged."""
+    seed 1, attn_u8 seed 2 and attn_bk seed 3, so regenerating one file leaves the others' inputs unchanged."""
     if set(which) & set(CASES[:5]):
         rng = np.random.default_rng(0)
         quant_case(rng)
@@ -200,6 +220,8 @@ def main(which=CASES):
         rot_case(np.random.default_rng(1))
     if "attn_u8" in which:
         attn_u8_case(np.random.default_rng(2))
+    if "attn_bk" in which:
+        attn_bk_case(np.random.default_rng(3))
     for f in sorted(os.listdir(HERE)):
         if f.endswith(".npz"):
             print(f, os.path.getsize(os.path.join(HERE, f)))

@@ -169,3 +169,75 @@ def test_u8_full_size_sampled(dev):
     assert rel_l2(got, ref) < TOL
     exact = oa.attention_exact(qn, kn, vn, SC, rows=rows)[:, 0]
     assert rel_l2(got, exact) < 0.03
+
+
+# ----------------------------------------------------------------------------- configs 60-61 (per-block K)
+def _check_bk(pp, exp, pre, s_k):
+    for n in ("q8", "qs", "k8", "kbs", "kmean"):
+        if pre + n in exp:
+            assert np.array_equal(to_np(pp[n]), exp[pre + n]), pre + n
+    kb = exp[pre + "kbs"]
+    assert np.array_equal(to_np(pp["side_kb"]), kb), pre + "side kb"
+    for n in ("vinit", "vscale", "vmean"):
+        assert np.array_equal(to_np(pp[n]), exp[pre + n]), pre + n
+    vt = to_np(pp["vt"])
+    keys = _perm_keys_u8(vt.shape[2])
+    vpad = np.zeros((vt.shape[2],) + exp[pre + "v8"].shape[1:], np.int8)
+    vpad[:s_k] = exp[pre + "v8"]
+    assert np.array_equal(vt, vpad[keys].transpose(1, 2, 0)), pre + "vt"
+
+
+def test_bk_prepass_golden(dev, golden):
+    """Configs 60-61's pre-pass: per-token Q codes and scales, per-block K codes and scales (also in the side
+    records the main kernel reads), V codes, accumulator starts, kmean, vscale, vmean bit-exact."""
+    from rapid_h3 import attention
+    g = golden("attention_bk")
+    q, k, v = (to_dev(g[n], dev) for n in ("q", "k", "v"))
+    s = g["q"].shape[0]
+    _check_bk(attention.prepass_bk(q, k, v), g, "", s)
+    _check_bk(attention.prepass_bk(q, k, v, rotate=False, smooth_v=False), g, "n", s)
+    _check_bk(attention.prepass_bk(q, k[:200], v[:200]), g, "c", 200)
+
+
+def test_bk_forward_golden(dev, golden):
+    """attention(config=60 / 61), the drop-in module, no rotation / no V smoothing, cross-attention, and the main
+    kernel alone; within 3 % of exact attention; configs 60-69 refuse the fused RMSNorm + RoPE path."""
+    import torch
+    from rapid_h3 import attention, attn_int8
+    g = golden("attention_bk")
+    q, k, v = (to_dev(g[n], dev) for n in ("q", "k", "v"))
+    s = g["q"].shape[0]
+
+    def check(out, name):
+        got = bf16_to_f32(to_np(out))
+        ref = bf16_to_f32(g[name])
+        assert rel_l2(got, ref) < TOL, (name, rel_l2(got, ref))
+
+    check(attention.attention(q, k, v, config=60), "out")
+    check(attn_int8.attention(q, k, v, config=61), "out")
+    check(attention.attention(q, k, v, config=60, rotate=False, smooth_v=False), "nout")
+    check(attention.attention(q, k[:200], v[:200], config=61), "cout")
+    pp = attention.prepass_bk(q, k, v)
+    assert torch.equal(attention.forward_bk(pp, s), attention.attention(q, k, v, config=60))
+    ex = oa.attention_exact(g["q"], g["k"], g["v"], SC)
+    assert rel_l2(bf16_to_f32(to_np(attention.attention(q, k, v, config=60))), ex) < 0.03
+    tab = torch.zeros(1, s, 1, 48, 2, 2, dtype=torch.bfloat16, device=dev)
+    w = torch.ones(128, dtype=torch.bfloat16, device=dev)
+    with pytest.raises(RuntimeError, match="no fused rms/rope"):
+        attention.attention_rr(q, k, v, tab, w, w, 1e-5, config=60)
+    with pytest.raises(NotImplementedError):
+        attention.attention(q, k, v, config=62)
+
+
+@pytest.mark.parametrize("sq,sk,h", [(1, 1, 1), (127, 129, 2), (256, 256, 1), (257, 600, 3), (1000, 77, 2)])
+def test_bk_shapes(dev, sq, sk, h):
+    """Query blocks around the 256-query workgroup, key tiles around the 128-key tile (the in-kernel pad mask of
+    a ragged last tile), cross-attention in both directions."""
+    from rapid_h3 import attention
+    rng = np.random.default_rng(sq * 5 + sk * 11 + h)
+    q = f32_to_bf16(rng.standard_normal((sq, h, 128)).astype(np.float32))
+    k = f32_to_bf16((rng.standard_normal((sk, h, 128)) + 2 * rng.standard_normal((1, h, 128))).astype(np.float32))
+    v = f32_to_bf16(rng.standard_normal((sk, h, 128)).astype(np.float32))
+    out = attention.attention(to_dev(q, dev), to_dev(k, dev), to_dev(v, dev), config=60)
+    ref = oa.attention_blockk_from_codes(oa.prepass_blockk(q, k, v), SC)[:sq]
+    assert rel_l2(bf16_to_f32(to_np(out)), ref) < TOL

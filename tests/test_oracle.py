@@ -455,6 +455,10 @@ def test_golden_fixtures_regenerate(golden):
     pp = oa.prepass_u8(u["q"], u["k"], u["v"])
     for n in ("q8", "qs", "k8", "ksb", "vinit", "v8", "vscale", "vmean"):
         assert np.array_equal(pp[n], u[n]), n
+    b = golden("attention_bk")
+    pp = oa.prepass_blockk(b["q"], b["k"], b["v"])
+    for n in ("q8", "qs", "k8", "kbs", "vinit", "v8", "vscale", "vmean"):
+        assert np.array_equal(pp[n], b[n]), n
 
 
 # ----------------------------------------------------------------------------- production attention numerics
@@ -583,3 +587,84 @@ def test_attention_u8_accuracy_and_bias():
         p = np.exp(lg - lg.max(axis=1, keepdims=True))
         exb[:, h] = (p @ vf[:, h]) / p.sum(axis=1, keepdims=True)
     assert og.rel_l2(outb, exb) < 0.03 and og.rel_l2(outb, ex) > 0.1
+
+
+def test_block_quant_rot_known_answers():
+    """Configs 60-61's K quantizer: one scale per (head, 128-token block). A block whose only non-zero row is
+    one-hot rotates to +-1/sqrt(128): that row's codes are +-127 with the signs of Sylvester column i and the
+    block's other rows are code 0 under the same scale; without rotation the codes are torch's
+    round(x * (1 / sc)) with sc the block absmax / 127, and a partial last block takes its scale from its own
+    rows only."""
+    from scipy.linalg import hadamard
+    x = np.zeros((200, 2, 128), np.float32)
+    x[3, 0, 5] = 1.0
+    x[140:200, 1] = np.random.default_rng(9).standard_normal((60, 128)).astype(np.float32)
+    x[10, 1, 7] = 50.0
+    codes, kbs = oa.block_quant_rot(x, rotate=True)
+    assert codes.shape == (2, 256, 128) and kbs.shape == (2, 2)
+    assert np.array_equal(codes[0, 3], (127 * hadamard(128)[:, 5]).astype(np.int8))
+    assert not np.delete(codes[0, :128], 3, axis=0).any()
+    assert kbs[0, 0] == np.float32(oa.INV_SQRT128 / np.float32(127))
+    assert kbs[0, 1] == np.float32(np.float32(1e-8) / np.float32(127)) and not codes[0, 128:].any()
+    c2, s2 = oa.block_quant_rot(x, rotate=False)
+    for blk in range(2):
+        t = torch.from_numpy(x[128 * blk:128 * blk + 128, 1])
+        sc = (t.abs().max() / 127).float()
+        assert s2[1, blk] == sc.item()
+        ref = (t * (1.0 / sc)).round()
+        assert np.array_equal(c2[1, 128 * blk:128 * blk + t.shape[0]].astype(np.float32), ref.numpy())
+    assert c2[1, 10, 7] == 127 and not c2[1, 200:].any()
+
+
+def test_prepass_blockk_operands():
+    """Q per token (as the production pre-pass), K per block on K - kmean, V as the production pre-pass."""
+    q, k, v = _u8_inputs(11, s=300)
+    pp = oa.prepass_blockk(q, k, v)
+    pu = oa.prepass_u8(q, k, v)
+    for name in ("q8", "qs", "kmean", "v8", "vscale", "vmean", "vinit"):
+        assert np.array_equal(pp[name], pu[name]), name
+    kc, ks = oa.block_quant_rot((bf16_to_f32(k) - pu["kmean"][None]).astype(np.float32))
+    assert np.array_equal(pp["k8"], kc) and np.array_equal(pp["kbs"], ks) and pp["kbs"].shape == (2, 3)
+
+
+def test_attention_blockk_single_key_and_closed_form():
+    """One key: its P is 255, so the output is that key's dequantized V. Three tiles (300 keys): the online
+    rescaling equals the closed form sum_t 2^(tv_t - M) sum_j P_tj v_j / (same with v = 1), P_tj =
+    rint(2^(fma(acc_j, cc_t, fma(-ti_t, cc_t, log2 255)))), cc_t = c * kb_t, tv_t = ti_t cc_t, keys past Sk
+    excluded; the output is within the reference's error band of exact attention (and a kernel that skips the
+    block scale or the pad mask is not)."""
+    q, k, v = _u8_inputs(12, s=1, sk=1)
+    pp = oa.prepass_blockk(q, k, v)
+    out = oa.attention_blockk_from_codes(pp, 128 ** -0.5)[:1]
+    dq = (pp["v8"].astype(np.float64) * pp["vscale"][None] + pp["vmean"][None]).astype(np.float32)
+    assert np.allclose(out, dq, rtol=0, atol=1e-6)
+    q, k, v = _u8_inputs(13, s=5, sk=300)
+    pp = oa.prepass_blockk(q, k, v)
+    sl2 = np.float32(np.float32(128 ** -0.5) * np.float32(1.4426950408889634))
+    out = oa.attention_blockk_from_codes(pp, 128 ** -0.5)[:5]
+    for h in range(2):
+        acc = (pp["q8"][h, :5].astype(np.int64) @ pp["k8"][h, :300].astype(np.int64).T).astype(np.float64)
+        c = (pp["qs"][h, :5] * sl2).astype(np.float32)[:, None]
+        vq = pp["v8"][:, h].astype(np.float64)
+        parts = []
+        for t, j in enumerate((0, 128, 256)):
+            a = acc[:, j:min(j + 128, 300)]
+            ti = a.max(axis=1, keepdims=True)
+            cc = (c * pp["kbs"][h, t]).astype(np.float32).astype(np.float64)
+            bb = (-(oa.MAGIC + ti) * cc + np.float64(oa.LOG2_255)).astype(np.float32).astype(np.float64)
+            p = np.rint(np.exp2(((oa.MAGIC + a) * cc + bb).astype(np.float32).astype(np.float64)))
+            parts.append(((ti * cc).astype(np.float32).astype(np.float64), p, vq[j:j + a.shape[1]]))
+        mm = np.maximum.reduce([tv for tv, _, _ in parts])
+        num = sum(np.exp2(tv - mm) * (p @ vv) for tv, p, vv in parts)
+        den = sum(np.exp2(tv - mm) * p.sum(axis=1, keepdims=True) for tv, p, _ in parts)
+        ref = num / den * pp["vscale"][h][None] + pp["vmean"][h][None]
+        assert np.allclose(out[:, h], ref, rtol=0, atol=1e-5)
+    q, k, v = _u8_inputs(14, s=300)
+    pp = oa.prepass_blockk(q, k, v)
+    ex = oa.attention_exact(q, k, v, 128 ** -0.5)
+    good = oa.attention_blockk_from_codes(pp, 128 ** -0.5)[:300]
+    assert og.rel_l2(good, ex) < 0.03
+    bad = dict(pp, kbs=np.ones_like(pp["kbs"]))
+    assert og.rel_l2(oa.attention_blockk_from_codes(bad, 128 ** -0.5)[:300], ex) > 0.1
+    unmasked = dict(pp, v8=np.concatenate([pp["v8"], np.zeros((84, 2, 128), np.int8)]))
+    assert og.rel_l2(oa.attention_blockk_from_codes(unmasked, 128 ** -0.5)[:300], good) > 0.01
