@@ -29,12 +29,13 @@ using namespace attn;
 constexpr int BLK = 128;     // quantization block and attention tile (tokens)
 
 // ------------------------------------------------------------------ per-block quantizer
-// grid (Spad/128, H), 256 threads: wave w handles tokens w*32 .. w*32+31 of the block, 4 per pass
+// grid (H, Spad/128) (heads fastest, so the workgroups of one token block run together and share its rope-table
+// rows in L2), 256 threads: wave w handles tokens w*32 .. w*32+31 of the block, 4 per pass
 __global__ void __launch_bounds__(256) quant_kernel(const uint16_t* __restrict__ x, int64_t x_ss, int64_t x_sh,
                                                     int64_t S, int64_t Spad, RR rr, const float* __restrict__ mean,
                                                     int8_t* __restrict__ codes, float* __restrict__ scales) {
   __shared__ float wmax[4];
-  const int h = blockIdx.y, blk = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int h = blockIdx.x, blk = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l16 = lane & 15, sub = lane >> 4;
   float mv[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   if (mean) {
@@ -42,16 +43,21 @@ __global__ void __launch_bounds__(256) quant_kernel(const uint16_t* __restrict__
     const float4 b = *reinterpret_cast<const float4*>(mean + h * D + 8 * l16 + 4);
     mv[0] = a.x; mv[1] = a.y; mv[2] = a.z; mv[3] = a.w; mv[4] = b.x; mv[5] = b.y; mv[6] = b.z; mv[7] = b.w;
   }
+  float w[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  if (rr.tab) load8(rr.w + 8 * l16, w);
   float v[8][8];
   float amax = 0.0f;
 #pragma unroll
   for (int p = 0; p < 8; ++p) {
     const int64_t s = static_cast<int64_t>(blk) * BLK + wave * 32 + p * 4 + sub;
     const bool ok = s < S;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) v[p][e] = 0.0f;
-    if (ok) load8(x + s * x_ss + h * x_sh + 8 * l16, v[p]);
-    if (rr.tab) rms_rope8(v[p], lane, rr, ok ? s : 0);
+    // the row and its rope-table row are loaded together (rows past S read row S - 1 and are zeroed below)
+    const int64_t sl = ok ? s : S - 1;
+    const uint4 rx = *reinterpret_cast<const uint4*>(x + sl * x_ss + h * x_sh + 8 * l16);
+    uint4 rt[4];
+    if (rr.tab) rope_tab8_raw(rr, l16, sl, rt);
+    unpack8(rx, v[p]);
+    if (rr.tab) rms_rope8_raw(v[p], lane, rr, w, rt);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       v[p][e] = ok ? v[p][e] - mv[e] : 0.0f;
@@ -68,17 +74,15 @@ __global__ void __launch_bounds__(256) quant_kernel(const uint16_t* __restrict__
 #pragma unroll
   for (int p = 0; p < 8; ++p) {
     const int64_t s = static_cast<int64_t>(blk) * BLK + wave * 32 + p * 4 + sub;
-    uint32_t b[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float r = fminf(fmaxf(rint_div(v[p][e], sc, inv), -127.0f), 127.0f);
-      b[e] = static_cast<uint32_t>(static_cast<int32_t>(r)) & 0xffu;
-    }
-    uint2 o;
-    o.x = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
-    o.y = b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24);
-    *reinterpret_cast<uint2*>(codes + (static_cast<int64_t>(h) * Spad + s) * D + 8 * l16) = o;
+    // rint(x / sc) clamped to +-127: the multiply by 1/sc decides all lanes but those within 2^-12 of a
+    // half-integer, and one wave vote per 8 values sends only those through the IEEE division
+    *reinterpret_cast<uint2*>(codes + (static_cast<int64_t>(h) * Spad + s) * D + 8 * l16) = quant8_i8(v[p], sc, inv);
   }
+}
+
+void launch_quant(dim3 grid, hipStream_t st, const uint16_t* x, int64_t x_ss, int64_t x_sh, int64_t S, int64_t Spad,
+                  const RR& rr, const float* mean, int8_t* codes, float* scales) {
+  hipLaunchKernelGGL(quant_kernel, grid, dim3(256), 0, st, x, x_ss, x_sh, S, Spad, rr, mean, codes, scales);
 }
 
 // ------------------------------------------------------------------ V transpose
@@ -89,13 +93,13 @@ __device__ __forceinline__ int perm32(int p) {
   return 16 * m + 8 * (e >> 2) + 4 * g + (e & 3);
 }
 
-// grid (Skpad/64, H), 256 threads
+// grid (H, Skpad/64) (heads fastest, so a block's token rows are read together), 256 threads
 __global__ void __launch_bounds__(256) vt_kernel(const uint16_t* __restrict__ v, int64_t v_ss, int64_t v_sh,
                                                  int64_t S, int64_t Spad, uint16_t* __restrict__ vt) {
   constexpr int T = 64, P = D + 8;
   __shared__ uint16_t tile[T * P];
-  const int h = blockIdx.y, tid = threadIdx.x;
-  const int64_t s0 = static_cast<int64_t>(blockIdx.x) * T;
+  const int h = blockIdx.x, tid = threadIdx.x;
+  const int64_t s0 = static_cast<int64_t>(blockIdx.y) * T;
   for (int i = tid; i < T * D / 8; i += 256) {
     const int r = i / (D / 8), c8 = (i % (D / 8)) * 8;
     uint4 val = make_uint4(0, 0, 0, 0);
@@ -425,7 +429,9 @@ int check_qkv(const char* name, const uint16_t* q, int64_t q_ss, int64_t q_sh, c
               int64_t k_sh, const uint16_t* v, int64_t v_ss, int64_t v_sh, int64_t Sq, int64_t Sk, int64_t H) {
   RH3_REQUIRE(Sq > 0 && Sk > 0 && H > 0, "%s: sizes must be positive (Sq=%lld Sk=%lld H=%lld)", name, (long long)Sq,
               (long long)Sk, (long long)H);
-  RH3_REQUIRE(pad(Sq) / BLK < 65536 * 32768ll && H < 65536, "%s: grid too large", name);
+  // the pre-pass grids are (H, token blocks): at most 65,535 blocks of 128 tokens on either side
+  RH3_REQUIRE(pad(Sq) / BLK < 65536 && H < 65536, "%s: Sq=%lld exceeds the 8,388,480-token grid limit", name,
+              (long long)Sq);
   RH3_REQUIRE(pad(Sk) / BLK <= 4096, "%s: Sk=%lld exceeds the 524288-key limit of the attention kernel", name,
               (long long)Sk);
   RH3_REQUIRE(q && k && v, "%s: null q/k/v", name);
@@ -442,18 +448,18 @@ int prepass(const uint16_t* q, int64_t q_ss, int64_t q_sh, const uint16_t* k, in
   const int nchunk = static_cast<int>((Sk + CHUNK - 1) / CHUNK);
   const float* mean = nullptr;
   if (smooth_k) {
-    hipLaunchKernelGGL(stats_kernel, dim3(nchunk, H), dim3(STATS_NT), 0, st, k, k_ss, k_sh, Sk, rk, w.part);
+    launch_stats(dim3(H, nchunk), st, k, k_ss, k_sh, Sk, rk, w.part);
     hipLaunchKernelGGL(kmean_kernel, dim3(H), dim3(KMEAN_NT), 0, st, w.part, nchunk, Sk, w.kmean);
     mean = w.kmean;
   } else {
     // a fill kernel, not hipMemsetAsync, so the call stays safe inside a captured HIP graph
     hipLaunchKernelGGL(zero_kernel, dim3((H * D + 255) / 256), dim3(256), 0, st, w.kmean, H * D);
   }
-  hipLaunchKernelGGL(quant_kernel, dim3(sqp / BLK, H), dim3(256), 0, st, q, q_ss, q_sh, Sq, sqp, rq,
+  launch_quant(dim3(H, sqp / BLK), st, q, q_ss, q_sh, Sq, sqp, rq,
                      static_cast<const float*>(nullptr), w.q8, w.qs);
-  hipLaunchKernelGGL(quant_kernel, dim3(skp / BLK, H), dim3(256), 0, st, k, k_ss, k_sh, Sk, skp, rk, mean, w.k8,
+  launch_quant(dim3(H, skp / BLK), st, k, k_ss, k_sh, Sk, skp, rk, mean, w.k8,
                      w.ks);
-  hipLaunchKernelGGL(vt_kernel, dim3(skp / 64, H), dim3(256), 0, st, v, v_ss, v_sh, Sk, skp, w.vt);
+  hipLaunchKernelGGL(vt_kernel, dim3(H, skp / 64), dim3(256), 0, st, v, v_ss, v_sh, Sk, skp, w.vt);
   return launch_status("attention prepass");
 }
 
@@ -533,9 +539,9 @@ extern "C" int rh3_attention_prepass_qkv(const uint16_t* k, int64_t k_ss, int64_
   } else {
     hipLaunchKernelGGL(zero_kernel, dim3((H * D + 255) / 256), dim3(256), 0, stream, w.kmean, H * D);
   }
-  hipLaunchKernelGGL(quant_kernel, dim3(skp / BLK, H), dim3(256), 0, stream, k, k_ss, k_sh, S, skp, rk, mean, w.k8,
+  launch_quant(dim3(H, skp / BLK), stream, k, k_ss, k_sh, S, skp, rk, mean, w.k8,
                      w.ks);
-  hipLaunchKernelGGL(vt_kernel, dim3(skp / 64, H), dim3(256), 0, stream, v, v_ss, v_sh, S, skp, w.vt);
+  hipLaunchKernelGGL(vt_kernel, dim3(H, skp / 64), dim3(256), 0, stream, v, v_ss, v_sh, S, skp, w.vt);
   if (int e = launch_status("attention prepass_qkv")) return e;
   ptrs[0] = w.q8; ptrs[1] = w.qs; ptrs[2] = w.k8; ptrs[3] = w.ks; ptrs[4] = w.kmean; ptrs[5] = w.vt;
   return RH3_OK;

@@ -21,24 +21,29 @@ typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 // Sums of bf16 values in float64 are exact here (a few hundred thousand values of 8 significant bits within a
 // few dozen binades), so every summation order below gives the same bits.
 //
-// grid (nchunk, H), STATS_NT threads = 16 token slots x 16 lanes
+// grid (H, nchunk) (heads fastest: the workgroups of one chunk run together and share its rope-table rows in
+// L2), STATS_NT threads = 16 token slots x 16 lanes. A row and its rope-table row are loaded together; rows past
+// S read row S - 1 and are not added, so no lane-divergent branch stands between the loads.
 constexpr int STATS_NT = 256;
+template <bool RRON>
 __global__ void __launch_bounds__(STATS_NT) stats_kernel(const uint16_t* __restrict__ k, int64_t k_ss, int64_t k_sh,
                                                     int64_t S, RR rr, double* __restrict__ part) {
   __shared__ double red[16][D];
-  const int h = blockIdx.y, c = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
+  const int h = blockIdx.x, c = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
   const int slot = tid >> 4, l16 = tid & 15;
   double acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  float w[8];
+  if constexpr (RRON) load8(rr.w + 8 * l16, w);
   for (int it = 0; it < CHUNK / 16; ++it) {
     const int64_t s = static_cast<int64_t>(c) * CHUNK + it * 16 + slot;
-    const bool ok = s < S;  // uniform per 16-lane group
-    float x[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    if (ok) load8(k + s * k_ss + h * k_sh + 8 * l16, x);
-    if (rr.tab) {
-      // the shuffles inside rms_rope8 need every lane of the wave; out-of-range rows use token 0's table
-      rms_rope8(x, lane, rr, ok ? s : 0);
-    }
-    if (ok) {
+    const int64_t sl = s < S ? s : S - 1;
+    const uint4 rx = *reinterpret_cast<const uint4*>(k + sl * k_ss + h * k_sh + 8 * l16);
+    uint4 rt[4];
+    if constexpr (RRON) rope_tab8_raw(rr, l16, sl, rt);
+    float x[8];
+    unpack8(rx, x);
+    if constexpr (RRON) rms_rope8_raw(x, lane, rr, w, rt);
+    if (s < S) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc[e] += static_cast<double>(x[e]);
     }
@@ -49,8 +54,15 @@ __global__ void __launch_bounds__(STATS_NT) stats_kernel(const uint16_t* __restr
   if (tid < D) {
     double t = 0.0;
     for (int i = 0; i < 16; ++i) t += red[i][tid];
-    part[(static_cast<int64_t>(h) * gridDim.x + c) * D + tid] = t;
+    part[(static_cast<int64_t>(h) * gridDim.y + c) * D + tid] = t;
   }
+}
+
+// the K statistics of one launch: stats_kernel with or without the RMSNorm + RoPE prologue
+inline void launch_stats(dim3 grid, hipStream_t st, const uint16_t* k, int64_t k_ss, int64_t k_sh, int64_t S,
+                         const RR& rr, double* part) {
+  if (rr.tab) hipLaunchKernelGGL(stats_kernel<true>, grid, dim3(STATS_NT), 0, st, k, k_ss, k_sh, S, rr, part);
+  else hipLaunchKernelGGL(stats_kernel<false>, grid, dim3(STATS_NT), 0, st, k, k_ss, k_sh, S, rr, part);
 }
 
 __global__ void zero_kernel(float* __restrict__ p, int64_t n) {

@@ -23,9 +23,10 @@ __device__ __forceinline__ void load8(const uint16_t* p, float* v) {
 // lane l16 owns channels 8*l16..8*l16+7). Fixed order: per-lane x*x sum over e, then xor 8,4,2,1.
 __device__ __forceinline__ void rms_rope8(float* x, int lane, const RR& rr, int64_t s) {
   const int l16 = lane & 15;
+  // x is a bf16 value, so x * x is exact in fp32 and fma(x, x, ss) rounds exactly as ss + x * x
   float ss = 0.0f;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) ss = ss + x[e] * x[e];
+  for (int e = 0; e < 8; ++e) ss = fmaf(x[e], x[e], ss);
   ss = ss + __shfl_xor(ss, 8, 64);
   ss = ss + __shfl_xor(ss, 4, 64);
   ss = ss + __shfl_xor(ss, 2, 64);
@@ -55,8 +56,10 @@ __device__ __forceinline__ void rms_rope8(float* x, int lane, const RR& rr, int6
     for (int e = 0; e < 8; ++e) {
       const float a = first ? y[e] : py[e];
       const float b = first ? py[e] : y[e];
-      x[e] = first ? round_bf((a * tv[4 * e + 0]) + (b * tv[4 * e + 1]))
-                   : round_bf((a * tv[4 * e + 2]) + (b * tv[4 * e + 3]));
+      // a, b and the table are bf16 values: a * t is exact in fp32, so fma(a, t0, b * t1) rounds exactly as
+      // (a * t0) + (b * t1)
+      x[e] = first ? round_bf(fmaf(a, tv[4 * e + 0], b * tv[4 * e + 1]))
+                   : round_bf(fmaf(a, tv[4 * e + 2], b * tv[4 * e + 3]));
     }
   } else {
 #pragma unroll
@@ -77,11 +80,22 @@ __device__ __forceinline__ void rope_tab8(const RR& rr, int l16, int64_t s, floa
   }
 }
 
+// rope_tab8 with no lane-dependent branch (lanes past rot load pair 0 of the row and ignore it), as raw bf16
+// words, so that a kernel can issue the row and table loads of several tokens before any arithmetic
+__device__ __forceinline__ void rope_tab8_raw(const RR& rr, int l16, int64_t s, uint4* raw) {
+  const int hr = rr.rot >> 1, c0 = 8 * l16;
+  const int i0 = c0 < hr ? c0 : (c0 < rr.rot ? c0 - hr : 0);
+  const uint16_t* t = rr.tab + (s * hr + i0) * 4;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) raw[q] = *reinterpret_cast<const uint4*>(t + 8 * q);
+}
+
 __device__ __forceinline__ void rms_rope8_pre(float* x, int lane, const RR& rr, const float* w, const float* tv) {
   const int l16 = lane & 15;
+  // x is a bf16 value, so x * x is exact in fp32 and fma(x, x, ss) rounds exactly as ss + x * x
   float ss = 0.0f;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) ss = ss + x[e] * x[e];
+  for (int e = 0; e < 8; ++e) ss = fmaf(x[e], x[e], ss);
   ss = ss + __shfl_xor(ss, 8, 64);
   ss = ss + __shfl_xor(ss, 4, 64);
   ss = ss + __shfl_xor(ss, 2, 64);
@@ -104,12 +118,54 @@ __device__ __forceinline__ void rms_rope8_pre(float* x, int lane, const RR& rr, 
     for (int e = 0; e < 8; ++e) {
       const float a = first ? y[e] : py[e];
       const float b = first ? py[e] : y[e];
-      x[e] = first ? round_bf((a * tv[4 * e + 0]) + (b * tv[4 * e + 1]))
-                   : round_bf((a * tv[4 * e + 2]) + (b * tv[4 * e + 3]));
+      // a, b and the table are bf16 values: a * t is exact in fp32, so fma(a, t0, b * t1) rounds exactly as
+      // (a * t0) + (b * t1)
+      x[e] = first ? round_bf(fmaf(a, tv[4 * e + 0], b * tv[4 * e + 1]))
+                   : round_bf(fmaf(a, tv[4 * e + 2], b * tv[4 * e + 3]));
     }
   } else {
 #pragma unroll
     for (int e = 0; e < 8; ++e) x[e] = y[e];
+  }
+}
+
+// rms_rope8_pre on the raw table words of rope_tab8_raw, with no lane-dependent branch. With a, b the pair of the
+// reference's formula, a first-half lane computes round_bf(a t00 + b t01) = round_bf(fma(y, t00, py t01)) and a
+// second-half lane round_bf(a t10 + b t11) = round_bf(fma(y, t11, py t10)) (a = py, b = y there): every product of
+// bf16 values is exact in fp32, so both forms round alike. Each lane therefore needs one coefficient pair (A, B):
+// (t00, t01) from the pair's first word, (t11, t10) from its second word, (1, 0) past rot; v_perm_b32 with
+// per-lane selectors moves the right bf16 halves into place, one instruction per coefficient.
+__device__ __forceinline__ void rms_rope8_raw(float* x, int lane, const RR& rr, const float* w, const uint4* rt) {
+  const int l16 = lane & 15;
+  float ss = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ss = fmaf(x[e], x[e], ss);
+  ss = ss + __shfl_xor(ss, 8, 64);
+  ss = ss + __shfl_xor(ss, 4, 64);
+  ss = ss + __shfl_xor(ss, 2, 64);
+  ss = ss + __shfl_xor(ss, 1, 64);
+  const float r = 1.0f / sqrtf(ss / 128.0f + rr.eps);
+  float y[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) y[e] = round_bf((r * x[e]) * w[e]);
+  const int hr = rr.rot >> 1, step = hr >> 3;
+  const int c0 = 8 * l16;
+  const bool first = c0 < hr, rotl = c0 < rr.rot;
+  const int src = first ? l16 + step : (rotl ? l16 - step : l16);
+  float py[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) py[e] = __shfl(y[e], (lane & ~15) + src, 64);
+  // v_perm_b32(hi, lo, sel): selector bytes 0-3 take lo's bytes, 4-7 hi's, 0x0c gives 0x00
+  const uint32_t sela = first || !rotl ? 0x01000c0cu : 0x07060c0cu;  // A: lo16(word 0) or hi16(word 1)
+  const uint32_t selb = first || !rotl ? 0x03020c0cu : 0x05040c0cu;  // B: hi16(word 0) or lo16(word 1)
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const uint4 q = rt[e >> 1];
+    const uint32_t w0 = rotl ? ((e & 1) ? q.z : q.x) : 0x00003f80u;  // (1.0, 0) past rot
+    const uint32_t w1 = (e & 1) ? q.w : q.y;
+    const float A = __uint_as_float(__builtin_amdgcn_perm(w1, w0, sela));
+    const float B = __uint_as_float(__builtin_amdgcn_perm(w1, w0, selb));
+    x[e] = round_bf(fmaf(y[e], A, py[e] * B));
   }
 }
 

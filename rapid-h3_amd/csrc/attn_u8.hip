@@ -42,28 +42,38 @@ constexpr float LOG2_255 = 7.99435343685886f;       // attn_int8.cu:24
 constexpr float INV_SQRT128 = 0.08838834764831845f;  // attn_int8.cu:127
 
 // ------------------------------------------------------------------ V statistics
-// grid (nchunk, H), 256 threads = 16 token slots x 16 lanes (8 channels each)
+// grid (H, nchunk) (heads fastest, so a chunk's token rows are read together), 256 threads = 16 token slots x 16
+// lanes (8 channels each)
 __global__ void __launch_bounds__(256) vstats_kernel(const uint16_t* __restrict__ v, int64_t v_ss, int64_t v_sh,
                                                      int64_t S, double* __restrict__ vsum,
                                                      float* __restrict__ vmax, float* __restrict__ vmin) {
   __shared__ double red[16][D];
   __shared__ float rmx[16][D], rmn[16][D];
-  const int h = blockIdx.y, c = blockIdx.x, tid = threadIdx.x;
+  const int h = blockIdx.x, c = blockIdx.y, tid = threadIdx.x;
   const int slot = tid >> 4, l16 = tid & 15;
   double acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   float mx[8], mn[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) { mx[e] = -INFINITY; mn[e] = INFINITY; }
-  for (int it = 0; it < CHUNK / 16; ++it) {
-    const int64_t s = static_cast<int64_t>(c) * CHUNK + it * 16 + slot;
-    if (s < S) {
-      float x[8];
-      load8(v + s * v_ss + h * v_sh + 8 * l16, x);
+  // the rows of four iterations are loaded before any is used (rows past S read row S - 1 and are skipped)
+  for (int it0 = 0; it0 < CHUNK / 16; it0 += 4) {
+    uint4 rx[4];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        acc[e] += static_cast<double>(x[e]);
-        mx[e] = fmaxf(mx[e], x[e]);
-        mn[e] = fminf(mn[e], x[e]);
+    for (int i = 0; i < 4; ++i) {
+      const int64_t s = static_cast<int64_t>(c) * CHUNK + (it0 + i) * 16 + slot;
+      rx[i] = *reinterpret_cast<const uint4*>(v + (s < S ? s : S - 1) * v_ss + h * v_sh + 8 * l16);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (static_cast<int64_t>(c) * CHUNK + (it0 + i) * 16 + slot < S) {
+        float x[8];
+        unpack8(rx[i], x);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          acc[e] += static_cast<double>(x[e]);
+          mx[e] = fmaxf(mx[e], x[e]);
+          mn[e] = fminf(mn[e], x[e]);
+        }
       }
     }
   }
@@ -82,7 +92,7 @@ __global__ void __launch_bounds__(256) vstats_kernel(const uint16_t* __restrict_
       a = fmaxf(a, rmx[i][tid]);
       b = fminf(b, rmn[i][tid]);
     }
-    const int64_t o = (static_cast<int64_t>(h) * gridDim.x + c) * D + tid;
+    const int64_t o = (static_cast<int64_t>(h) * gridDim.y + c) * D + tid;
     vsum[o] = t;
     vmax[o] = a;
     vmin[o] = b;
@@ -148,9 +158,21 @@ __global__ void __launch_bounds__(256) tokq_kernel(const uint16_t* __restrict__ 
     }
     return;
   }
+  // the row, the rope-table row and the norm weights are loaded together, before any arithmetic
+  const uint4 rx = *reinterpret_cast<const uint4*>(x + s * x_ss + h * x_sh + 8 * l16);
+  uint4 rt[4];
+  uint4 rw = make_uint4(0, 0, 0, 0);
+  if (rr.tab) {
+    rope_tab8_raw(rr, l16, s, rt);
+    rw = *reinterpret_cast<const uint4*>(rr.w + 8 * l16);
+  }
   float v[8];
-  load8(x + s * x_ss + h * x_sh + 8 * l16, v);
-  if (rr.tab) rms_rope8(v, lane, rr, s);
+  unpack8(rx, v);
+  if (rr.tab) {
+    float w[8];
+    unpack8(rw, w);
+    rms_rope8_raw(v, lane, rr, w, rt);
+  }
   if (mean) {
     float m[8];
     const float4 a = *reinterpret_cast<const float4*>(mean + h * D + 8 * l16);
@@ -173,7 +195,7 @@ __global__ void __launch_bounds__(256) tokq_kernel(const uint16_t* __restrict__ 
 }
 
 // ------------------------------------------------------------------ per-block K (configs 60-61)
-// grid (Skpad / 128, H), 256 threads: wave w quantizes tokens 32 w .. 32 w + 31 of the block, four 16-lane rows
+// grid (H, Skpad / 128) (heads fastest), 256 threads: wave w quantizes tokens 32 w .. 32 w + 31 of the block, four 16-lane rows
 // per pass. K - kmean -> [normalized H128] -> one scale per (head, 128-key block) sc = max(amax, 1e-8) / 127,
 // codes rint(x * (1 / sc)) (quant_k_block, attn_int8.cu:404-443); sc goes to kbs [H][Skpad/128] and to the first
 // float of the block's side record, where the main kernel reads it. Padded tokens are zero rows.
@@ -182,7 +204,7 @@ __global__ void __launch_bounds__(256) blockk_kernel(const uint16_t* __restrict_
                                                      int rotate, int8_t* __restrict__ codes,
                                                      float* __restrict__ kbs, float* __restrict__ side) {
   __shared__ float wmax[4];
-  const int h = blockIdx.y, blk = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int h = blockIdx.x, blk = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l16 = lane & 15, sub = lane >> 4;
   float m[8];
   {
@@ -239,15 +261,15 @@ __device__ __forceinline__ int perm_u8(int p) {
   return 8 * (r >> 2) + 4 * g + (r & 3);
 }
 
-// grid (Skpad / 128, H), 256 threads
+// grid (H, Skpad / 128) (heads fastest), 256 threads
 __global__ void __launch_bounds__(256) vq_kernel(const uint16_t* __restrict__ v, int64_t v_ss, int64_t v_sh,
                                                  int64_t S, int64_t Spad, const float* __restrict__ vmean,
                                                  const float* __restrict__ vscale, int8_t* __restrict__ vt,
                                                  int32_t* __restrict__ side) {
   constexpr int P = D + 16;  // row pitch of the key-major code tile
   __shared__ int8_t tile[TILE * P];
-  const int h = blockIdx.y, tid = threadIdx.x, l16 = tid & 15;
-  const int64_t s0 = static_cast<int64_t>(blockIdx.x) * TILE;
+  const int h = blockIdx.x, tid = threadIdx.x, l16 = tid & 15;
+  const int64_t s0 = static_cast<int64_t>(blockIdx.y) * TILE;
   float vm[8], vs[8], iv[8];
   {
     const float4 a = *reinterpret_cast<const float4*>(vmean + h * D + 8 * l16);
@@ -289,7 +311,7 @@ __global__ void __launch_bounds__(256) vq_kernel(const uint16_t* __restrict__ v,
         make_uint4(w[0], w[1], w[2], w[3]);
   }
   // accumulator starts: 1.5*2^23 bits + 128 * (sum of the tile's codes of channel d); the pad is zeroed
-  int32_t* rec = side + (static_cast<int64_t>(h) * (Spad / TILE) + blockIdx.x) * (SIDE / 4);
+  int32_t* rec = side + (static_cast<int64_t>(h) * (Spad / TILE) + blockIdx.y) * (SIDE / 4);
   if (tid < D) {
     int sum = 0;
     for (int k = 0; k < TILE; ++k) sum += static_cast<int8_t>(tile[k * P + tid]);
@@ -611,6 +633,8 @@ int check_qkv_u8(const char* name, const uint16_t* q, int64_t q_ss, int64_t q_sh
               (long long)Sk, (long long)H);
   RH3_REQUIRE(H < 65536 && (Sq + U8_BQ - 1) / U8_BQ < (1ll << 31), "%s: grid too large", name);
   RH3_REQUIRE(padk(Sq) * H < (1ll << 31) && padk(Sk) * H < (1ll << 31), "%s: Spad * H must stay below 2^31", name);
+  // the key-side pre-pass grids are (H, key blocks): at most 65,535 blocks of 128 keys
+  RH3_REQUIRE(padk(Sk) / TILE < 65536, "%s: Sk=%lld exceeds the 8,388,480-key grid limit", name, (long long)Sk);
   RH3_REQUIRE(q && k && v, "%s: null q/k/v", name);
   RH3_REQUIRE(aligned16(q) && aligned16(k) && aligned16(v), "%s: q/k/v must be 16-byte aligned", name);
   RH3_REQUIRE(q_ss % 8 == 0 && q_sh % 8 == 0 && k_ss % 8 == 0 && k_sh % 8 == 0 && v_ss % 8 == 0 && v_sh % 8 == 0,
@@ -632,21 +656,21 @@ int prepass_u8(const uint16_t* q, int64_t q_ss, int64_t q_sh, const uint16_t* k,
   const int nchunk = static_cast<int>((Sk + CHUNK - 1) / CHUNK);
   const float* mean = nullptr;
   if (smooth_k) {
-    hipLaunchKernelGGL(stats_kernel, dim3(nchunk, H), dim3(STATS_NT), 0, st, k, k_ss, k_sh, Sk, rk, w.kpart);
+    launch_stats(dim3(H, nchunk), st, k, k_ss, k_sh, Sk, rk, w.kpart);
     hipLaunchKernelGGL(kmean_kernel, dim3(H), dim3(KMEAN_NT), 0, st, w.kpart, nchunk, Sk, w.kmean);
     mean = w.kmean;
   } else {
     // a fill kernel, not hipMemsetAsync, so the call stays safe inside a captured HIP graph
     hipLaunchKernelGGL(zero_kernel, dim3((H * D + 255) / 256), dim3(256), 0, st, w.kmean, H * D);
   }
-  hipLaunchKernelGGL(vstats_kernel, dim3(nchunk, H), dim3(256), 0, st, v, v_ss, v_sh, Sk, w.vsum, w.vmax, w.vmin);
+  hipLaunchKernelGGL(vstats_kernel, dim3(H, nchunk), dim3(256), 0, st, v, v_ss, v_sh, Sk, w.vsum, w.vmax, w.vmin);
   hipLaunchKernelGGL(vfinal_kernel, dim3(H), dim3(VFINAL_NT), 0, st, w.vsum, w.vmax, w.vmin, nchunk, Sk, smooth_v, w.vmean,
                      w.vscale);
   hipLaunchKernelGGL(tokq_kernel, dim3(sqp * H / 16), dim3(256), 0, st, q, q_ss, q_sh, Sq, sqp, H, rq,
                      static_cast<const float*>(nullptr), rotate, w.q8, w.qs, static_cast<float*>(nullptr));
   hipLaunchKernelGGL(tokq_kernel, dim3(skp * H / 16), dim3(256), 0, st, k, k_ss, k_sh, Sk, skp, H, rk, mean, rotate,
                      w.k8, w.ks, reinterpret_cast<float*>(w.side));
-  hipLaunchKernelGGL(vq_kernel, dim3(skp / TILE, H), dim3(256), 0, st, v, v_ss, v_sh, Sk, skp, w.vmean, w.vscale,
+  hipLaunchKernelGGL(vq_kernel, dim3(H, skp / TILE), dim3(256), 0, st, v, v_ss, v_sh, Sk, skp, w.vmean, w.vscale,
                      w.vt, reinterpret_cast<int32_t*>(w.side));
   return launch_status("attention_u8 prepass");
 }
@@ -669,19 +693,19 @@ int prepass_bk(const uint16_t* q, int64_t q_ss, int64_t q_sh, const uint16_t* k,
   const int nchunk = static_cast<int>((Sk + CHUNK - 1) / CHUNK);
   const RR none{nullptr, nullptr, 0.f, 0};
   if (smooth_k) {
-    hipLaunchKernelGGL(stats_kernel, dim3(nchunk, H), dim3(STATS_NT), 0, st, k, k_ss, k_sh, Sk, none, w.kpart);
+    launch_stats(dim3(H, nchunk), st, k, k_ss, k_sh, Sk, none, w.kpart);
     hipLaunchKernelGGL(kmean_kernel, dim3(H), dim3(KMEAN_NT), 0, st, w.kpart, nchunk, Sk, w.kmean);
   } else {
     hipLaunchKernelGGL(zero_kernel, dim3((H * D + 255) / 256), dim3(256), 0, st, w.kmean, H * D);
   }
-  hipLaunchKernelGGL(vstats_kernel, dim3(nchunk, H), dim3(256), 0, st, v, v_ss, v_sh, Sk, w.vsum, w.vmax, w.vmin);
+  hipLaunchKernelGGL(vstats_kernel, dim3(H, nchunk), dim3(256), 0, st, v, v_ss, v_sh, Sk, w.vsum, w.vmax, w.vmin);
   hipLaunchKernelGGL(vfinal_kernel, dim3(H), dim3(VFINAL_NT), 0, st, w.vsum, w.vmax, w.vmin, nchunk, Sk, smooth_v,
                      w.vmean, w.vscale);
   hipLaunchKernelGGL(tokq_kernel, dim3(sqp * H / 16), dim3(256), 0, st, q, q_ss, q_sh, Sq, sqp, H, none,
                      static_cast<const float*>(nullptr), rotate, w.q8, w.qs, static_cast<float*>(nullptr));
-  hipLaunchKernelGGL(blockk_kernel, dim3(skp / TILE, H), dim3(256), 0, st, k, k_ss, k_sh, Sk, skp,
+  hipLaunchKernelGGL(blockk_kernel, dim3(H, skp / TILE), dim3(256), 0, st, k, k_ss, k_sh, Sk, skp,
                      static_cast<const float*>(w.kmean), rotate, w.k8, w.ks, reinterpret_cast<float*>(w.side));
-  hipLaunchKernelGGL(vq_kernel, dim3(skp / TILE, H), dim3(256), 0, st, v, v_ss, v_sh, Sk, skp, w.vmean, w.vscale,
+  hipLaunchKernelGGL(vq_kernel, dim3(H, skp / TILE), dim3(256), 0, st, v, v_ss, v_sh, Sk, skp, w.vmean, w.vscale,
                      w.vt, reinterpret_cast<int32_t*>(w.side));
   return launch_status("attention_bk prepass");
 }
@@ -796,7 +820,7 @@ extern "C" int rh3_attention_u8_prepass_qkv(const uint16_t* k, int64_t k_ss, int
                      w.vscale);
   hipLaunchKernelGGL(tokq_kernel, dim3(skp * H / 16), dim3(256), 0, stream, k, k_ss, k_sh, S, skp, H, rk, mean, rotate,
                      w.k8, w.ks, reinterpret_cast<float*>(w.side));
-  hipLaunchKernelGGL(vq_kernel, dim3(skp / TILE, H), dim3(256), 0, stream, v, v_ss, v_sh, S, skp, w.vmean, w.vscale,
+  hipLaunchKernelGGL(vq_kernel, dim3(H, skp / TILE), dim3(256), 0, stream, v, v_ss, v_sh, S, skp, w.vmean, w.vscale,
                      w.vt, reinterpret_cast<int32_t*>(w.side));
   if (int e = launch_status("attention_u8 prepass_qkv")) return e;
   ptrs[0] = w.q8; ptrs[1] = w.qs; ptrs[2] = w.k8; ptrs[3] = w.ks; ptrs[4] = w.side; ptrs[5] = w.vt;
