@@ -324,6 +324,45 @@ int rh3_attention_bk_forward(int64_t Sq, int64_t Sk, int64_t H, float scale,
                              uint16_t* out, int64_t o_ss, int64_t o_sh,
                              void* workspace, int64_t workspace_bytes, hipStream_t stream);
 
+/* ---------------------------------------------------------------------------------------------
+ * INT8 flash attention with FP8 P.V (attn_int8.cu configs 50-56: attn_fwd5 :1563-1785, quant_v's fp8 branch
+ * :467-473). Q and K as the production numerics (per-token H128-rotated codes, per-key (scale, bias) pairs);
+ * V per channel as e4m3 codes of ((v - vmean) / vscale) * fp32(448 / 127). Per group of `tile` keys (64 or 128,
+ * the reference's BN): the running max m grows to the group max (O and l scaled by 2^((m_old - m) c)),
+ * P = e4m3(2^(fma(t, c, log2 448 - m c))), l += P unquantized, O += P . V on the FP8 MFMA in fp32; out =
+ * bf16(O / l * vscale * fp32(127 / 448) + vmean). RMSNorm + RoPE as the production entry points (tab != NULL),
+ * no text bias. Workspace as rh3_attention_u8_workspace_bytes.
+ * ------------------------------------------------------------------------------------------- */
+
+/* replaces attn_int8.attention / attention_rr with config 50-56 (or 150-156) -> int8_attention(_rr)
+ * (attn_int8.py:30-47, attn_int8.cu:2660-2676, :2804-2810). tile: 64 for configs 50, 51, 54, 56, 128 for 52,
+ * 53, 55. */
+int rh3_int8_attention_f8(const uint16_t* q, int64_t q_ss, int64_t q_sh,
+                          const uint16_t* k, int64_t k_ss, int64_t k_sh,
+                          const uint16_t* v, int64_t v_ss, int64_t v_sh,
+                          int64_t Sq, int64_t Sk, int64_t H, const uint16_t* tab, int rot,
+                          const uint16_t* qw, const uint16_t* kw, float eps, float scale, int tile,
+                          int smooth_k, int smooth_v, int rotate,
+                          uint16_t* out, int64_t o_ss, int64_t o_sh,
+                          void* workspace, int64_t workspace_bytes, hipStream_t stream);
+
+/* Pre-pass operands of configs 50-56 for verification (the reference's int8_prepass with config 50): ptrs as
+ * rh3_attention_u8_prepass, with vt [H, 128, Skpad] e4m3 codes (keys permuted within 64-key chunks) and the
+ * side records' accumulator starts unused. */
+int rh3_attention_f8_prepass(const uint16_t* q, int64_t q_ss, int64_t q_sh,
+                             const uint16_t* k, int64_t k_ss, int64_t k_sh,
+                             const uint16_t* v, int64_t v_ss, int64_t v_sh,
+                             int64_t Sq, int64_t Sk, int64_t H, const uint16_t* tab, int rot,
+                             const uint16_t* qw, const uint16_t* kw, float eps,
+                             int smooth_k, int smooth_v, int rotate,
+                             void* workspace, int64_t workspace_bytes, void** ptrs /* [9] */,
+                             hipStream_t stream);
+
+/* The FP8 P.V main kernel alone, on a workspace rh3_attention_f8_prepass filled for (Sq, Sk, H). */
+int rh3_attention_f8_forward(int64_t Sq, int64_t Sk, int64_t H, float scale, int tile,
+                             uint16_t* out, int64_t o_ss, int64_t o_sh,
+                             void* workspace, int64_t workspace_bytes, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

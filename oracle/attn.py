@@ -387,3 +387,73 @@ def attention_blockk_from_codes(pp, scale, rows=None, heads=None, sk=None):
             o = o * a + ts * (p @ vp[j0:j0 + TILE].astype(np.float64))
         out[:, hi] = (o / l * pp["vscale"][h][None].astype(np.float64) + pp["vmean"][h][None]).astype(F32)
     return out
+
+
+LOG2_448 = F32(8.807354922057604)      # attn_int8.cu:1557
+V_FP8_STRETCH = F32(F32(448.0) / F32(127.0))   # attn_int8.cu:468 (r = 448.f / 127.f)
+V_FP8_UNSTRETCH = F32(F32(127.0) / F32(448.0))  # attn_int8.cu:2642 (vscale *= 127.f / 448.f)
+
+
+def v_fp8(v, smooth_v=True):
+    """V [S, H, D] (bf16 bits) -> (e4m3fn codes [S, H, D] uint8, vscale [H, D], vmean [H, D]) for the FP8 P.V
+    configs (attn_int8.cu:467-473): code = e4m3(satfinite(((v - vmean) / vscale) * fp32(448 / 127))), vscale and
+    vmean as v_int8 (the kernel's epilogue multiplies vscale by fp32(127 / 448), :2642)."""
+    from .numerics import f32_to_fp8_e4m3
+    vf = _as_f32(v)
+    _, sc, vm = v_int8(v, smooth_v)
+    x = (((vf - vm[None]).astype(F32) / sc[None]).astype(F32) * V_FP8_STRETCH).astype(F32)
+    return f32_to_fp8_e4m3(np.clip(x, F32(-448.0), F32(448.0))), sc, vm
+
+
+def prepass_fp8v(q, k, v, rr=None, smooth_k=True, smooth_v=True, rotate=True):
+    """Pre-pass operands of the FP8 P.V configs 50-56 (attn_int8.cu:2568-2644 with fp8v): Q / K as prepass_u8
+    (per-token codes and scales, per-key (scale, bias) pairs), V as e4m3 codes (v_fp8)."""
+    pp = prepass_u8(q, k, v, rr, smooth_k, smooth_v, rotate)
+    vf8, vs, vm = v_fp8(v, smooth_v)
+    pp.update(vf8=vf8, vscale=vs, vmean=vm)
+    for n in ("v8", "vinit"):
+        pp.pop(n)
+    return pp
+
+
+def attention_fp8pv_from_codes(pp, scale, rows=None, heads=None, sk=None, tile=64):
+    """The FP8 P.V main kernel (attn_fwd5, attn_int8.cu:1563-1785) on prepass_fp8v's operands, tile by tile (tile =
+    64 keys for configs 50, 51, 54, 56, 128 for 52, 53, 55): t = fma(1.5*2^23 + acc, s_key, b_key), tile max tm;
+    where tm exceeds the running max m: n = max(m, tm), O and l scaled by 2^((m - n) c), m = n; then
+    p = 2^(fma(t, c, fma(-m, c, log2 448))) (0 < p <= 448), l += p (unquantized), O += e4m3(p) . e4m3 V;
+    out = O / l * (vscale * fp32(127 / 448)) + vmean. 2^x in float64 from the fp32 argument, the sums in float64
+    (the kernels' exp2 is a hardware approximation and their sums are fp32). Returns fp32 [rows, heads, D]."""
+    from .numerics import f32_to_fp8_e4m3, fp8_e4m3_to_f32
+    q8, qs, k8, ksb, vf8 = pp["q8"], pp["qs"], pp["k8"], pp["ksb"], pp["vf8"]
+    sk = vf8.shape[0] if sk is None else sk
+    skp = spad(sk)
+    hh = range(q8.shape[0]) if heads is None else heads
+    rows = np.arange(q8.shape[1]) if rows is None else np.asarray(rows)
+    sl2 = F32(F32(scale) * F32(1.4426950408889634))
+    out = np.zeros((len(rows), len(hh), D), F32)
+    for hi, h in enumerate(hh):
+        vp = np.zeros((skp, D), np.float64)
+        vp[:sk] = fp8_e4m3_to_f32(vf8[:, h])
+        acc = q8[h, rows].astype(np.float64) @ k8[h, :skp].astype(np.float64).T
+        with np.errstate(invalid="ignore"):
+            t = _fma32((MAGIC + acc).astype(F32), ksb[h, :skp, 0][None], ksb[h, :skp, 1][None])
+        c = (qs[h, rows] * sl2).astype(F32)[:, None]
+        m = np.full((len(rows), 1), -np.inf, F32)
+        l = np.zeros((len(rows), 1))
+        o = np.zeros((len(rows), D))
+        for j0 in range(0, skp, tile):
+            tt = t[:, j0:j0 + tile]
+            tm = tt.max(axis=1, keepdims=True)
+            n = np.maximum(m, tm)
+            with np.errstate(invalid="ignore"):
+                a = np.nan_to_num(np.exp2(((m - n).astype(F32) * c).astype(F32).astype(np.float64)), nan=0.0)
+            o, l, m = o * a, l * a, n
+            b = _fma32(-m, c, LOG2_448)
+            with np.errstate(invalid="ignore"):
+                p = np.nan_to_num(np.exp2(_fma32(tt, c, b).astype(np.float64)), nan=0.0).astype(F32)
+            l = l + p.astype(np.float64).sum(axis=1, keepdims=True)
+            p8 = fp8_e4m3_to_f32(f32_to_fp8_e4m3(np.minimum(p, F32(448.0)))).astype(np.float64)
+            o = o + p8 @ vp[j0:j0 + tile]
+        vs = (pp["vscale"][h] * V_FP8_UNSTRETCH).astype(F32).astype(np.float64)
+        out[:, hi] = (o / l * vs[None] + pp["vmean"][h][None]).astype(F32)
+    return out

@@ -39,6 +39,9 @@ constexpr int SIDE_VINIT = 1024;          // byte offset of the accumulator star
 constexpr int MAGIC_I = 0x4B400000;       // bits of 1.5 * 2^23
 constexpr float MAGIC_F = 12582912.0f;
 constexpr float LOG2_255 = 7.99435343685886f;       // attn_int8.cu:24
+constexpr float LOG2_448 = 8.807354922057604f;      // attn_int8.cu:1557
+constexpr float V_STRETCH = 448.0f / 127.0f;        // attn_int8.cu:468
+constexpr float V_UNSTRETCH = 127.0f / 448.0f;      // attn_int8.cu:2642
 constexpr float INV_SQRT128 = 0.08838834764831845f;  // attn_int8.cu:127
 
 // ------------------------------------------------------------------ V statistics
@@ -261,7 +264,17 @@ __device__ __forceinline__ int perm_u8(int p) {
   return 8 * (r >> 2) + 4 * g + (r & 3);
 }
 
-// grid (H, Skpad / 128) (heads fastest), 256 threads
+// Position p of a 64-key chunk of the e4m3 layout holds key perm_f8(p): p = 32 g + 16 h + r <-> key 32 h + 8 (r / 4)
+// + 4 g + r % 4, the key of register r of 32-key block h in lane group g's S^T accumulator, so that a lane's 32 P
+// bytes of the chunk are its B operand of the 64-deep FP8 MFMA.
+__device__ __forceinline__ int perm_f8(int p) {
+  const int g = p >> 5, hh = (p >> 4) & 1, r = p & 15;
+  return 32 * hh + 8 * (r >> 2) + 4 * g + (r & 3);
+}
+
+// grid (H, Skpad / 128) (heads fastest), 256 threads. F8 (configs 50-56): e4m3 codes of ((v - vmean) / vscale) *
+// fp32(448 / 127) (attn_int8.cu:467-473) in the perm_f8 order, and no accumulator starts.
+template <bool F8>
 __global__ void __launch_bounds__(256) vq_kernel(const uint16_t* __restrict__ v, int64_t v_ss, int64_t v_sh,
                                                  int64_t S, int64_t Spad, const float* __restrict__ vmean,
                                                  const float* __restrict__ vscale, int8_t* __restrict__ vt,
@@ -287,12 +300,20 @@ __global__ void __launch_bounds__(256) vq_kernel(const uint16_t* __restrict__ v,
     if (s0 + r < S) {
       float x[8];
       load8(v + (s0 + r) * v_ss + h * v_sh + 8 * l16, x);
-      uint32_t b[8];
+      if constexpr (F8) {
+        float y[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e)
-        b[e] = static_cast<uint32_t>(static_cast<int32_t>(rint_div(x[e] - vm[e], vs[e], iv[e]))) & 0xffu;
-      o.x = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
-      o.y = b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24);
+        for (int e = 0; e < 8; ++e) y[e] = fminf(fmaxf(((x[e] - vm[e]) / vs[e]) * V_STRETCH, -448.0f), 448.0f);
+        o.x = __builtin_amdgcn_cvt_pk_fp8_f32(y[2], y[3], __builtin_amdgcn_cvt_pk_fp8_f32(y[0], y[1], 0, false), true);
+        o.y = __builtin_amdgcn_cvt_pk_fp8_f32(y[6], y[7], __builtin_amdgcn_cvt_pk_fp8_f32(y[4], y[5], 0, false), true);
+      } else {
+        uint32_t b[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          b[e] = static_cast<uint32_t>(static_cast<int32_t>(rint_div(x[e] - vm[e], vs[e], iv[e]))) & 0xffu;
+        o.x = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
+        o.y = b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24);
+      }
     }
     *reinterpret_cast<uint2*>(&tile[r * P + 8 * l16]) = o;
   }
@@ -304,13 +325,14 @@ __global__ void __launch_bounds__(256) vq_kernel(const uint16_t* __restrict__ v,
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
       const int p = pc + e;
-      const int key = (p & ~31) + perm_u8(p & 31);
+      const int key = F8 ? (p & ~63) + perm_f8(p & 63) : (p & ~31) + perm_u8(p & 31);
       w[e >> 2] |= (static_cast<uint32_t>(static_cast<uint8_t>(tile[key * P + d]))) << (8 * (e & 3));
     }
     *reinterpret_cast<uint4*>(vt + (static_cast<int64_t>(h) * D + d) * Spad + s0 + pc) =
         make_uint4(w[0], w[1], w[2], w[3]);
   }
   // accumulator starts: 1.5*2^23 bits + 128 * (sum of the tile's codes of channel d); the pad is zeroed
+  if constexpr (F8) return;
   int32_t* rec = side + (static_cast<int64_t>(h) * (Spad / TILE) + blockIdx.y) * (SIDE / 4);
   if (tid < D) {
     int sum = 0;
@@ -361,8 +383,14 @@ __device__ __forceinline__ float max3f(float a, float b, float c) {
 // instead of the per-key pairs: the tile max is the integer max ti of the raw accumulators (keys past Sk forced to
 // 1.5*2^23 - 2^22 first), cc = c kb, tv = (ti - 1.5*2^23) cc, n = max(m, tv), a = 2^(m - n), ts = 2^(tv - n),
 // P = rint(2^(fma(acc bits, cc, fma(-ti bits, cc, log2 255)))); the P.V, row sums and fold are the same.
-template <bool BK>
+// MODE 2 (FP8 P.V, configs 50-56, attn_fwd5 :1563-1785): the per-key dequant of MODE 0, then per group of MAXG keys
+// (64 or 128, the reference's tile) the group max updates the running max m exactly (O and l scaled by
+// 2^((m_old - m) c) when it grows), P = 2^(fma(t, c, fma(-m, c, log2 448))) in e4m3 (v_cvt_pk_fp8_f32: OCP e4m3fn,
+// round to nearest even), l += P unquantized, and O^T += V^T . P^T on v_mfma_scale_f32_32x32x64_f8f6f4 (e4m3 V
+// from vq_kernel<true>) straight into the fp32 accumulators: no per-tile fold.
+template <int MODE, int MAXG = 128>
 __global__ void __launch_bounds__(U8_NT, 1) attn_u8_kernel(const U8Args a) {
+  constexpr bool BK = MODE == 1;
   constexpr int KB = TILE * D, VB = D * TILE, SLOT = KB + VB + SIDE;
   __shared__ __attribute__((aligned(16))) int8_t ring[4 * SLOT];
   const int h = blockIdx.y, qb = blockIdx.x;
@@ -423,6 +451,16 @@ __global__ void __launch_bounds__(U8_NT, 1) attn_u8_kernel(const U8Args a) {
   // 32 db + 8 i + 4 g .. +3 at SIDE_VINIT + 4 d
   const uint32_t soff = ring_lds + KB + VB + 32 * g;
   const uint32_t ioff = ring_lds + KB + VB + SIDE_VINIT + 16 * g;
+  // MODE 2: the e4m3 V^T fragment (db, 64-key chunk cc) of lane (l32, g) is logical chunks 4 cc + 2 g + h (h = 0, 1)
+  // of row 32 db + l32, stored at chunk ^ ((row ^ (row >> 3)) & 7) = (4 (cc ^ (db & 1)) + 2 g + h) ^ y2
+  uint32_t voff8[2][2];
+  {
+    const int y2 = (l32 ^ (l32 >> 3)) & 7;
+#pragma unroll
+    for (int c2 = 0; c2 < 2; ++c2)
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) voff8[c2][hh] = ring_lds + KB + l32 * 128 + (((4 * c2 + 2 * g + hh) ^ y2) << 4);
+  }
 
   v16f o[4];
 #pragma unroll
@@ -568,6 +606,83 @@ __global__ void __launch_bounds__(U8_NT, 1) attn_u8_kernel(const U8Args a) {
     }
   };
 
+  auto softmax_pv_f8 = [&](const int j) __attribute__((always_inline)) {
+    const uint32_t so = static_cast<uint32_t>(j & 3) * SLOT;
+    float t[4][16];
+    // t of blocks kb0 .. kb1 - 1 (MAXG 64: per 64-key chunk, so that only one chunk's scores are live at a time)
+    auto dequant = [&](const int kb0, const int kb1) __attribute__((always_inline)) {
+#pragma unroll
+    for (int kb = kb0; kb < kb1; ++kb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const v4i p01 = *reinterpret_cast<lds_v4i_u8*>(static_cast<uintptr_t>(soff + so + kb * 256 + i * 64));
+        const v4i p23 = *reinterpret_cast<lds_v4i_u8*>(static_cast<uintptr_t>(soff + so + kb * 256 + i * 64 + 16));
+        const float ps[4] = {__int_as_float(p01[0]), __int_as_float(p01[2]), __int_as_float(p23[0]),
+                             __int_as_float(p23[2])};
+        const float pb[4] = {__int_as_float(p01[1]), __int_as_float(p01[3]), __int_as_float(p23[1]),
+                             __int_as_float(p23[3])};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) t[kb][4 * i + e] = fmaf(__int_as_float(s[kb][4 * i + e]), ps[e], pb[e]);
+      }
+    };
+    if constexpr (MAXG == 128) dequant(0, 4);
+    float bb = 0.0f;
+#pragma unroll
+    for (int cc = 0; cc < 2; ++cc) {
+      if constexpr (MAXG == 64) dequant(2 * cc, 2 * cc + 2);
+      if (MAXG == 64 || cc == 0) {
+        float tm = -INFINITY;
+#pragma unroll
+        for (int kb = 2 * cc; kb < 2 * cc + MAXG / 32; ++kb)
+#pragma unroll
+          for (int r = 0; r < 16; r += 2) tm = max3f(tm, t[kb][r], t[kb][r + 1]);
+        {
+          const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_int(tm), __float_as_int(tm), false, false);
+          tm = fmaxf(__int_as_float(sw[0]), __int_as_float(sw[1]));
+        }
+        if (__builtin_amdgcn_ballot_w64(tm > mx) != 0) {  // a = 1 exactly on the rows whose max stays
+          const float n = fmaxf(mx, tm);
+          const float al = __builtin_amdgcn_exp2f((mx - n) * c);
+          lrow = lrow * al;
+#pragma unroll
+          for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o[db][r] = o[db][r] * al;
+          mx = n;
+        }
+        bb = fmaf(-mx, c, LOG2_448);
+      }
+      // P of the chunk's two 32-key blocks in e4m3, four per word: the B operand of the 64-deep MFMA
+      v8i pf;
+#pragma unroll
+      for (int hb = 0; hb < 2; ++hb)
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const int kb = 2 * cc + hb;
+          const float p0 = __builtin_amdgcn_exp2f(fmaf(t[kb][4 * w + 0], c, bb));
+          const float p1 = __builtin_amdgcn_exp2f(fmaf(t[kb][4 * w + 1], c, bb));
+          const float p2 = __builtin_amdgcn_exp2f(fmaf(t[kb][4 * w + 2], c, bb));
+          const float p3 = __builtin_amdgcn_exp2f(fmaf(t[kb][4 * w + 3], c, bb));
+          lrow = lrow + (p0 + p1);
+          lrow = lrow + (p2 + p3);
+          uint32_t x = __builtin_amdgcn_cvt_pk_fp8_f32(p0, p1, 0, false);
+          x = __builtin_amdgcn_cvt_pk_fp8_f32(p2, p3, x, true);
+          pf[4 * hb + w] = static_cast<int>(x);
+        }
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        const uint32_t base = so + db * 4096;
+        const v4i lo = *reinterpret_cast<lds_v4i_u8*>(static_cast<uintptr_t>(voff8[cc ^ (db & 1)][0] + base));
+        const v4i hi = *reinterpret_cast<lds_v4i_u8*>(static_cast<uintptr_t>(voff8[cc ^ (db & 1)][1] + base));
+        v8i vf;
+        vf[0] = lo[0]; vf[1] = lo[1]; vf[2] = lo[2]; vf[3] = lo[3];
+        vf[4] = hi[0]; vf[5] = hi[1]; vf[6] = hi[2]; vf[7] = hi[3];
+        // cbsz / blgp type 0 = FP8 E4M3 for both operands; zero scale operands select the unscaled form
+        o[db] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vf, pf, o[db], 0, 0, 0, 0, 0, 0);
+      }
+    }
+  };
+
   // Barrier B_j ends the use of ring slot j. Leading waves reach B_j after softmax_pv(j), lagging waves after
   // qk(j), so between B_(j-1) and B_j a lagging wave runs softmax_pv(j-1) while a leading wave runs qk(j). Each
   // wave issues its copies of tile j+2 right after B_(j-1), into slot (j+2) % 4, whose last reader
@@ -595,7 +710,8 @@ __global__ void __launch_bounds__(U8_NT, 1) attn_u8_kernel(const U8Args a) {
       barrier();
       load_tile(j + 3);
     }
-    softmax_pv(j);
+    if constexpr (MODE == 2) softmax_pv_f8(j);
+    else softmax_pv(j);
     if (!lag) barrier();
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no global->LDS copy outlives the workgroup
@@ -611,7 +727,10 @@ __global__ void __launch_bounds__(U8_NT, 1) attn_u8_kernel(const U8Args a) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int d = db * 32 + 8 * i + 4 * g;
-        const float4 s4 = *reinterpret_cast<const float4*>(vs + d);
+        float4 s4 = *reinterpret_cast<const float4*>(vs + d);
+        if constexpr (MODE == 2) {  // the e4m3 V codes were stretched by 448 / 127 (attn_int8.cu:2642)
+          s4.x = s4.x * V_UNSTRETCH; s4.y = s4.y * V_UNSTRETCH; s4.z = s4.z * V_UNSTRETCH; s4.w = s4.w * V_UNSTRETCH;
+        }
         const float4 m4 = *reinterpret_cast<const float4*>(vm + d);
         uint2 w;
         w.x = pack_bf2(fmaf(o[db][4 * i + 0] * il, s4.x, m4.x), fmaf(o[db][4 * i + 1] * il, s4.y, m4.y));
@@ -651,7 +770,8 @@ int check_rr_u8(const char* name, const uint16_t* tab, int rot, const uint16_t* 
 
 int prepass_u8(const uint16_t* q, int64_t q_ss, int64_t q_sh, const uint16_t* k, int64_t k_ss, int64_t k_sh,
                const uint16_t* v, int64_t v_ss, int64_t v_sh, int64_t Sq, int64_t Sk, int64_t H, const RR& rq,
-               const RR& rk, int smooth_k, int smooth_v, int rotate, const WorkU8& w, hipStream_t st) {
+               const RR& rk, int smooth_k, int smooth_v, int rotate, const WorkU8& w, hipStream_t st,
+               bool f8 = false) {
   const int64_t sqp = padk(Sq), skp = padk(Sk);
   const int nchunk = static_cast<int>((Sk + CHUNK - 1) / CHUNK);
   const float* mean = nullptr;
@@ -670,16 +790,31 @@ int prepass_u8(const uint16_t* q, int64_t q_ss, int64_t q_sh, const uint16_t* k,
                      static_cast<const float*>(nullptr), rotate, w.q8, w.qs, static_cast<float*>(nullptr));
   hipLaunchKernelGGL(tokq_kernel, dim3(skp * H / 16), dim3(256), 0, st, k, k_ss, k_sh, Sk, skp, H, rk, mean, rotate,
                      w.k8, w.ks, reinterpret_cast<float*>(w.side));
-  hipLaunchKernelGGL(vq_kernel, dim3(H, skp / TILE), dim3(256), 0, st, v, v_ss, v_sh, Sk, skp, w.vmean, w.vscale,
-                     w.vt, reinterpret_cast<int32_t*>(w.side));
+  if (f8)  // configs 50-56: e4m3 V codes (attn_int8.cu:2639-2642)
+    hipLaunchKernelGGL(vq_kernel<true>, dim3(H, skp / TILE), dim3(256), 0, st, v, v_ss, v_sh, Sk, skp, w.vmean,
+                       w.vscale, w.vt, reinterpret_cast<int32_t*>(w.side));
+  else
+    hipLaunchKernelGGL(vq_kernel<false>, dim3(H, skp / TILE), dim3(256), 0, st, v, v_ss, v_sh, Sk, skp, w.vmean,
+                       w.vscale, w.vt, reinterpret_cast<int32_t*>(w.side));
   return launch_status("attention_u8 prepass");
+}
+
+// configs 50-56: the FP8 P.V main kernel; tile = the reference's BN (64 or 128 keys per running-max update)
+int forward_f8(const WorkU8& w, int64_t Sq, int64_t Sk, int64_t H, float scale, int tile, uint16_t* out, int64_t o_ss,
+               int64_t o_sh, hipStream_t st) {
+  U8Args f{w.q8, w.qs, w.k8, w.side, w.vt, w.vscale, w.vmean, out, o_ss, o_sh, Sq, Sk, padk(Sq), padk(Sk),
+           scale * 1.4426950408889634f, 0, 0.0f};
+  const dim3 grid((Sq + U8_BQ - 1) / U8_BQ, H);
+  if (tile == 64) hipLaunchKernelGGL((attn_u8_kernel<2, 64>), grid, dim3(U8_NT), 0, st, f);
+  else hipLaunchKernelGGL((attn_u8_kernel<2, 128>), grid, dim3(U8_NT), 0, st, f);
+  return launch_status("attention_f8 forward");
 }
 
 int forward_u8(const WorkU8& w, int64_t Sq, int64_t Sk, int64_t H, float scale, int nbias, double bias, uint16_t* out,
                int64_t o_ss, int64_t o_sh, hipStream_t st) {
   U8Args f{w.q8, w.qs, w.k8, w.side, w.vt, w.vscale, w.vmean, out, o_ss, o_sh, Sq, Sk, padk(Sq), padk(Sk),
            scale * 1.4426950408889634f, nbias, static_cast<float>(bias * 1.4426950408889634)};
-  hipLaunchKernelGGL(attn_u8_kernel<false>, dim3((Sq + U8_BQ - 1) / U8_BQ, H), dim3(U8_NT), 0, st, f);
+  hipLaunchKernelGGL(attn_u8_kernel<0>, dim3((Sq + U8_BQ - 1) / U8_BQ, H), dim3(U8_NT), 0, st, f);
   return launch_status("attention_u8 forward");
 }
 
@@ -705,7 +840,7 @@ int prepass_bk(const uint16_t* q, int64_t q_ss, int64_t q_sh, const uint16_t* k,
                      static_cast<const float*>(nullptr), rotate, w.q8, w.qs, static_cast<float*>(nullptr));
   hipLaunchKernelGGL(blockk_kernel, dim3(H, skp / TILE), dim3(256), 0, st, k, k_ss, k_sh, Sk, skp,
                      static_cast<const float*>(w.kmean), rotate, w.k8, w.ks, reinterpret_cast<float*>(w.side));
-  hipLaunchKernelGGL(vq_kernel, dim3(H, skp / TILE), dim3(256), 0, st, v, v_ss, v_sh, Sk, skp, w.vmean, w.vscale,
+  hipLaunchKernelGGL(vq_kernel<false>, dim3(H, skp / TILE), dim3(256), 0, st, v, v_ss, v_sh, Sk, skp, w.vmean, w.vscale,
                      w.vt, reinterpret_cast<int32_t*>(w.side));
   return launch_status("attention_bk prepass");
 }
@@ -714,7 +849,7 @@ int forward_bk(const WorkU8& w, int64_t Sq, int64_t Sk, int64_t H, float scale, 
                int64_t o_sh, hipStream_t st) {
   U8Args f{w.q8, w.qs, w.k8, w.side, w.vt, w.vscale, w.vmean, out, o_ss, o_sh, Sq, Sk, padk(Sq), padk(Sk),
            scale * 1.4426950408889634f, 0, 0.0f};
-  hipLaunchKernelGGL(attn_u8_kernel<true>, dim3((Sq + U8_BQ - 1) / U8_BQ, H), dim3(U8_NT), 0, st, f);
+  hipLaunchKernelGGL(attn_u8_kernel<1>, dim3((Sq + U8_BQ - 1) / U8_BQ, H), dim3(U8_NT), 0, st, f);
   return launch_status("attention_bk forward");
 }
 
@@ -820,7 +955,7 @@ extern "C" int rh3_attention_u8_prepass_qkv(const uint16_t* k, int64_t k_ss, int
                      w.vscale);
   hipLaunchKernelGGL(tokq_kernel, dim3(skp * H / 16), dim3(256), 0, stream, k, k_ss, k_sh, S, skp, H, rk, mean, rotate,
                      w.k8, w.ks, reinterpret_cast<float*>(w.side));
-  hipLaunchKernelGGL(vq_kernel, dim3(H, skp / TILE), dim3(256), 0, stream, v, v_ss, v_sh, S, skp, w.vmean, w.vscale,
+  hipLaunchKernelGGL(vq_kernel<false>, dim3(H, skp / TILE), dim3(256), 0, stream, v, v_ss, v_sh, S, skp, w.vmean, w.vscale,
                      w.vt, reinterpret_cast<int32_t*>(w.side));
   if (int e = launch_status("attention_u8 prepass_qkv")) return e;
   ptrs[0] = w.q8; ptrs[1] = w.qs; ptrs[2] = w.k8; ptrs[3] = w.ks; ptrs[4] = w.side; ptrs[5] = w.vt;
@@ -914,4 +1049,59 @@ extern "C" int rh3_int8_attention_bk(const uint16_t* q, int64_t q_ss, int64_t q_
   if (int e = prepass_bk(q, q_ss, q_sh, k, k_ss, k_sh, v, v_ss, v_sh, Sq, Sk, H, smooth_k, smooth_v, rotate, w, stream))
     return e;
   return forward_bk(w, Sq, Sk, H, scale, out, o_ss, o_sh, stream);
+}
+
+extern "C" int rh3_attention_f8_prepass(const uint16_t* q, int64_t q_ss, int64_t q_sh, const uint16_t* k,
+                                        int64_t k_ss, int64_t k_sh, const uint16_t* v, int64_t v_ss, int64_t v_sh,
+                                        int64_t Sq, int64_t Sk, int64_t H, const uint16_t* tab, int rot,
+                                        const uint16_t* qw, const uint16_t* kw, float eps, int smooth_k, int smooth_v,
+                                        int rotate, void* workspace, int64_t workspace_bytes, void** ptrs,
+                                        hipStream_t stream) {
+  clear_error();
+  if (int e = check_qkv_u8("attention_f8_prepass", q, q_ss, q_sh, k, k_ss, k_sh, v, v_ss, v_sh, Sq, Sk, H)) return e;
+  RH3_REQUIRE(ptrs, "attention_f8_prepass: ptrs required");
+  const WorkU8 w = layout_u8(workspace, Sq, Sk, H);
+  RH3_REQUIRE(workspace && aligned16(workspace) && workspace_bytes >= w.bytes,
+              "attention_f8_prepass: workspace %lld bytes < required %lld", (long long)workspace_bytes,
+              (long long)w.bytes);
+  RR rq{nullptr, nullptr, 0.f, 0}, rk{nullptr, nullptr, 0.f, 0};
+  if (tab) {
+    if (int e = check_rr_u8("attention_f8_prepass", tab, rot, qw, kw)) return e;
+    RH3_REQUIRE(Sq == Sk, "attention_f8_prepass: RMSNorm+RoPE needs self-attention (Sq == Sk)");
+    rq = RR{tab, qw, eps, rot};
+    rk = RR{tab, kw, eps, rot};
+  }
+  if (int e = prepass_u8(q, q_ss, q_sh, k, k_ss, k_sh, v, v_ss, v_sh, Sq, Sk, H, rq, rk, smooth_k, smooth_v, rotate,
+                         w, stream, true))
+    return e;
+  ptrs[0] = w.q8; ptrs[1] = w.qs; ptrs[2] = w.k8; ptrs[3] = w.ks; ptrs[4] = w.side; ptrs[5] = w.vt;
+  ptrs[6] = w.kmean; ptrs[7] = w.vscale; ptrs[8] = w.vmean;
+  return RH3_OK;
+}
+
+extern "C" int rh3_attention_f8_forward(int64_t Sq, int64_t Sk, int64_t H, float scale, int tile, uint16_t* out,
+                                        int64_t o_ss, int64_t o_sh, void* workspace, int64_t workspace_bytes,
+                                        hipStream_t stream) {
+  clear_error();
+  RH3_REQUIRE(Sq > 0 && Sk > 0 && H > 0, "attention_f8_forward: sizes must be positive");
+  RH3_REQUIRE(tile == 64 || tile == 128, "attention_f8_forward: tile %d (64 or 128 keys)", tile);
+  if (int e = check_out_u8("attention_f8_forward", out, o_ss, o_sh)) return e;
+  const WorkU8 w = layout_u8(workspace, Sq, Sk, H);
+  RH3_REQUIRE(workspace && aligned16(workspace) && workspace_bytes >= w.bytes,
+              "attention_f8_forward: workspace %lld bytes < required %lld", (long long)workspace_bytes,
+              (long long)w.bytes);
+  return forward_f8(w, Sq, Sk, H, scale, tile, out, o_ss, o_sh, stream);
+}
+
+extern "C" int rh3_int8_attention_f8(const uint16_t* q, int64_t q_ss, int64_t q_sh, const uint16_t* k, int64_t k_ss,
+                                     int64_t k_sh, const uint16_t* v, int64_t v_ss, int64_t v_sh, int64_t Sq,
+                                     int64_t Sk, int64_t H, const uint16_t* tab, int rot, const uint16_t* qw,
+                                     const uint16_t* kw, float eps, float scale, int tile, int smooth_k, int smooth_v,
+                                     int rotate, uint16_t* out, int64_t o_ss, int64_t o_sh, void* workspace,
+                                     int64_t workspace_bytes, hipStream_t stream) {
+  void* ptrs[9];
+  if (int e = rh3_attention_f8_prepass(q, q_ss, q_sh, k, k_ss, k_sh, v, v_ss, v_sh, Sq, Sk, H, tab, rot, qw, kw, eps,
+                                       smooth_k, smooth_v, rotate, workspace, workspace_bytes, ptrs, stream))
+    return e;
+  return rh3_attention_f8_forward(Sq, Sk, H, scale, tile, out, o_ss, o_sh, workspace, workspace_bytes, stream);
 }

@@ -60,6 +60,11 @@ SIGNATURES = {
     "rh3_attention_bk_prepass": ([_P, _I, _I, _P, _I, _I, _P, _I, _I, _I, _I, _I, _C, _C, _C, _P, _I,
                                   ctypes.POINTER(ctypes.c_void_p), _P], _C),
     "rh3_attention_bk_forward": ([_I, _I, _I, _F, _P, _I, _I, _P, _I, _P], _C),
+    "rh3_int8_attention_f8": ([_P, _I, _I, _P, _I, _I, _P, _I, _I, _I, _I, _I, _P, _C, _P, _P, _F, _F, _C, _C, _C, _C,
+                               _P, _I, _I, _P, _I, _P], _C),
+    "rh3_attention_f8_prepass": ([_P, _I, _I, _P, _I, _I, _P, _I, _I, _I, _I, _I, _P, _C, _P, _P, _F, _C, _C, _C,
+                                  _P, _I, ctypes.POINTER(ctypes.c_void_p), _P], _C),
+    "rh3_attention_f8_forward": ([_I, _I, _I, _F, _C, _P, _I, _I, _P, _I, _P], _C),
 }
 
 RH3_DTYPE_BF16 = 1

@@ -16,8 +16,14 @@ Signatures follow /root/reference/custom_nodes/rapid_h3/attn_int8.py:30-65. Two 
     with one K scale per 128-key block (after the smoothing and the H128 rotation), an integer tile max over
     the raw accumulators and no per-key dequantization. No RMSNorm + RoPE path and no text bias (the
     reference's own limits, attn_int8.cu:2606, :2764).
-Configs 50-59 (FP8 P.V) and 62-69 are not built and raise NotImplementedError. The reference's "config 3xx" is
-attention_pre (Q operands and K / V statistics from the qkv GEMM epilogue) with a kernel config 80-99.
+  * configs 50-56 (attn_int8.cu attn_fwd5 :1563-1785): the production Q / K numerics with e4m3 V (per channel,
+    stretched to 448) and P in e4m3 against the running max (scaled to 448), P.V on the FP8 MFMA straight into fp32,
+    the running max updated per 64 keys (configs 50, 51, 54, 56) or 128 keys (52, 53, 55); the reference's
+    two-level accumulation of 51 / 53 is the same sum with another fp32 rounding order. RMSNorm + RoPE path yes,
+    text bias no (as in the reference).
+Configs 57-59 and 62-69 do not exist in the reference's dispatch (attn_int8.cu:2776-2830) and raise
+NotImplementedError. The reference's "config 3xx" is attention_pre (Q operands and K / V statistics from the qkv
+GEMM epilogue) with a kernel config 80-99.
 """
 import torch
 
@@ -64,9 +70,33 @@ def _production(config, name):
     if c < 0 or c >= 300:
         raise NotImplementedError(f"{name}: config {c} is not built for gfx950 (3xx needs the qkv-GEMM epilogue "
                                   "pre-pass)")
-    if 50 <= c % 100 < 70:
-        raise NotImplementedError(f"{name}: config {c} (FP8 P.V / per-block K) is not built for gfx950")
+    if c % 100 in (57, 58, 59) or 62 <= c % 100 < 70:
+        raise NotImplementedError(f"{name}: config {c} does not exist in the reference's kernel dispatch")
     return True
+
+
+def _fp8_tile(config):
+    """Keys per running-max update of the FP8 P.V configs 50-56 (the reference's BN, attn_int8.cu:2804-2810), or
+    None for any other config."""
+    if config is None or not 50 <= int(config) % 100 < 60:
+        return None
+    c = int(config) % 100
+    if c > 56:
+        raise NotImplementedError(f"config {int(config)}: the FP8 P.V kernel is configs 50-56 only")
+    return 128 if c in (52, 53, 55) else 64
+
+
+def _attention_f8(name, q, k, v, rr, scale, tile, smooth_k, smooth_v, rotate, out):
+    sq, h, _ = q.shape
+    sk = k.shape[0]
+    out = _out(q, out)
+    tab, qw, kw, eps, rot = rr if rr is not None else (None, None, None, 0.0, 0)
+    ws = workspace_u8(sq, sk, h, q.device)
+    nat.call("rh3_int8_attention_f8", nat.ptr(q), q.stride(0), q.stride(1), nat.ptr(k), k.stride(0), k.stride(1),
+             nat.ptr(v), v.stride(0), v.stride(1), sq, sk, h, nat.ptr(tab), rot, nat.ptr(qw), nat.ptr(kw),
+             float(eps), float(scale), int(tile), int(bool(smooth_k)), int(bool(smooth_v)), int(bool(rotate)),
+             nat.ptr(out), out.stride(0), out.stride(1), nat.ptr(ws), ws.numel(), nat.stream(q.device))
+    return out
 
 
 def _block_k(config):
@@ -118,6 +148,9 @@ def attention(q, k, v, scale=None, config=None, smooth_k=True, smooth_v=True, ro
     scale = q.shape[-1] ** -0.5 if scale is None else scale
     if _block_k(config):
         return _attention_bk(q, k, v, scale, smooth_k, smooth_v, rotate, out)
+    tile = _fp8_tile(config)
+    if tile:
+        return _attention_f8("attention", q, k, v, None, scale, tile, smooth_k, smooth_v, rotate, out)
     if _production(config, "attention"):
         return _attention_u8("attention", q, k, v, None, scale, 0, 0.0, smooth_k, smooth_v, rotate, out)
     out = _out(q, out)
@@ -162,6 +195,10 @@ def attention_rr(q, k, v, tab, qw, kw, eps, scale=None, config=94, smooth_k=True
         raise RuntimeError("configs 60-69 have no fused rms/rope path")    # attn_int8.cu:2606
     tab, qw, kw, rot = _check_rr(q, tab, qw, kw)
     scale = q.shape[-1] ** -0.5 if scale is None else scale
+    tile = _fp8_tile(config)
+    if tile:
+        return _attention_f8("attention_rr", q, k, v, (tab, qw, kw, eps, rot), scale, tile, smooth_k, smooth_v, rotate,
+                             out)
     if _production(config, "attention_rr"):
         return _attention_u8("attention_rr", q, k, v, (tab, qw, kw, eps, rot), scale, 0, 0.0, smooth_k, smooth_v,
                              rotate, out)
@@ -332,6 +369,8 @@ def attention_pre(k, v, q8, qs, part, tab, kw, eps, scale=None, config=94, smoot
     ([S, H, 128] bf16 views). The same result as attention_rr with config on that GEMM's q, k, v. The rotate
     flag must match the one int8_gemm_qkv_prep used."""
     _production(config, "attention_pre")
+    if 50 <= int(config) % 100 < 70:
+        raise RuntimeError("config 3xx: configs 80-99")    # attn_int8.cu:2592
     if q8.untyped_storage().data_ptr() != part.untyped_storage().data_ptr():
         raise RuntimeError("attention_pre: q8 / qs / part must be the views int8_gemm_qkv_prep returned")
     ws = torch.empty(0, dtype=torch.uint8, device=q8.device).set_(q8.untyped_storage())
@@ -405,4 +444,39 @@ def forward_bk(pp, sq, out=None, scale=None):
     ws = pp["_ws"]
     nat.call("rh3_attention_bk_forward", sq, sk, h, float(scale), nat.ptr(out), out.stride(0), out.stride(1),
              nat.ptr(ws), ws.numel(), nat.stream(out.device))
+    return out
+
+
+def prepass_f8(q, k, v, tab=None, qw=None, kw=None, eps=1e-5, smooth_k=True, smooth_v=True, rotate=True):
+    """Pre-pass operands of the FP8 P.V configs 50-56 (for verification): dict as prepass_u8() with vt
+    [H, 128, Skpad] uint8 e4m3 codes (keys permuted within 64-key chunks) and without vinit."""
+    import ctypes
+    _check_qkv(q, k, v, "prepass_f8")
+    sq, h, _ = q.shape
+    sk = k.shape[0]
+    rot = 0
+    if tab is not None:
+        tab, qw, kw, rot = _check_rr(q, tab, qw, kw)
+    ws = workspace_u8(sq, sk, h, q.device)
+    ptrs = (ctypes.c_void_p * 9)()
+    nat.call("rh3_attention_f8_prepass", nat.ptr(q), q.stride(0), q.stride(1), nat.ptr(k), k.stride(0), k.stride(1),
+             nat.ptr(v), v.stride(0), v.stride(1), sq, sk, h, nat.ptr(tab), rot, nat.ptr(qw), nat.ptr(kw),
+             float(eps), int(bool(smooth_k)), int(bool(smooth_v)), int(bool(rotate)), nat.ptr(ws), ws.numel(), ptrs,
+             nat.stream(q.device))
+    vw = _u8_views(ws, ptrs, sq, sk, h)
+    vw["vt"] = vw["vt"].view(torch.uint8)
+    del vw["vinit"]
+    return vw
+
+
+def forward_f8(pp, sq, out=None, scale=None, tile=64):
+    """The FP8 P.V main kernel alone on operands prepass_f8() produced: out [Sq, H, 128] bf16."""
+    h = pp["q8"].shape[0]
+    sk = pp["_sk"]
+    scale = D ** -0.5 if scale is None else scale
+    if out is None:
+        out = torch.empty((sq, h, D), device=pp["q8"].device, dtype=torch.bfloat16)
+    ws = pp["_ws"]
+    nat.call("rh3_attention_f8_forward", sq, sk, h, float(scale), int(tile), nat.ptr(out), out.stride(0),
+             out.stride(1), nat.ptr(ws), ws.numel(), nat.stream(out.device))
     return out

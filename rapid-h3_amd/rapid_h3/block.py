@@ -87,7 +87,7 @@ def fused_block(x, w: BlockWeights, mod, segments, rope_tab, idx=None, mark=None
     records a stream event there); the kernels and their order are the same with or without it.
     trace: optional dict that receives every intermediate (a checker's view of each stage).
     attn_config: None runs the per-block bf16 P.V attention; an int runs the reference's production
-    numerics with that config (its 1xx presets, __init__.py:274-291). text_bias = (nbias, bias) adds the
+    numerics with that config (its 1xx presets, __init__.py:274-291), 50-56 its FP8 P.V kernel. text_bias = (nbias, bias) adds the
     Jenga text bias (configs 90 / 94 only). fuse_qkv (even head counts): the QKV GEMM's epilogue writes the
     attention's Q operands and K / V statistics itself (gemm.int8_gemm_qkv, the reference's config 3xx
     path), so the pre-pass skips its Q pass and statistics passes; the result is the same bit for bit. Off by
@@ -112,9 +112,12 @@ def fused_block(x, w: BlockWeights, mod, segments, rope_tab, idx=None, mark=None
             raise RuntimeError("text bias: needs the production attention (attn_config 90 or 94)")
     else:
         _attn._production(attn_config, "fused_block")
+        if 60 <= int(attn_config) % 100 < 70:
+            raise RuntimeError("configs 60-69 have no fused rms/rope path")    # attn_int8.cu:2606
         if text_bias is not None and text_bias[0] and int(attn_config) % 100 not in (90, 94):
             raise RuntimeError("text bias: config 94 or 90 only")
-    fused = fuse_qkv and h % 2 == 0
+    f8_tile = _attn._fp8_tile(attn_config)     # configs 50-56: the FP8 P.V kernel
+    fused = fuse_qkv and h % 2 == 0 and not f8_tile
     if fused:
         wsb = (_attn.workspace if numerics == 0 else _attn.workspace_u8)(s, s, h, x.device)
         qkv = _gemm.int8_gemm_qkv(xq, xs, w.qkv.q, w.qkv.scale, h, wsb, numerics, tab=rope_tab, qw=w.q_norm_w,
@@ -130,12 +133,16 @@ def fused_block(x, w: BlockWeights, mod, segments, rope_tab, idx=None, mark=None
         pp = _attn.prepass_qkv(k, v, wsb, numerics, rope_tab, w.k_norm_w, w.qk_eps)
     elif numerics == 0:
         pp = _attn.prepass(q, k, v, rope_tab, w.q_norm_w, w.k_norm_w, w.qk_eps)
+    elif f8_tile:
+        pp = _attn.prepass_f8(q, k, v, rope_tab, w.q_norm_w, w.k_norm_w, w.qk_eps)
     else:
         pp = _attn.prepass_u8(q, k, v, rope_tab, w.q_norm_w, w.k_norm_w, w.qk_eps)
     keep("q8", pp["q8"]), keep("qs", pp["qs"])
     tick("attn_prepass")
     if numerics == 0:
         _attn.forward(pp, s, out=o[0].transpose(0, 1))
+    elif f8_tile:
+        _attn.forward_f8(pp, s, out=o[0].transpose(0, 1), tile=f8_tile)
     else:
         nbias, bias = text_bias if text_bias is not None else (0, 0.0)
         _attn.forward_u8(pp, s, out=o[0].transpose(0, 1), nbias=nbias, bias=bias)

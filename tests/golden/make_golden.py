@@ -203,12 +203,36 @@ def attn_bk_case(rng):
     np.savez_compressed(os.path.join(HERE, "attention_bk.npz"), q=q, k=k, v=v, **out)
 
 
-CASES = ("quant", "norm_mod", "heads", "gemm", "attn", "rot", "attn_u8", "attn_bk")
+def attn_f8_case(rng):
+    """FP8 P.V attention (configs 50-56): plain with 64- and 128-key running-max groups, fused RMSNorm + RoPE,
+    without rotation and V smoothing, and cross-attention (300 queries over 200 keys). Outputs rounded to bf16."""
+    s, h = 300, 2
+    q = bf16(rng.standard_normal((s, h, 128)))
+    k = bf16(rng.standard_normal((s, h, 128)) + 2.0 * rng.standard_normal((1, h, 128)))
+    v = bf16(rng.standard_normal((s, h, 128)) + 0.5 * rng.standard_normal((1, h, 128)))
+    tab = bf16(oa.rope_table(np.arange(s) % 37, rot=96).reshape(s, 48, 2, 2))
+    qw = bf16(1.0 + 0.3 * rng.standard_normal(128))
+    kw = bf16(1.0 + 0.3 * rng.standard_normal(128))
+    sc = 128 ** -0.5
+    keys = ("q8", "qs", "k8", "ksb", "vf8", "vscale", "vmean", "kmean")
+    out = {}
+    for pre, kw_ in (("", {}), ("r", {"rr": (tab, qw, kw, 1e-5)}), ("n", {"rotate": False, "smooth_v": False})):
+        pp = oa.prepass_fp8v(q, k, v, **kw_)
+        out.update({pre + n: pp[n] for n in keys})
+        out[pre + "out64"] = bf16(oa.attention_fp8pv_from_codes(pp, sc, tile=64)[:s])
+        out[pre + "out128"] = bf16(oa.attention_fp8pv_from_codes(pp, sc, tile=128)[:s])
+    pp = oa.prepass_fp8v(q, k[:200], v[:200])
+    out.update({"c" + n: pp[n] for n in keys if n not in ("q8", "qs")})
+    out["cout64"] = bf16(oa.attention_fp8pv_from_codes(pp, sc, tile=64)[:s])
+    np.savez_compressed(os.path.join(HERE, "attention_f8.npz"), q=q, k=k, v=v, tab=tab, qw=qw, kw=kw, **out)
+
+
+CASES = ("quant", "norm_mod", "heads", "gemm", "attn", "rot", "attn_u8", "attn_bk", "attn_f8")
 
 
 def main(which=CASES):
     """Each group draws from its own fixed stream: the first five share seed 0 in this order, rot uses
-    seed 1, attn_u8 seed 2 and attn_bk seed 3, so regenerating one file leaves the others' inputs unchanged."""
+    seed 1, attn_u8 seed 2, attn_bk seed 3 and attn_f8 seed 4, so regenerating one file leaves the others' inputs unchanged."""
     if set(which) & set(CASES[:5]):
         rng = np.random.default_rng(0)
         quant_case(rng)
@@ -222,6 +246,8 @@ def main(which=CASES):
         attn_u8_case(np.random.default_rng(2))
     if "attn_bk" in which:
         attn_bk_case(np.random.default_rng(3))
+    if "attn_f8" in which:
+        attn_f8_case(np.random.default_rng(4))
     for f in sorted(os.listdir(HERE)):
         if f.endswith(".npz"):
             print(f, os.path.getsize(os.path.join(HERE, f)))

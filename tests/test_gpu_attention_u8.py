@@ -133,17 +133,17 @@ def test_u8_routing_and_errors(dev):
     x = torch.zeros(300, 1, 128, dtype=torch.bfloat16, device=dev)
     tab = torch.zeros(1, 300, 1, 48, 2, 2, dtype=torch.bfloat16, device=dev)
     w = torch.ones(128, dtype=torch.bfloat16, device=dev)
-    with pytest.raises(NotImplementedError):
-        attention.attention(x, x, x, config=52)
-    with pytest.raises(NotImplementedError):
-        attention.attention(x, x, x, config=361)
+    for c in (57, 59, 62, 69, 361):    # not in the reference's kernel dispatch
+        with pytest.raises(NotImplementedError):
+            attention.attention(x, x, x, config=c)
     with pytest.raises(RuntimeError, match="config 94 or 90"):
         attention.attention_rr_bias(x, x, x, tab, w, w, 1e-5, 5, 1.0, config=80)
     with pytest.raises(RuntimeError, match="nbias"):
         attention.attention_rr_bias(x, x, x, tab, w, w, 1e-5, 301, 1.0)
     # all-zero inputs: uniform softmax over zero V
-    out = attention.attention(x, x, x, config=94)
-    assert not torch.isnan(out.float()).any() and not out.float().abs().max().item()
+    for c in (94, 60, 50):
+        out = attention.attention(x, x, x, config=c)
+        assert not torch.isnan(out.float()).any() and not out.float().abs().max().item(), c
 
 
 def test_u8_full_size_sampled(dev):
@@ -240,4 +240,92 @@ def test_bk_shapes(dev, sq, sk, h):
     v = f32_to_bf16(rng.standard_normal((sk, h, 128)).astype(np.float32))
     out = attention.attention(to_dev(q, dev), to_dev(k, dev), to_dev(v, dev), config=60)
     ref = oa.attention_blockk_from_codes(oa.prepass_blockk(q, k, v), SC)[:sq]
+    assert rel_l2(bf16_to_f32(to_np(out)), ref) < TOL
+
+
+# ----------------------------------------------------------------------------- configs 50-56 (FP8 P.V)
+def _perm_keys_f8(skp):
+    """Key held at each position of the e4m3 V^T layout: p = 32 g + 16 h + r inside a 64-key chunk <-> key
+    32 h + 8 (r / 4) + 4 g + r % 4."""
+    p = np.arange(skp)
+    w = p & 63
+    g, hh, r = w >> 5, (w >> 4) & 1, w & 15
+    return (p & ~63) + 32 * hh + 8 * (r >> 2) + 4 * g + (r & 3)
+
+
+def _check_f8(pp, exp, pre, s_k):
+    for n in ("q8", "qs", "k8", "ks", "kmean"):
+        if pre + n in exp:
+            assert np.array_equal(to_np(pp[n]), exp[pre + n]), pre + n
+    assert np.array_equal(to_np(pp["ksb"]), exp[pre + "ksb"]), pre + "ksb"
+    for n in ("vscale", "vmean"):
+        assert np.array_equal(to_np(pp[n]), exp[pre + n]), pre + n
+    vt = to_np(pp["vt"])                                           # [H, 128, Skpad] e4m3 codes
+    keys = _perm_keys_f8(vt.shape[2])
+    vpad = np.zeros((vt.shape[2],) + exp[pre + "vf8"].shape[1:], np.uint8)
+    vpad[:s_k] = exp[pre + "vf8"]
+    assert np.array_equal(vt, vpad[keys].transpose(1, 2, 0)), pre + "vt"
+
+
+def test_f8_prepass_golden(dev, golden):
+    """Configs 50-56's pre-pass: Q / K codes, scales and per-key pairs as the production numerics, e4m3 V codes
+    (on the hardware's v_cvt_pk_fp8_f32) in the 64-key-chunk layout, vscale, vmean, kmean bit-exact."""
+    from rapid_h3 import attention
+    g = golden("attention_f8")
+    q, k, v = (to_dev(g[n], dev) for n in ("q", "k", "v"))
+    s = g["q"].shape[0]
+    tab, qw, kw = _rr(g, dev, s)
+    _check_f8(attention.prepass_f8(q, k, v), g, "", s)
+    _check_f8(attention.prepass_f8(q, k, v, tab, qw, kw, 1e-5), g, "r", s)
+    _check_f8(attention.prepass_f8(q, k, v, rotate=False, smooth_v=False), g, "n", s)
+    _check_f8(attention.prepass_f8(q, k[:200], v[:200]), g, "c", 200)
+
+
+def test_f8_forward_golden(dev, golden):
+    """Every route to the FP8 P.V kernel: configs 50 / 54 / 56 (64-key running-max groups) and 52 / 53 / 55
+    (128), attention_rr (1xx presets), no rotation / no V smoothing, cross-attention, the main kernel alone and
+    the drop-in module; within the FP8 error band of exact attention; no text bias (as in the reference)."""
+    import torch
+    from rapid_h3 import attention, attn_int8
+    g = golden("attention_f8")
+    q, k, v = (to_dev(g[n], dev) for n in ("q", "k", "v"))
+    s = g["q"].shape[0]
+    tab, qw, kw = _rr(g, dev, s)
+
+    def check(out, name):
+        got = bf16_to_f32(to_np(out))
+        ref = bf16_to_f32(g[name])
+        assert rel_l2(got, ref) < TOL, (name, rel_l2(got, ref))
+
+    for c in (50, 54, 56, 150):
+        check(attention.attention(q, k, v, config=c), "out64")
+    for c in (52, 53, 55):
+        check(attn_int8.attention(q, k, v, config=c), "out128")
+    check(attention.attention_rr(q, k, v, tab, qw, kw, 1e-5, config=150), "rout64")
+    check(attention.attention_rr(q, k, v, tab, qw, kw, 1e-5, config=52), "rout128")
+    check(attention.attention(q, k, v, config=51, rotate=False, smooth_v=False), "nout64")
+    check(attention.attention(q, k[:200], v[:200], config=50), "cout64")
+    pp = attention.prepass_f8(q, k, v)
+    assert torch.equal(attention.forward_f8(pp, s, tile=64), attention.attention(q, k, v, config=50))
+    ex = oa.attention_exact(g["q"], g["k"], g["v"], SC)
+    assert rel_l2(bf16_to_f32(to_np(attention.attention(q, k, v, config=52))), ex) < 0.03
+    with pytest.raises(RuntimeError, match="config 94 or 90"):
+        attention.attention_rr_bias(q, k, v, tab, qw, kw, 1e-5, 10, 1.0, config=50)
+    with pytest.raises(NotImplementedError):
+        attention.attention(q, k, v, config=57)
+
+
+@pytest.mark.parametrize("sq,sk,h,c", [(1, 1, 1, 50), (127, 129, 2, 52), (256, 256, 1, 50), (257, 600, 3, 55),
+                                       (1000, 77, 2, 56), (300, 192, 1, 54)])
+def test_f8_shapes(dev, sq, sk, h, c):
+    """Query blocks around the 256-query workgroup, key tiles around the 128-key tile, a last tile whose second
+    64-key chunk is all padding (sk = 192, 77), cross-attention in both directions."""
+    from rapid_h3 import attention
+    rng = np.random.default_rng(sq * 3 + sk * 7 + h + c)
+    q = f32_to_bf16(rng.standard_normal((sq, h, 128)).astype(np.float32))
+    k = f32_to_bf16((rng.standard_normal((sk, h, 128)) + 2 * rng.standard_normal((1, h, 128))).astype(np.float32))
+    v = f32_to_bf16(rng.standard_normal((sk, h, 128)).astype(np.float32))
+    out = attention.attention(to_dev(q, dev), to_dev(k, dev), to_dev(v, dev), config=c)
+    tile = 128 if c in (52, 53, 55) else 64
+    ref = oa.attention_fp8pv_from_codes(oa.prepass_fp8v(q, k, v), SC, tile=tile)[:sq]
     assert rel_l2(bf16_to_f32(to_np(out)), ref) < TOL

@@ -459,6 +459,10 @@ def test_golden_fixtures_regenerate(golden):
     pp = oa.prepass_blockk(b["q"], b["k"], b["v"])
     for n in ("q8", "qs", "k8", "kbs", "vinit", "v8", "vscale", "vmean"):
         assert np.array_equal(pp[n], b[n]), n
+    f = golden("attention_f8")
+    pp = oa.prepass_fp8v(f["q"], f["k"], f["v"])
+    for n in ("q8", "qs", "k8", "ksb", "vf8", "vscale", "vmean"):
+        assert np.array_equal(pp[n], f[n]), n
 
 
 # ----------------------------------------------------------------------------- production attention numerics
@@ -668,3 +672,63 @@ def test_attention_blockk_single_key_and_closed_form():
     assert og.rel_l2(oa.attention_blockk_from_codes(bad, 128 ** -0.5)[:300], ex) > 0.1
     unmasked = dict(pp, v8=np.concatenate([pp["v8"], np.zeros((84, 2, 128), np.int8)]))
     assert og.rel_l2(oa.attention_blockk_from_codes(unmasked, 128 ** -0.5)[:300], good) > 0.01
+
+
+# ----------------------------------------------------------------------------- FP8 P.V (configs 50-56)
+def test_v_fp8_matches_torch():
+    """e4m3 V codes: torch's float8_e4m3fn cast of ((v - vmean) / vscale) * fp32(448 / 127); the extreme deviation
+    of each channel lands on +-448; vscale and vmean are the int8 path's."""
+    _, _, v = _u8_inputs(21)
+    codes, sc, vm = oa.v_fp8(v)
+    tv = t_bf16(v).float()
+    x = ((tv - torch.from_numpy(vm)) / torch.from_numpy(sc)) * torch.tensor(np.float32(448.0) / np.float32(127.0))
+    ref = x.clamp(-448, 448).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(codes, ref)
+    dec = fp8_e4m3_to_f32(codes)
+    assert (np.abs(dec).max(axis=0) == 448).all()
+    _, s8, m8 = oa.v_int8(v)
+    assert np.array_equal(sc, s8) and np.array_equal(vm, m8)
+
+
+def test_attention_fp8pv_single_key_and_closed_form():
+    """One key: p = 448, so the output is that key's decoded V times vscale * 127 / 448 plus vmean. Five 64-key
+    tiles: the online rescaling equals the closed form O = sum_t 2^((m_t - M) c) P8_t . V, l = sum_t 2^((m_t - M) c)
+    sum p_t with m_t the running max after tile t and P8_t = e4m3(2^(fma(t, c, fma(-m_t, c, log2 448)))); within
+    the FP8 error band of exact attention for 64- and 128-key tiles, and a kernel that drops the 127 / 448 factor
+    is not."""
+    q, k, v = _u8_inputs(22, s=1, sk=1)
+    pp = oa.prepass_fp8v(q, k, v)
+    out = oa.attention_fp8pv_from_codes(pp, 128 ** -0.5)[:1]
+    dq = fp8_e4m3_to_f32(pp["vf8"]).astype(np.float64) * (pp["vscale"] * oa.V_FP8_UNSTRETCH)[None] + pp["vmean"][None]
+    assert np.allclose(out, dq, rtol=1e-5, atol=1e-6)
+    q, k, v = _u8_inputs(23, s=5, sk=300)
+    pp = oa.prepass_fp8v(q, k, v)
+    sl2 = np.float32(np.float32(128 ** -0.5) * np.float32(1.4426950408889634))
+    out = oa.attention_fp8pv_from_codes(pp, 128 ** -0.5, tile=64)[:5]
+    for h in range(2):
+        acc = pp["q8"][h, :5].astype(np.int64) @ pp["k8"][h, :300].astype(np.int64).T
+        t = (((oa.MAGIC + acc) * pp["ksb"][h, :300, 0][None].astype(np.float64)
+              + pp["ksb"][h, :300, 1][None].astype(np.float64))).astype(np.float32)
+        c = (pp["qs"][h, :5] * sl2).astype(np.float32)[:, None]
+        vq = fp8_e4m3_to_f32(pp["vf8"][:, h]).astype(np.float64)
+        runs, parts = -np.inf, []
+        for j in range(0, 300, 64):
+            tt = t[:, j:j + 64]
+            runs = np.maximum(runs, tt.max(axis=1, keepdims=True))
+            bb = (-runs.astype(np.float64) * c + np.float64(oa.LOG2_448)).astype(np.float32)
+            p = np.exp2((tt.astype(np.float64) * c + bb).astype(np.float32).astype(np.float64)).astype(np.float32)
+            p8 = fp8_e4m3_to_f32(f32_to_fp8_e4m3(np.minimum(p, np.float32(448)))).astype(np.float64)
+            parts.append((runs.copy(), p8 @ vq[j:j + 64], p.astype(np.float64).sum(axis=1, keepdims=True)))
+        mm = parts[-1][0]
+        w = [np.exp2((r - mm).astype(np.float64) * c) for r, _, _ in parts]
+        num = sum(wi * pv for wi, (_, pv, _) in zip(w, parts))
+        den = sum(wi * ps for wi, (_, _, ps) in zip(w, parts))
+        ref = num / den * (pp["vscale"][h] * oa.V_FP8_UNSTRETCH)[None] + pp["vmean"][h][None]
+        assert np.allclose(out[:, h], ref, rtol=1e-5, atol=1e-5)
+    q, k, v = _u8_inputs(24, s=300)
+    pp = oa.prepass_fp8v(q, k, v)
+    ex = oa.attention_exact(q, k, v, 128 ** -0.5)
+    for tile in (64, 128):
+        assert og.rel_l2(oa.attention_fp8pv_from_codes(pp, 128 ** -0.5, tile=tile)[:300], ex) < 0.03
+    bad = dict(pp, vscale=(pp["vscale"] / oa.V_FP8_UNSTRETCH).astype(np.float32))
+    assert og.rel_l2(oa.attention_fp8pv_from_codes(bad, 128 ** -0.5)[:300], ex) > 0.1
