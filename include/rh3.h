@@ -103,6 +103,15 @@ int rh3_rot_quant_heads_i8(const uint16_t* o, int64_t H, int64_t M, int64_t ld_h
 int rh3_convrot_f32(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t K,
                     float* y, int64_t ldy, hipStream_t stream);
 
+/* NVFP4 round trip of the verification modes nvfp4_fake / nvfp4_rot_fake: replaces kernels.fake_nvfp4
+ * (kernels.py:38-49) followed by the callers' bf16 cast (kernels.py:56, :122). x [M, K] bf16 (RH3_DTYPE_BF16)
+ * or fp32 (RH3_DTYPE_F32), K % 16 == 0; out [M, K] bf16 (row stride ldo % 8 == 0, 16-byte aligned);
+ * amax_ws: one device float of caller scratch (the tensor absmax, written before it is read). One fp32 scale
+ * per tensor gs = max(amax / 2688, 1e-12); per 16-element block s = e4m3(min(amax_b / 6 / gs, 448)) * gs (1 where
+ * 0); values rounded to the e2m1 grid of x / s with ties to the lower point, times s. */
+int rh3_fake_nvfp4(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t K, uint16_t* out, int64_t ldo,
+                   float* amax_ws, hipStream_t stream);
+
 /* replaces kernels.quantize_weight(w, "int8_rot") (kernels.py:62-72): convrot(w) (exact, rounded to
  * fp32), then per-row s = max(amax/127, 1e-12), q = round(w_rot / s); w [N, K] bf16 or fp32 */
 int rh3_quant_weight_rot_i8(const void* w, int w_dtype, int64_t ldw, int64_t N, int64_t K,

@@ -233,3 +233,26 @@ def convrot_matmul(x, group=256):
     m, k = v.shape
     h = regular_hadamard(group)
     return (v.reshape(-1, group) @ h.T).reshape(m, k).astype(F32)
+
+
+E2M1 = np.array([0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0], F32)   # kernels.py:35
+
+
+def fake_nvfp4(x):
+    """kernels.fake_nvfp4 (kernels.py:38-49), the NVFP4 round trip of the verification modes nvfp4_fake /
+    nvfp4_rot_fake: x fp32 (last dim a multiple of 16) -> fp32. One fp32 scale per tensor gs = max(amax / (448 *
+    6), 1e-12); per 16-element block s = e4m3(min(fp32(fp32(block amax / 6) / gs), 448)) * gs (1 where that is 0);
+    q = x / s rounded to the e2m1 grid {0, .5, 1, 1.5, 2, 3, 4, 6} by torch.bucketize over the midpoints
+    (right=False: a tie goes to the lower value), result = grid * sign(q) * s."""
+    from .numerics import fp8_e4m3_to_f32
+    x = np.asarray(x, F32)
+    t = x.reshape(-1, 16)
+    gs = np.maximum((np.abs(t).max() / F32(448.0 * 6.0)).astype(F32), EPS_SCALE).astype(F32)
+    bm = np.abs(t).max(axis=1, keepdims=True)
+    sb = np.minimum(((bm / F32(6.0)).astype(F32) / gs).astype(F32), FP8_MAX).astype(F32)
+    s = (fp8_e4m3_to_f32(f32_to_fp8_e4m3(sb)) * gs).astype(F32)
+    s = np.where(s == 0, F32(1.0), s).astype(F32)
+    q = (t / s).astype(F32)
+    mid = ((E2M1[1:] + E2M1[:-1]) / F32(2.0)).astype(F32)
+    idx = np.searchsorted(mid, np.minimum(np.abs(q), F32(6.0)), side="left")
+    return ((E2M1[idx] * np.sign(q)).astype(F32) * s).astype(F32).reshape(x.shape)

@@ -551,3 +551,107 @@ extern "C" int rh3_quant_swiglu_i8(const uint16_t* x, int64_t ldx, int64_t M, in
   QuantArgs a{x, ldx, 0, M, F, nullptr, 0.f, nullptr, nullptr, nullptr, 0, q, ldq, s};
   return launch<KIND_SWIGLU, false, float>(a, stream, "quant_swiglu_i8");
 }
+
+// ---------------------------------------------------------------- NVFP4 round trip (verification modes)
+namespace rh3 {
+namespace {
+
+// |x| max of the whole [M, K] tensor into *amax (non-negative floats order like their bit patterns, so an
+// unsigned atomic max is exact and order-free); *amax is zeroed by fill_zero_kernel first
+template <typename T>
+__global__ void __launch_bounds__(256) absmax_kernel(const T* __restrict__ x, int64_t ldx, int64_t M, int64_t K,
+                                                     unsigned int* __restrict__ amax) {
+  __shared__ float red[4];
+  float m = 0.0f;
+  const int64_t n = M * K;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n; i += static_cast<int64_t>(gridDim.x) * 256) {
+    const int64_t r = i / K, c = i % K;
+    float v;
+    if constexpr (sizeof(T) == 2) v = bf2f(x[r * ldx + c]);
+    else v = x[r * ldx + c];
+    m = fmaxf(m, fabsf(v));
+  }
+  m = wave_max(m);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) atomicMax(amax, __float_as_uint(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]))));
+}
+
+__global__ void fill_zero_kernel(unsigned int* p) { *p = 0u; }
+
+// one thread per 16-element block along the rows (K % 16 == 0): kernels.fake_nvfp4 (kernels.py:38-49) then the
+// bf16 cast of its callers (:56, :122)
+template <typename T>
+__global__ void __launch_bounds__(256) fake_nvfp4_kernel(const T* __restrict__ x, int64_t ldx, int64_t M, int64_t K,
+                                                         uint16_t* __restrict__ out, int64_t ldo,
+                                                         const unsigned int* __restrict__ amax) {
+  const int64_t b = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x, nb = K / 16;
+  if (b >= M * nb) return;
+  const int64_t r = b / nb, c0 = (b % nb) * 16;
+  float v[16];
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    if constexpr (sizeof(T) == 2) v[e] = bf2f(x[r * ldx + c0 + e]);
+    else v[e] = x[r * ldx + c0 + e];
+  }
+  const float gs = fmaxf(__uint_as_float(*amax) / 2688.0f, 1e-12f);
+  float bm = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) bm = fmaxf(bm, fabsf(v[e]));
+  const float sb = fminf((bm / 6.0f) / gs, 448.0f);
+  // e4m3fn round to nearest even (0 <= sb <= 448), decoded back to fp32
+  const uint32_t code = __builtin_amdgcn_cvt_pk_fp8_f32(sb, 0.0f, 0, false) & 0xffu;
+  const uint32_t ex = (code >> 3) & 0xfu, mt = code & 7u;
+  const float dec = ex ? __uint_as_float(((ex + 120u) << 23) | (mt << 20)) : static_cast<float>(mt) * 0x1p-9f;
+  float s = dec * gs;
+  if (s == 0.0f) s = 1.0f;
+  uint32_t w[8];
+#pragma unroll
+  for (int e = 0; e < 16; e += 2) {
+    float y[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const float q = v[e + u] / s;
+      const float a = fminf(fabsf(q), 6.0f);
+      // the e2m1 grid point of torch.bucketize over the midpoints (a tie goes to the lower point)
+      const float g = a <= 0.25f ? 0.0f : a <= 0.75f ? 0.5f : a <= 1.25f ? 1.0f : a <= 1.75f ? 1.5f
+                    : a <= 2.5f ? 2.0f : a <= 3.5f ? 3.0f : a <= 5.0f ? 4.0f : 6.0f;
+      const float sg = q > 0.0f ? 1.0f : (q < 0.0f ? -1.0f : 0.0f);
+      y[u] = (g * sg) * s;
+    }
+    w[e >> 1] = pack_bf2(y[0], y[1]);
+  }
+  uint4* o = reinterpret_cast<uint4*>(out + r * ldo + c0);
+  o[0] = make_uint4(w[0], w[1], w[2], w[3]);
+  o[1] = make_uint4(w[4], w[5], w[6], w[7]);
+}
+
+}  // namespace
+}  // namespace rh3
+
+extern "C" int rh3_fake_nvfp4(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t K, uint16_t* out,
+                              int64_t ldo, float* amax_ws, hipStream_t stream) {
+  using namespace rh3;
+  clear_error();
+  RH3_REQUIRE(M >= 0 && K >= 0 && K % 16 == 0, "fake_nvfp4: K=%lld must be a multiple of 16", (long long)K);
+  if (M == 0 || K == 0) return RH3_OK;
+  RH3_REQUIRE(x && out && amax_ws, "fake_nvfp4: null pointer");
+  RH3_REQUIRE(x_dtype == RH3_DTYPE_BF16 || x_dtype == RH3_DTYPE_F32, "fake_nvfp4: x_dtype %d", x_dtype);
+  RH3_REQUIRE(ldx >= K && ldo >= K && ldo % 8 == 0 && aligned16(out), "fake_nvfp4: strides / alignment");
+  RH3_REQUIRE(M * (K / 16) < (1ll << 31) * 256ll, "fake_nvfp4: tensor too large");
+  unsigned int* am = reinterpret_cast<unsigned int*>(amax_ws);
+  hipLaunchKernelGGL(fill_zero_kernel, dim3(1), dim3(1), 0, stream, am);
+  const int64_t n = M * K;
+  const unsigned grid = static_cast<unsigned>(std::min<int64_t>((n + 255) / 256, 4096));
+  const unsigned gq = static_cast<unsigned>((M * (K / 16) + 255) / 256);
+  if (x_dtype == RH3_DTYPE_BF16) {
+    hipLaunchKernelGGL(absmax_kernel<uint16_t>, dim3(grid), dim3(256), 0, stream, static_cast<const uint16_t*>(x), ldx, M, K, am);
+    hipLaunchKernelGGL(fake_nvfp4_kernel<uint16_t>, dim3(gq), dim3(256), 0, stream, static_cast<const uint16_t*>(x), ldx, M, K,
+                       out, ldo, am);
+  } else {
+    hipLaunchKernelGGL(absmax_kernel<float>, dim3(grid), dim3(256), 0, stream, static_cast<const float*>(x), ldx, M, K, am);
+    hipLaunchKernelGGL(fake_nvfp4_kernel<float>, dim3(gq), dim3(256), 0, stream, static_cast<const float*>(x), ldx, M, K,
+                       out, ldo, am);
+  }
+  return launch_status("fake_nvfp4");
+}

@@ -31,6 +31,7 @@ SIGNATURES = {
     "rh3_rot_quant_heads_i8": ([_P, _I, _I, _I, _I, _P, _I, _P, _P], _C),
     "rh3_convrot_f32": ([_P, _C, _I, _I, _I, _P, _I, _P], _C),
     "rh3_quant_weight_rot_i8": ([_P, _C, _I, _I, _I, _P, _I, _P, _P], _C),
+    "rh3_fake_nvfp4": ([_P, _C, _I, _I, _I, _P, _I, _P, _P], _C),
     "rh3_gemm_i8": ([_P, _I, _P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _P], _C),
     "rh3_gemm_i8_swiglu": ([_P, _I, _P, _P, _I, _P, _P, _I, _I, _I, _I, _P], _C),
     "rh3_gemm_i8_gated": ([_P, _I, _P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _P], _C),

@@ -10,7 +10,8 @@ Differences from the reference, all on purpose:
     torch, kernels.py:88-98);
   * int8_rot weights are rotated exactly (float64 butterflies, rounded once to fp32) instead of by a
     torch fp32 matmul of unspecified order;
-  * the nvfp4 verification modes are not built for gfx950 and raise.
+  * the nvfp4 verification modes run their fp32 round trip on a HIP kernel (rh3_fake_nvfp4) and the
+    bf16 x bf16 product on torch.nn.functional.linear, as the reference does (kernels.py:53-56, :120-122).
 """
 from dataclasses import dataclass
 
@@ -21,7 +22,8 @@ from . import gemm as _gemm, quant as _quant
 
 FP8 = torch.float8_e4m3fn
 FP8_MAX = 448.0
-MODES = ("bf16", "fp8_tensor", "fp8_rowwise", "fp8_rowwise_torch", "int8_rowwise", "int8_fast", "int8_rot")
+MODES = ("bf16", "fp8_tensor", "fp8_rowwise", "fp8_rowwise_torch", "int8_rowwise", "int8_fast", "int8_rot",
+         "nvfp4_fake", "nvfp4_rot_fake")
 
 
 @dataclass
@@ -42,8 +44,9 @@ def quantize_weight(w, mode):
     """kernels.quantize_weight (kernels.py:52-72) for bf16 weights [N, K]."""
     if mode == "int8_fast":
         mode = "int8_rowwise"
-    if mode in ("nvfp4_fake", "nvfp4_rot_fake"):
-        raise NotImplementedError(f"quantize_weight: mode {mode} is not built for gfx950")
+    if mode in ("nvfp4_fake", "nvfp4_rot_fake"):   # verification only: a bf16 weight after the round trip
+        wf = _quant.convrot_f32(w) if mode == "nvfp4_rot_fake" else w.contiguous()
+        return QWeight(_quant.fake_nvfp4_bf16(wf), None)
     if mode == "int8_rot":
         q, s = _quant.quantize_weight_rot(w)
         return QWeight(q, s.t().contiguous())
@@ -83,8 +86,11 @@ def gemm_config(k, n):
 
 def linear(x, qw, mode):
     """y = x @ W^T for x [M, K] bf16 and a QWeight of W [N, K]; returns x.dtype (kernels.py:107-137)."""
-    if mode in ("nvfp4_fake", "nvfp4_rot_fake"):
-        raise NotImplementedError(f"linear: mode {mode} is not built for gfx950")
+    if mode in ("nvfp4_fake", "nvfp4_rot_fake"):   # verification only (kernels.py:120-122)
+        x2 = x.reshape(-1, x.shape[-1]).contiguous()
+        xr = _quant.convrot_f32(x2) if mode == "nvfp4_rot_fake" else x2
+        y = torch.nn.functional.linear(_quant.fake_nvfp4_bf16(xr), qw.q)
+        return y.reshape(*x.shape[:-1], qw.q.shape[0]).to(x.dtype)
     if x.dtype != torch.bfloat16:
         raise TypeError("linear: bf16 activations only")
     x = x.contiguous()

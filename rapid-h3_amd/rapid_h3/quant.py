@@ -194,6 +194,22 @@ def convrot_f32(x):
     return y
 
 
+def fake_nvfp4_bf16(x):
+    """kernels.fake_nvfp4(x).to(torch.bfloat16) (kernels.py:38-49, :56, :122): the NVFP4 round trip of a 2-D GPU
+    tensor (bf16 or fp32, last dim a multiple of 16) on rh3_fake_nvfp4 -> bf16 of the same shape."""
+    if x.ndim != 2 or x.stride(1) != 1 or not x.is_cuda:
+        raise AssertionError("fake_nvfp4: x must be a 2-D GPU tensor with a contiguous last dim (no CPU path)")
+    m, k = x.shape
+    if k % 16:
+        raise AssertionError("fake_nvfp4: the last dim must be a multiple of 16")
+    dt = _dtype_code(x, "fake_nvfp4")
+    out = torch.empty((m, k), device=x.device, dtype=torch.bfloat16)
+    amax = torch.empty(1, device=x.device, dtype=torch.float32)
+    nat.call("rh3_fake_nvfp4", nat.ptr(x), dt, x.stride(0), m, k, nat.ptr(out), out.stride(0), nat.ptr(amax),
+             nat.stream(x.device))
+    return out
+
+
 def quantize_weight_rot(w):
     """kernels.quantize_weight(w, "int8_rot"): per-row INT8 of convrot(w) -> (q [N, K] int8, s [N, 1] fp32)."""
     if w.ndim != 2 or not w.is_cuda:

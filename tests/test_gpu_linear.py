@@ -75,3 +75,46 @@ def test_c1_linear_full_size(dev):
         xq, xs = quant_x(xn)
         assert np.array_equal(y, og.int8_gemm(xq, xs, *oq.quantize_weight(wn, mode))), mode
         assert og.rel_l2(bf16_to_f32(y), exact) < bound, mode
+
+
+def test_nvfp4_verification_modes(dev):
+    """The NVFP4 round trip (kernels.fake_nvfp4 + bf16 cast) on the GPU equals the oracle's bit for bit, on bf16
+    and fp32 rows with outlier and all-zero blocks; quantize_weight / linear in nvfp4_fake and nvfp4_rot_fake give
+    torch's bf16 linear of those round trips (the reference's F.linear, kernels.py:120-122), with QuantLinear too."""
+    import torch
+    from oracle import quant as oq
+    from oracle.numerics import f32_to_bf16
+    from rapid_h3 import kernels, quant
+    from rapid_h3.linear import QuantLinear
+    rng = np.random.default_rng(41)
+    x = (rng.standard_normal((96, 512)) * np.exp(rng.standard_normal((96, 1)))).astype(np.float32)
+    x[:, rng.choice(512, 5, replace=False)] *= 30.0
+    x[7, 32:48] = 0.0
+    xb = f32_to_bf16(x)
+    got = to_np(quant.fake_nvfp4_bf16(torch.from_numpy(xb.view(np.int16)).to(dev).view(torch.bfloat16)))
+    assert np.array_equal(got, f32_to_bf16(oq.fake_nvfp4(bf16_f32(xb))))
+    got32 = to_np(quant.fake_nvfp4_bf16(torch.from_numpy(x).to(dev)))
+    assert np.array_equal(got32, f32_to_bf16(oq.fake_nvfp4(x)))
+    g = torch.Generator(device="cpu").manual_seed(6)
+    w = (0.02 * torch.randn(264, 512, generator=g)).to(torch.bfloat16).to(dev)
+    xt = torch.randn(3, 40, 512, generator=g).to(torch.bfloat16).to(dev)
+    for mode in ("nvfp4_fake", "nvfp4_rot_fake"):
+        qw = kernels.quantize_weight(w, mode)
+        assert qw.scale is None and qw.q.dtype == torch.bfloat16 and tuple(qw.q.shape) == (264, 512)
+        wn = bf16_f32(to_np(w))
+        xn = bf16_f32(to_np(xt.reshape(-1, 512)))
+        if mode == "nvfp4_rot_fake":
+            wn, xn = oq.convrot(wn), oq.convrot(xn)
+        assert np.array_equal(to_np(qw.q), f32_to_bf16(oq.fake_nvfp4(wn)))
+        y = kernels.linear(xt, qw, mode)
+        assert tuple(y.shape) == (3, 40, 264) and y.dtype == torch.bfloat16
+        xf = torch.from_numpy(f32_to_bf16(oq.fake_nvfp4(xn)).view(np.int16)).to(dev).view(torch.bfloat16)
+        ref = torch.nn.functional.linear(xf, qw.q)
+        assert torch.equal(y.reshape(-1, 264), ref)
+        lin = QuantLinear(w, None, mode)
+        assert torch.equal(lin(xt), y)
+
+
+def bf16_f32(u16):
+    from oracle.numerics import bf16_to_f32
+    return bf16_to_f32(u16)

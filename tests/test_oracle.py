@@ -732,3 +732,34 @@ def test_attention_fp8pv_single_key_and_closed_form():
         assert og.rel_l2(oa.attention_fp8pv_from_codes(pp, 128 ** -0.5, tile=tile)[:300], ex) < 0.03
     bad = dict(pp, vscale=(pp["vscale"] / oa.V_FP8_UNSTRETCH).astype(np.float32))
     assert og.rel_l2(oa.attention_fp8pv_from_codes(bad, 128 ** -0.5)[:300], ex) > 0.1
+
+
+# ----------------------------------------------------------------------------- NVFP4 verification modes
+def test_fake_nvfp4_known_answers():
+    """With the tensor amax 2.625 = 2688 * 2^-10 every scale is exact (gs = 2^-10, the max block's e4m3 scale
+    448, s = 0.4375): values on the e2m1 grid times s come back unchanged, midpoints go to the lower grid value
+    (torch.bucketize with right=False), magnitudes past 6 s clamp to 6 s, a zero block stays zero (its scale
+    becomes 1), the map is odd, and the grid index agrees with torch.bucketize on random inputs."""
+    s = np.float32(0.4375)
+    blk = np.zeros((4, 16), np.float32)
+    blk[0, :8] = oq.E2M1 * s
+    blk[0, 8] = np.float32(2.625)
+    blk[1, :7] = ((oq.E2M1[1:] + oq.E2M1[:-1]) / 2) * s                 # the seven midpoints
+    blk[1, 7] = np.float32(2.625)
+    blk[3, :4] = [0.1, -0.2, 0.3, -0.05]
+    out = oq.fake_nvfp4(blk)
+    assert np.array_equal(out[0], blk[0])
+    assert np.array_equal(out[1, :7], oq.E2M1[:7] * s)
+    assert not out[2].any()
+    assert np.array_equal(oq.fake_nvfp4(-blk), -out)
+    rng = np.random.default_rng(31)
+    x = (rng.standard_normal((64, 64)) * np.exp(rng.standard_normal((64, 1)))).astype(np.float32)
+    y = oq.fake_nvfp4(x)
+    t = torch.from_numpy(x).reshape(-1, 16)
+    gs = (t.abs().amax() / (448.0 * 6.0)).clamp_min(1e-12)
+    sb = (t.abs().amax(dim=1, keepdim=True) / 6.0 / gs).clamp(max=448.0).to(torch.float8_e4m3fn).float() * gs
+    sb = torch.where(sb == 0, torch.ones_like(sb), sb)
+    grid = torch.tensor(oq.E2M1)
+    idx = torch.bucketize((t / sb).abs().clamp(max=6.0), (grid[1:] + grid[:-1]) / 2)
+    assert np.array_equal(np.abs(y.reshape(-1, 16)), (grid[idx] * sb).numpy())
+    assert np.abs(y - x).max() <= np.abs(x).max() / 6 + 1e-6            # at most one grid gap (2 s <= amax / 3)
