@@ -153,6 +153,44 @@ def test_gemm_full_size_qkv(dev):
     assert bool(torch.equal(lhs, rhs))
 
 
+@pytest.mark.parametrize("epi", ["swiglu", "gated"])
+def test_gemm_full_size_ffn(dev, epi):
+    """The other two C2 GEMMs at M = 145,152 with their fused epilogues, on 256 sampled rows against the oracle:
+    FFN-up (N = 16,384, K = 3072) with the SwiGLU epilogue over the swiglu_perm interleave (within 1 bf16 ulp on
+    < 1 % of elements: the exp is approximate on both sides), FFN-down (N = 3072, K = 8192) with the in-place
+    gated residual (bit-exact), and the rows outside the sample untouched by the sampling."""
+    import torch
+    from rapid_h3 import gemm, quant
+    m = 145152
+    n, k = (16384, 3072) if epi == "swiglu" else (3072, 8192)
+    g = torch.Generator(device=dev).manual_seed(7)
+    x = torch.randn(m, k, generator=g, device=dev)
+    x[:, torch.randperm(k, generator=g, device=dev)[:k // 100]] *= 20
+    xb = x.to(torch.bfloat16)
+    del x
+    w = (0.02 * torch.randn(n, k, generator=g, device=dev)).to(torch.bfloat16)
+    xq, xs = quant.quant_rows_i8(xb)
+    wq, ws = quant.quant_rows_i8(w)
+    rows = torch.from_numpy(np.sort(np.random.default_rng(8).choice(m, 256, replace=False))).to(dev)
+    xr, xsr = to_np(xq[rows]), to_np(xs[rows])
+    if epi == "swiglu":
+        perm = gemm.swiglu_perm(n, dev)
+        wp, wsp = wq[perm].contiguous(), ws[perm].t().contiguous()
+        h = gemm.int8_gemm_swiglu(xq, xs, wp, wsp)
+        assert tuple(h.shape) == (m, n // 2)
+        ref = og.int8_gemm_swiglu(xr, xsr, to_np(wp), to_np(wsp))
+        d = _bf16_ulps(to_np(h[rows]), ref)
+        assert d.max() <= 1 and (d > 0).mean() < 0.01
+    else:
+        gate = (0.5 * torch.randn(n, generator=g, device=dev)).to(torch.bfloat16)
+        resid = torch.randn(m, n, generator=g, device=dev).to(torch.bfloat16)
+        r0 = to_np(resid[rows])
+        out = gemm.int8_gemm_gated_residual(xq, xs, wq, ws.t(), gate, resid)
+        assert out.data_ptr() == resid.data_ptr()
+        ref = og.int8_gemm_gated_residual(xr, xsr, to_np(wq), to_np(ws).T, to_np(gate), r0)
+        assert np.array_equal(to_np(resid[rows]), ref)
+
+
 @pytest.mark.parametrize("n,k", [(9216, 3072), (16384, 3072), (3072, 8192)])
 def test_fp8_full_size_c3(dev, n, k):
     """the FP8 (OCP e4m3) row-wise GEMM on the three C2 shapes at M = 145,152, bf16
