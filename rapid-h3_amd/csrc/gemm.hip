@@ -659,19 +659,24 @@ __global__ void __launch_bounds__(512, 2) gemm_persistent_kernel(const GemmArgs 
   const int wm = wave / (NW / 2), wn = wave % (NW / 2);
   const int l32 = lane & 31, g = lane >> 5;
 
-  // global -> LDS copy geometry as in gemm_kernel (swizzle applied on the global side)
-  const int8_t* xp[NL];
-  const int8_t* wp[NL];
+  // global -> LDS copy geometry as in gemm_kernel (swizzle applied on the global side), held as a tile base
+  // (uniform, so in scalar registers) plus a 32-bit byte offset per lane (row r clamped to the last valid row,
+  // 16-byte chunk c): half the vector registers of 64-bit lane pointers, which the epilogues need (the host
+  // keeps 255 * ld + 64 below 2^32)
+  const int8_t* xb = a.x;
+  const int8_t* wb = a.w;
+  uint32_t xo[NL], wo[NL];
   auto tile_ptrs = [&](int64_t m0, int64_t n0) __attribute__((always_inline)) {
+    xb = a.x + m0 * a.ldx;
+    wb = a.w + n0 * a.ldw;
+    const int rmx = static_cast<int>(min<int64_t>(BM - 1, a.M - 1 - m0));
+    const int rmw = static_cast<int>(min<int64_t>(BN - 1, a.N - 1 - n0));
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
       const int p = (NL * wave + i) * 64 + lane, r = p >> 2;
       const int c = (p & 3) ^ (((r >> 1) & 3) ^ ((r >> 3) & 1));
-      int64_t mr = m0 + r, nr = n0 + r;
-      mr = mr < a.M ? mr : a.M - 1;
-      nr = nr < a.N ? nr : a.N - 1;
-      xp[i] = a.x + mr * a.ldx + c * 16;
-      wp[i] = a.w + nr * a.ldw + c * 16;
+      xo[i] = static_cast<uint32_t>(min(r, rmx)) * static_cast<uint32_t>(a.ldx) + c * 16;
+      wo[i] = static_cast<uint32_t>(min(r, rmw)) * static_cast<uint32_t>(a.ldw) + c * 16;
     }
   };
   const int nk = static_cast<int>(a.K / BK);
@@ -679,8 +684,8 @@ __global__ void __launch_bounds__(512, 2) gemm_persistent_kernel(const GemmArgs 
     const int64_t k0 = static_cast<int64_t>(kt) * BK;
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
-      __builtin_amdgcn_global_load_lds(xp[i] + k0, stg + (NL * wave + i) * 1024, 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(wp[i] + k0, stg + TILE_BYTES + (NL * wave + i) * 1024, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(xb + k0 + xo[i], stg + (NL * wave + i) * 1024, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(wb + k0 + wo[i], stg + TILE_BYTES + (NL * wave + i) * 1024, 16, 0, 0);
     }
   };
 
@@ -917,7 +922,9 @@ int run(GemmArgs a, hipStream_t st, const char* name) {
   if constexpr (EPI != EPI_QKV && RH3_GEMM_NW == 8) {
     const int64_t nk = a.K / BK;
     const int cus = device_cus();
-    if (RH3_GEMM_PERSIST && nk % 4 == 0 && nk >= 8 && cus > 0) {
+    // the persistent kernel's 32-bit lane offsets reach 255 rows of either operand
+    const bool off32 = 255 * a.ldx + 64 < (1ll << 32) && 255 * a.ldw + 64 < (1ll << 32);
+    if (RH3_GEMM_PERSIST && nk % 4 == 0 && nk >= 8 && cus > 0 && off32) {
       const int64_t grid = nb < cus ? nb : cus;  // one workgroup per CU (the LDS use admits no second)
       hipLaunchKernelGGL((gemm_persistent_kernel<FP8, EPI>), dim3(static_cast<unsigned>(grid)), dim3(512), 0, st, a);
       return launch_status(name);
