@@ -16,6 +16,8 @@
 //   v_mfma_f32_32x32x16_bf16 (D on rows, queries on lanes, so the per-query rescale is per lane).
 //   The row sum l adds the same bf16-rounded P the MFMA consumes (attn_int8.cu:8-10, :652-656).
 //   K and Vt tiles (8 + 16 KiB per step) go through a 4-slot LDS ring with XOR-swizzled 16-byte chunks.
+//   With one workgroup per CU the grid runs in rounds; a last round at most half full runs as two key
+//   halves per workgroup (fp32 partials), merged by attn_combine_kernel.
 #include <type_traits>
 
 #include "attn_common.hpp"
@@ -136,6 +138,10 @@ struct FwdArgs {
   int64_t o_ss, o_sh;
   int64_t Sq, Sk, Sqpad, Skpad;
   float scale_log2;
+  int nqb;      // query blocks per head; (head, query block) id = h * nqb + qb (query blocks fastest)
+  int nmain;    // workgroups 0 .. nmain-1 run ids 0 .. nmain-1 whole
+  int npair;    // workgroups nmain + i and nmain + npair + i run the two key halves of id nmain + i
+  float* tail;  // [2][npair][FWD_BQ][TAIL_ROW] fp32 partials of the split ids
 };
 
 // K tile: 128 rows (keys) x 128 B, chunk c of row r at c ^ ((r ^ (r >> 3)) & 7)
@@ -147,6 +153,8 @@ __device__ __forceinline__ int vswz(int r, int c) { return r * 256 + ((c ^ (r & 
 // ~168 registers per wave, so a step covers 64 keys. Per wave and step: 8 i8 MFMAs (S^T = K Q^T), 16 bf16
 // MFMAs (O^T += V^T P^T) and ~150 VALU instructions (32 scores: convert, scale, exp2, pack, row sum, max).
 constexpr int FWD_WAVES = 12, FWD_NT = FWD_WAVES * 64, FWD_BQ = FWD_WAVES * 32;
+static_assert(FWD_BQ == attn_ws::FWD_BQ, "workspace layout constants");
+constexpr int TAIL_ROW = attn_ws::TAIL_ROW;
 constexpr int MAGIC_I = 0x4B400000;  // bits of 1.5 * 2^23
 constexpr float MAGIC_F = 12582912.0f;
 constexpr int STEP = 64;  // keys per step
@@ -161,11 +169,15 @@ constexpr float RESCALE_LOG2 = 8.0f;
 // holds K: 64 keys x 128 B (chunk c of row r at c ^ ((r ^ (r >> 3)) & 7)), then V^T: 128 d x 64 keys x
 // 2 B (chunk c of row r at c ^ (r & 7)). Steps past Sk are not run; the ragged last step is a separate
 // instantiation, so the full steps carry no key mask.
-__global__ void __launch_bounds__(FWD_NT, 1) attn_fwd_kernel(const FwdArgs a) {
-  constexpr int KB = STEP * D, VB = D * STEP * 2, SLOT = KB + VB;
-  __shared__ __attribute__((aligned(16))) int8_t ring[4 * SLOT];
-  __shared__ float kscale[4096];  // per-128-key-block K scales of this head (Skpad/128 <= 4096)
-  const int h = blockIdx.y, qb = blockIdx.x;
+// SPLIT: bid < npair runs the first half of the steps of id nmain + bid, bid >= npair the second half of id
+// nmain + bid - npair, and each writes its unnormalised O, running max and row sum to the tail partials.
+constexpr int FWD_SLOT = STEP * D + D * STEP * 2;
+template <bool SPLIT>
+__device__ __forceinline__ void fwd_body(const FwdArgs& a, const int bid, int8_t* ring, float* kscale) {
+  constexpr int KB = STEP * D, SLOT = FWD_SLOT;
+  const int half = SPLIT ? bid / a.npair : 0;
+  const int id = SPLIT ? a.nmain + bid - half * a.npair : bid;
+  const int h = id / a.nqb, qb = id - h * a.nqb;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, g = lane >> 5;
@@ -217,6 +229,8 @@ __global__ void __launch_bounds__(FWD_NT, 1) attn_fwd_kernel(const FwdArgs a) {
   // steps that hold keys below Sk; the key side is padded to 128, so nsteps * 64 <= Skpad
   const int nfull = static_cast<int>(a.Sk / STEP), rem = static_cast<int>(a.Sk % STEP);
   const int nsteps = nfull + (rem > 0);
+  // steps [j0, j1) of this workgroup; a split's first half holds only full steps (nsteps / 2 <= nfull)
+  const int j0 = half ? nsteps / 2 : 0, j1 = SPLIT && !half ? nsteps / 2 : nsteps;
   // wave-uniform LDS bases (lane 0's offsets) of the two copies inside slot 0
   const uint32_t ring_lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(ring));
   const uint32_t dbase0 = ring_lds + __builtin_amdgcn_readfirstlane(dst0);
@@ -392,18 +406,32 @@ __global__ void __launch_bounds__(FWD_NT, 1) attn_fwd_kernel(const FwdArgs a) {
     if (phase == 0) barrier();
   };
 
-  load_step(0);
-  load_step(1);
+  load_step(j0);
+  load_step(j0 + 1);
   // vmcnt(0) through the builtin, so the compiler also sees the Q loads above as complete and adds no
   // wait of its own inside the loop (gfx9 s_waitcnt: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8])
   __builtin_amdgcn_s_waitcnt(0x0f70);
   __syncthreads();
-  if (phase != 0) load_step(2);
-  for (int j = 0; j < nfull; ++j) step(j, std::false_type{});
-  if (rem > 0) step(nfull, std::true_type{});
+  if (phase != 0) load_step(j0 + 2);
+  const int jf = min(j1, nfull);
+  for (int j = j0; j < jf; ++j) step(j, std::false_type{});
+  if (rem > 0 && j1 == nsteps) step(nfull, std::true_type{});
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no global->LDS load outlives the workgroup
 
   const float lt = lrow + __shfl_xor(lrow, 32, 64);
+  if constexpr (SPLIT) {
+    if (q < a.Sq) {
+      float* tp = a.tail + ((static_cast<int64_t>(half) * a.npair + (id - a.nmain)) * FWD_BQ + wave * 32 + l32) * TAIL_ROW;
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int rq = 0; rq < 4; ++rq)
+          *reinterpret_cast<float4*>(tp + db * 32 + 8 * rq + 4 * g) =
+              make_float4(o[db][4 * rq], o[db][4 * rq + 1], o[db][4 * rq + 2], o[db][4 * rq + 3]);
+      if (g == 0) *reinterpret_cast<float2*>(tp + D) = make_float2(mref, lt);
+    }
+    return;
+  }
   const float il = 1.0f / lt;
   if (q < a.Sq) {
     uint16_t* op = a.out + q * a.o_ss + static_cast<int64_t>(h) * a.o_sh;
@@ -418,6 +446,51 @@ __global__ void __launch_bounds__(FWD_NT, 1) attn_fwd_kernel(const FwdArgs a) {
         *reinterpret_cast<uint2*>(op + d) = w;
       }
   }
+}
+
+// One launch: the unsplit workgroups first, then the split halves, which take CUs as the last unsplit
+// workgroups finish. The LDS ring and scale table are declared once, shared by both bodies.
+__global__ void __launch_bounds__(FWD_NT, 1) attn_fwd_kernel(const FwdArgs a) {
+  __shared__ __attribute__((aligned(16))) int8_t ring[4 * FWD_SLOT];
+  __shared__ float kscale[4096];  // per-128-key-block K scales of this head (Skpad/128 <= 4096)
+  const int bid = static_cast<int>(blockIdx.x);
+  if (bid < a.nmain)
+    fwd_body<false>(a, bid, ring, kscale);
+  else
+    fwd_body<true>(a, bid - a.nmain, ring, kscale);
+}
+
+// Merge of the two key halves of a split workgroup: m = max(m0, m1), O = (O0 2^(m0-m) + O1 2^(m1-m)) / l with
+// l = l0 2^(m0-m) + l1 2^(m1-m). grid (npair, FWD_BQ / 16), 256 threads: 16 queries x 16 lanes of 8 dims.
+__global__ void __launch_bounds__(256) attn_combine_kernel(const float* __restrict__ tail, int npair, int nmain,
+                                                           int nqb, int64_t Sq, uint16_t* __restrict__ out,
+                                                           int64_t o_ss, int64_t o_sh) {
+  const int pair = blockIdx.x, ql = blockIdx.y * 16 + (threadIdx.x >> 4), c = threadIdx.x & 15;
+  const int id = nmain + pair, h = id / nqb, qb = id - h * nqb;
+  const int64_t q = static_cast<int64_t>(qb) * FWD_BQ + ql;
+  if (q >= Sq) return;
+  const float* t0 = tail + (static_cast<int64_t>(pair) * FWD_BQ + ql) * TAIL_ROW;
+  const float* t1 = t0 + static_cast<int64_t>(npair) * FWD_BQ * TAIL_ROW;
+  const float2 ml0 = *reinterpret_cast<const float2*>(t0 + D), ml1 = *reinterpret_cast<const float2*>(t1 + D);
+  const float m = fmaxf(ml0.x, ml1.x);
+  const float a0 = __builtin_amdgcn_exp2f(ml0.x - m), a1 = __builtin_amdgcn_exp2f(ml1.x - m);
+  const float il = 1.0f / (ml0.y * a0 + ml1.y * a1);
+  float r[8];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const float4 x = *reinterpret_cast<const float4*>(t0 + 8 * c + 4 * i);
+    const float4 y = *reinterpret_cast<const float4*>(t1 + 8 * c + 4 * i);
+    r[4 * i + 0] = (x.x * a0 + y.x * a1) * il;
+    r[4 * i + 1] = (x.y * a0 + y.y * a1) * il;
+    r[4 * i + 2] = (x.z * a0 + y.z * a1) * il;
+    r[4 * i + 3] = (x.w * a0 + y.w * a1) * il;
+  }
+  uint4 w;
+  w.x = pk_bf16(r[0], r[1]);
+  w.y = pk_bf16(r[2], r[3]);
+  w.z = pk_bf16(r[4], r[5]);
+  w.w = pk_bf16(r[6], r[7]);
+  *reinterpret_cast<uint4*>(out + q * o_ss + static_cast<int64_t>(h) * o_sh + 8 * c) = w;
 }
 
 // ------------------------------------------------------------------ host
@@ -465,9 +538,24 @@ int prepass(const uint16_t* q, int64_t q_ss, int64_t q_sh, const uint16_t* k, in
 
 int forward(const Work& w, int64_t Sq, int64_t Sk, int64_t H, float scale, uint16_t* out, int64_t o_ss,
             int64_t o_sh, hipStream_t st) {
-  FwdArgs f{w.q8, w.qs, w.k8, w.ks, w.vt, out, o_ss, o_sh, Sq, Sk, pad(Sq), pad(Sk),
-            scale * 1.4426950408889634f};
-  hipLaunchKernelGGL(attn_fwd_kernel, dim3((Sq + FWD_BQ - 1) / FWD_BQ, H), dim3(FWD_NT), 0, st, f);
+  const int64_t nwg = attn_ws::fwd_blocks(Sq, H);
+  RH3_REQUIRE(nwg < (int64_t{1} << 31) / FWD_NT, "attention forward: %lld workgroups exceed the grid limit",
+              (long long)nwg);
+  const int nqb = static_cast<int>((Sq + FWD_BQ - 1) / FWD_BQ);
+  // One workgroup per CU: the grid runs in rounds of `cus` workgroups. When the last round is at most half
+  // full, its workgroups run as two key halves each (a round half as long) and a merge kernel combines them.
+  const int cus = device_cus();
+  const int64_t last = cus > 0 ? nwg % cus : 0;
+  const int64_t nsteps = (Sk + STEP - 1) / STEP;
+  const int npair = w.tail && nwg > cus && last > 0 && 2 * last <= cus && last <= attn_ws::TAIL_MAX && nsteps >= 8
+                        ? static_cast<int>(last) : 0;
+  const int nmain = static_cast<int>(nwg - npair);
+  const FwdArgs f{w.q8, w.qs, w.k8, w.ks, w.vt, out, o_ss, o_sh, Sq, Sk, pad(Sq), pad(Sk),
+                  scale * 1.4426950408889634f, nqb, nmain, npair, w.tail};
+  hipLaunchKernelGGL(attn_fwd_kernel, dim3(static_cast<uint32_t>(nmain + 2 * npair)), dim3(FWD_NT), 0, st, f);
+  if (npair > 0)
+    hipLaunchKernelGGL(attn_combine_kernel, dim3(npair, FWD_BQ / 16), dim3(256), 0, st, w.tail, npair, nmain, nqb, Sq,
+                       out, o_ss, o_sh);
   return launch_status("attention forward");
 }
 

@@ -18,8 +18,16 @@ __host__ __device__ inline int64_t up256(int64_t b) { return (b + 255) / 256 * 2
 __host__ __device__ inline int64_t nchunks(int64_t s) { return (s + CHUNK - 1) / CHUNK; }
 
 // per-128-block recipe (bf16 P.V)
+constexpr int FWD_BQ = 384;     // queries per main-kernel workgroup
+constexpr int TAIL_MAX = 128;   // most (head, query block) workgroups whose keys the main kernel splits in two
+constexpr int TAIL_ROW = D + 4; // floats per query of a split partial: O[128], running max, row sum, 2 unused
+
+// (head, query block) workgroups of the main kernel
+__host__ __device__ inline int64_t fwd_blocks(int64_t Sq, int64_t H) { return (Sq + FWD_BQ - 1) / FWD_BQ * H; }
+
 struct Work {
   int8_t* q8; float* qs; int8_t* k8; float* ks; float* kmean; double* part; uint16_t* vt;
+  float* tail;  // [2][npair][FWD_BQ][TAIL_ROW] partials of the split last round; null when not reserved
   int64_t bytes;
 };
 
@@ -36,6 +44,9 @@ inline Work layout(void* base, int64_t Sq, int64_t Sk, int64_t H) {
   w.kmean = reinterpret_cast<float*>(take(H * D * 4));
   w.part = reinterpret_cast<double*>(take(H * nchunk * D * 8));
   w.vt = reinterpret_cast<uint16_t*>(take(H * D * skp * 2));
+  // only a grid larger than TAIL_MAX workgroups can leave a last round worth splitting
+  const int64_t nwg = fwd_blocks(Sq, H);
+  w.tail = nwg > TAIL_MAX ? reinterpret_cast<float*>(take(int64_t{2} * TAIL_MAX * FWD_BQ * TAIL_ROW * 4)) : nullptr;
   w.bytes = off;
   return w;
 }

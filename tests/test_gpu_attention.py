@@ -109,8 +109,37 @@ def test_attention_strided_out(dev):
     assert rel_l2(got, ref) < TOL
 
 
+def test_attention_split_tail(dev):
+    """A grid whose last round (one workgroup of 384 queries per CU) is at most half full: those workgroups
+    run as two key halves, each writing fp32 partials, merged by attn_combine_kernel. H is chosen from the
+    device's CU count so that 7 query blocks x H heads leave 16..cus/2 workgroups in the last round; the
+    heads holding them and head 0 (unsplit) against the oracle."""
+    import torch
+    from rapid_h3 import attention
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    s, nqb = 2600, 7  # 7 query blocks of 384; 41 key steps of 64, the last one ragged
+    h = next(hh for hh in range(1, 100000) if nqb * hh > cus and 16 <= (nqb * hh) % cus <= min(cus // 2, 128))
+    last = (nqb * h) % cus
+    tail_heads = sorted({i // nqb for i in range(nqb * h - last, nqb * h)})
+    rng = np.random.default_rng(21)
+    q = _bf(rng.standard_normal((s, h, 128)))
+    k = _bf(rng.standard_normal((s, h, 128)) + 2.0 * rng.standard_normal((1, h, 128)))
+    v = _bf(rng.standard_normal((s, h, 128)))
+    out = bf16_to_f32(to_np(attention.attention(to_dev(q, dev), to_dev(k, dev), to_dev(v, dev))))
+    assert np.isfinite(out).all()
+    for hh in [0] + tail_heads:
+        q8, qs, k8, ks, _ = oa.prepass(q[:, hh:hh + 1], k[:, hh:hh + 1])
+        ref = oa.attention_from_codes(q8, qs, k8, ks, v[:, hh:hh + 1], 128 ** -0.5)[:s, 0]
+        assert rel_l2(out[:, hh], ref) < TOL, hh
+        # each split query block on its own, so a wrong merge of one pair cannot hide in the head's norm
+        for i in range(nqb * h - last, nqb * h):
+            if i // nqb == hh:
+                r0, r1 = (i % nqb) * 384, min((i % nqb + 1) * 384, s)
+                assert rel_l2(out[r0:r1, hh], ref[r0:r1]) < TOL, (hh, i % nqb)
+
+
 def test_attention_full_size_sampled(dev):
-    """C4: S = 145,152, H = 24, D = 128 with a per-head K offset ~ N(0, 2). Codes, scales and kmean of 2
+    """C4: S = 145,152, H = 24, D = 128 with a per-head K offset ~ N(0, 2). Codes, scales and kmean of 3
     sampled heads bit-exact; output on 48 sampled query rows x those heads within tolerance, and
     against the unquantized float64 attention within 3 %."""
     import torch
@@ -123,7 +152,7 @@ def test_attention_full_size_sampled(dev):
     qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
     pp = attention.prepass(qd, kd, vd)
     out = attention.attention(qd, kd, vd)
-    heads = [3, 17]
+    heads = [3, 17, 23]  # on 256 CUs, query blocks 266-377 of head 23 form the split last round
     rows = np.sort(np.random.default_rng(3).choice(s, 48, replace=False))
     qn = q.view(torch.int16).numpy().view(np.uint16)
     kn = k.view(torch.int16).numpy().view(np.uint16)
