@@ -154,7 +154,7 @@ def rope_table(positions, rot=96, theta=10000.0):
 
 # ---------------------------------------------------------------- production numerics (configs 80-99)
 # The reference's production attention (attn_int8.cu config 80 = attn_fwd8 :2250-2511; configs 90/94 run the
-# same math on a persistent schedule, attn_cake/DESIGN.md "bit-identical to config 80"):
+# same math on a persistent schedule, csrc/attn_cake/DESIGN.md in the reference: "bit-identical to config 80"):
 #   pre-pass  (attn_int8.cu:2568-2644)
 #     * kmean, vmean: per-head channel means over all S tokens (K after the optional RMSNorm + RoPE);
 #       vscale = max(max(vmax - vm, vm - vmin), 1e-6) / 127                                (:97-109)

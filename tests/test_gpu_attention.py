@@ -109,23 +109,30 @@ def test_attention_strided_out(dev):
     assert rel_l2(got, ref) < TOL
 
 
-def test_attention_split_tail(dev):
+@pytest.mark.parametrize("sk,head_major", [(2600, False), (1100, True)])
+def test_attention_split_tail(dev, sk, head_major):
     """A grid whose last round (one workgroup of 384 queries per CU) is at most half full: those workgroups
     run as two key halves, each writing fp32 partials, merged by attn_combine_kernel. H is chosen from the
     device's CU count so that 7 query blocks x H heads leave 16..cus/2 workgroups in the last round; the
-    heads holding them and head 0 (unsplit) against the oracle."""
+    heads holding them and head 0 (unsplit) against the oracle. Self-attention with [S, H, D] output, and
+    cross-attention (1,100 keys: 18 steps, the last ragged) into a head-major [1, H, S, D] buffer."""
     import torch
     from rapid_h3 import attention
     cus = torch.cuda.get_device_properties(0).multi_processor_count
-    s, nqb = 2600, 7  # 7 query blocks of 384; 41 key steps of 64, the last one ragged
+    s, nqb = 2600, 7  # 7 query blocks of 384; 2,600 keys = 41 key steps of 64, the last one ragged
     h = next(hh for hh in range(1, 100000) if nqb * hh > cus and 16 <= (nqb * hh) % cus <= min(cus // 2, 128))
     last = (nqb * h) % cus
     tail_heads = sorted({i // nqb for i in range(nqb * h - last, nqb * h)})
-    rng = np.random.default_rng(21)
+    rng = np.random.default_rng(21 + sk)
     q = _bf(rng.standard_normal((s, h, 128)))
-    k = _bf(rng.standard_normal((s, h, 128)) + 2.0 * rng.standard_normal((1, h, 128)))
-    v = _bf(rng.standard_normal((s, h, 128)))
-    out = bf16_to_f32(to_np(attention.attention(to_dev(q, dev), to_dev(k, dev), to_dev(v, dev))))
+    k = _bf(rng.standard_normal((sk, h, 128)) + 2.0 * rng.standard_normal((1, h, 128)))
+    v = _bf(rng.standard_normal((sk, h, 128)))
+    if head_major:
+        o = torch.empty(1, h, s, 128, dtype=torch.bfloat16, device=dev)
+        attention.attention(to_dev(q, dev), to_dev(k, dev), to_dev(v, dev), out=o[0].transpose(0, 1))
+        out = bf16_to_f32(to_np(o[0].transpose(0, 1)))
+    else:
+        out = bf16_to_f32(to_np(attention.attention(to_dev(q, dev), to_dev(k, dev), to_dev(v, dev))))
     assert np.isfinite(out).all()
     for hh in [0] + tail_heads:
         q8, qs, k8, ks, _ = oa.prepass(q[:, hh:hh + 1], k[:, hh:hh + 1])
