@@ -144,10 +144,11 @@ struct FwdArgs {
   float* tail;  // [2][npair][FWD_BQ][TAIL_ROW] fp32 partials of the split ids
 };
 
-// K tile: 128 rows (keys) x 128 B, chunk c of row r at c ^ ((r ^ (r >> 3)) & 7)
-__device__ __forceinline__ int kswz(int r, int c) { return r * 128 + ((c ^ ((r ^ (r >> 3)) & 7)) << 4); }
-// Vt tile: 128 rows (d) x 256 B, chunk c of row r at c ^ (r & 15)
-__device__ __forceinline__ int vswz(int r, int c) { return r * 256 + ((c ^ (r & 15)) << 4); }
+// XOR swizzle of the 16-byte chunks of a V^T slot row d (128 B rows): chunk c at c ^ vsw(d). gfx950 serves a
+// 16-byte LDS read 16 lanes at a time over 64 banks; the 16 lanes of a P.V fragment read rows d .. d+15 at one
+// chunk, and rows d and d+8 share a bank group under c ^ (d & 7) (a 2-way conflict on every V read, 40 % of the
+// kernel's LDS cycles). Folding in d >> 3 spreads the 16 rows over 16 groups.
+__device__ __forceinline__ int vsw(int d) { return ((d & 31) ^ ((d & 31) >> 3)) & 7; }
 
 // 12 waves (3 per SIMD), 32 queries each = 384 queries per workgroup (three 128-query scale blocks);
 // ~168 registers per wave, so a step covers 64 keys. Per wave and step: 8 i8 MFMAs (S^T = K Q^T), 16 bf16
@@ -167,7 +168,7 @@ constexpr float RESCALE_LOG2 = 8.0f;
 // Step j (64 keys) reads K(j) and V^T(j) from ring slot j % 4 and first loads K(j+2), V^T(j+2) into slot
 // (j+2) % 4, last read in step j-2 (every wave has passed the end-of-step barrier of step j-1). A slot
 // holds K: 64 keys x 128 B (chunk c of row r at c ^ ((r ^ (r >> 3)) & 7)), then V^T: 128 d x 64 keys x
-// 2 B (chunk c of row r at c ^ (r & 7)). Steps past Sk are not run; the ragged last step is a separate
+// 2 B (chunk c of row r at c ^ vsw(r)). Steps past Sk are not run; the ragged last step is a separate
 // instantiation, so the full steps carry no key mask.
 // SPLIT: bid < npair runs the first half of the steps of id nmain + bid, bid >= npair the second half of id
 // nmain + bid - npair, and each writes its unnormalised O, running max and row sum to the tail partials.
@@ -213,7 +214,7 @@ __device__ __forceinline__ void fwd_body(const FwdArgs& a, const int bid, int8_t
     };
     auto vpos = [&](int p, const int8_t*& src, int& dst) {
       const int d = p >> 3, pc = p & 7;
-      src = reinterpret_cast<const int8_t*>(vbase + static_cast<int64_t>(d) * a.Skpad + ((pc ^ (d & 7)) << 3));
+      src = reinterpret_cast<const int8_t*>(vbase + static_cast<int64_t>(d) * a.Skpad + ((pc ^ vsw(d)) << 3));
       dst = KB + p * 16;
     };
     if (wave < 8) {
@@ -245,7 +246,7 @@ __device__ __forceinline__ void fwd_body(const FwdArgs& a, const int bid, int8_t
   // Lane parts of the LDS read addresses inside a slot. K fragment (kb, ds): row kb*32 + l32, chunk
   // 2ds + g, stored at chunk ^ ((row ^ (row >> 3)) & 7) = (2ds ^ 4kb) ^ y with y = (g ^ l32 ^ (l32 >> 3)) & 7,
   // so the 8 reads use 4 lane offsets koff[(2ds ^ 4kb) / 2] plus the immediate kb * 4096. V^T fragment
-  // (kb, m, db): row db*32 + l32, chunk 4kb + 2m + g at chunk ^ (l32 & 7): 4 lane offsets voff[2kb + m]
+  // (kb, m, db): row db*32 + l32, chunk 4kb + 2m + g at chunk ^ vsw(l32): 4 lane offsets voff[2kb + m]
   // plus the immediate KB + db * 4096.
   uint32_t koff[4], voff[4];
   {
@@ -253,7 +254,7 @@ __device__ __forceinline__ void fwd_body(const FwdArgs& a, const int bid, int8_t
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       koff[i] = ring_lds + l32 * 128 + (((2 * i) ^ y) << 4);
-      voff[i] = ring_lds + l32 * 128 + (((2 * i + g) ^ (l32 & 7)) << 4);
+      voff[i] = ring_lds + l32 * 128 + (((2 * i + g) ^ vsw(l32)) << 4);
     }
   }
 
