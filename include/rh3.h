@@ -243,7 +243,8 @@ int rh3_attention_forward(int64_t Sq, int64_t Sk, int64_t H, float scale,
  * ------------------------------------------------------------------------------------------- */
 
 /* Byte offsets of the arrays inside an attention workspace for (Sq, Sk, H), with the workspace size last.
- * numerics 0 (rh3_attention_workspace_bytes): q8, qs, k8, ks, kmean, part, vt, bytes (8 values);
+ * numerics 0 (rh3_attention_workspace_bytes): q8, qs, k8, ks, kmean, part, vt, kn, bytes (9 values; kn [H, Skpad/128]
+ * fp32: per 128-key block, an upper bound of the largest L2 norm of a key's int8 codes);
  * numerics 1 (rh3_attention_u8_workspace_bytes): q8, qs, k8, ks, side, vt, kmean, vmean, vscale, kpart, vsum,
  * vmax, vmin, bytes (14 values). No device access. No counterpart in the reference, whose operands are
  * separate torch tensors (attn_int8.cu:2568-2644); callers use it to view what rh3_gemm_i8_qkv wrote. */

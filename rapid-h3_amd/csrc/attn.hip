@@ -33,10 +33,14 @@ constexpr int BLK = 128;     // quantization block and attention tile (tokens)
 // ------------------------------------------------------------------ per-block quantizer
 // grid (H, Spad/128) (heads fastest, so the workgroups of one token block run together and share its rope-table
 // rows in L2), 256 threads: wave w handles tokens w*32 .. w*32+31 of the block, 4 per pass
+// knorm (K only, may be null): per block, an upper bound of the largest L2 norm of a token's 128 int8 codes,
+// which lets the main kernel bound every logit of the block without scanning its scores
 __global__ void __launch_bounds__(256) quant_kernel(const uint16_t* __restrict__ x, int64_t x_ss, int64_t x_sh,
                                                     int64_t S, int64_t Spad, RR rr, const float* __restrict__ mean,
-                                                    int8_t* __restrict__ codes, float* __restrict__ scales) {
+                                                    int8_t* __restrict__ codes, float* __restrict__ scales,
+                                                    float* __restrict__ knorm) {
   __shared__ float wmax[4];
+  __shared__ int wnorm[4];
   const int h = blockIdx.x, blk = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l16 = lane & 15, sub = lane >> 4;
   float mv[8] = {0, 0, 0, 0, 0, 0, 0, 0};
@@ -73,18 +77,38 @@ __global__ void __launch_bounds__(256) quant_kernel(const uint16_t* __restrict__
   const float sc = fmaxf(bm, 1e-8f) / 127.0f;
   const float inv = 1.0f / sc;
   if (tid == 0) scales[static_cast<int64_t>(h) * (Spad / BLK) + blk] = sc;
+  int n2 = 0;  // largest sum of squared codes over this lane's rows (each row's sum spans its 16 lanes)
 #pragma unroll
   for (int p = 0; p < 8; ++p) {
     const int64_t s = static_cast<int64_t>(blk) * BLK + wave * 32 + p * 4 + sub;
     // rint(x / sc) clamped to +-127: the multiply by 1/sc decides all lanes but those within 2^-12 of a
     // half-integer, and one wave vote per 8 values sends only those through the IEEE division
-    *reinterpret_cast<uint2*>(codes + (static_cast<int64_t>(h) * Spad + s) * D + 8 * l16) = quant8_i8(v[p], sc, inv);
+    const uint2 c8 = quant8_i8(v[p], sc, inv);
+    *reinterpret_cast<uint2*>(codes + (static_cast<int64_t>(h) * Spad + s) * D + 8 * l16) = c8;
+    if (knorm) {
+      int r = __builtin_amdgcn_sdot4(static_cast<int>(c8.x), static_cast<int>(c8.x), 0, false);
+      r = __builtin_amdgcn_sdot4(static_cast<int>(c8.y), static_cast<int>(c8.y), r, false);
+#pragma unroll
+      for (int o = 1; o < 16; o <<= 1) r += __shfl_xor(r, o, 64);
+      n2 = max(n2, r);
+    }
+  }
+  if (knorm) {
+#pragma unroll
+    for (int o = 16; o < 64; o <<= 1) n2 = max(n2, __shfl_xor(n2, o, 64));
+    if (lane == 0) wnorm[wave] = n2;
+    __syncthreads();
+    if (tid == 0) {
+      // the integer is exact in fp32 (<= 128 * 127^2); sqrt rounded, then pushed up past any rounding
+      const int m = max(max(wnorm[0], wnorm[1]), max(wnorm[2], wnorm[3]));
+      knorm[static_cast<int64_t>(h) * (Spad / BLK) + blk] = sqrtf(static_cast<float>(m)) * 1.0001f;
+    }
   }
 }
 
 void launch_quant(dim3 grid, hipStream_t st, const uint16_t* x, int64_t x_ss, int64_t x_sh, int64_t S, int64_t Spad,
-                  const RR& rr, const float* mean, int8_t* codes, float* scales) {
-  hipLaunchKernelGGL(quant_kernel, grid, dim3(256), 0, st, x, x_ss, x_sh, S, Spad, rr, mean, codes, scales);
+                  const RR& rr, const float* mean, int8_t* codes, float* scales, float* knorm) {
+  hipLaunchKernelGGL(quant_kernel, grid, dim3(256), 0, st, x, x_ss, x_sh, S, Spad, rr, mean, codes, scales, knorm);
 }
 
 // ------------------------------------------------------------------ V transpose
@@ -133,6 +157,7 @@ struct FwdArgs {
   const float* qs;   // [H][Sqpad/128]
   const int8_t* k8;  // [H][Skpad][128]
   const float* ks;   // [H][Skpad/128]
+  const float* kn;   // [H][Skpad/128] bound of the largest L2 norm of a key's codes per block
   const uint16_t* vt;  // [H][128][Skpad]
   uint16_t* out;
   int64_t o_ss, o_sh;
@@ -144,6 +169,11 @@ struct FwdArgs {
   float* tail;  // [2][npair][FWD_BQ][TAIL_ROW] fp32 partials of the split ids
 };
 
+// a wave-uniform float (lane 0's value), held in an SGPR
+__device__ __forceinline__ float uniform(float x) {
+  return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(x)));
+}
+
 // XOR swizzle of the 16-byte chunks of a V^T slot row d (128 B rows): chunk c at c ^ vsw(d). gfx950 serves a
 // 16-byte LDS read 16 lanes at a time over 64 banks; the 16 lanes of a P.V fragment read rows d .. d+15 at one
 // chunk, and rows d and d+8 share a bank group under c ^ (d & 7) (a 2-way conflict on every V read, 40 % of the
@@ -151,31 +181,34 @@ struct FwdArgs {
 __device__ __forceinline__ int vsw(int d) { return ((d & 31) ^ ((d & 31) >> 3)) & 7; }
 
 // 12 waves (3 per SIMD), 32 queries each = 384 queries per workgroup (three 128-query scale blocks);
-// ~168 registers per wave, so a step covers 64 keys. Per wave and step: 8 i8 MFMAs (S^T = K Q^T), 16 bf16
-// MFMAs (O^T += V^T P^T) and ~150 VALU instructions (32 scores: convert, scale, exp2, pack, row sum, max).
+// at most 168 registers per wave, so a step covers 64 keys. Per wave and step: 8 i8 MFMAs (S^T = K Q^T), 16 bf16
+// MFMAs (O^T += V^T P^T) and ~105 VALU instructions (the softmax of 32 scores per lane). Each 32x32 MFMA also
+// holds the SIMD's VALU issue for a few cycles, so the kernel is bound by VALU issue as much as by the MFMA pipe:
+// every vector instruction the step does not need is taken out (no vector address arithmetic for the copies, and
+// no score scan while a bound proves the running max is still good).
 constexpr int FWD_WAVES = 12, FWD_NT = FWD_WAVES * 64, FWD_BQ = FWD_WAVES * 32;
 static_assert(FWD_BQ == attn_ws::FWD_BQ, "workspace layout constants");
 constexpr int TAIL_ROW = attn_ws::TAIL_ROW;
 constexpr int MAGIC_I = 0x4B400000;  // bits of 1.5 * 2^23
 constexpr float MAGIC_F = 12582912.0f;
 constexpr int STEP = 64;  // keys per step
-#ifndef ATT_PHASES
-#define ATT_PHASES 0x010  // nibble i: the barrier phase of waves 4i..4i+3 (one per SIMD), see the main loop
-#endif
-// lazy rescale: the reference max moves only when a step max exceeds it by more than 2^8 (P <= 256)
+// lazy rescale: after a scan, the reference max moves only when the step max exceeds it by more than 2^8
 constexpr float RESCALE_LOG2 = 8.0f;
+// no scan while every logit of the step is provably below mref + 2^6 (then P < 2^64: O and l stay far from the
+// fp32 range for |v| < 2^40, and bf16 P keeps its relative precision at any magnitude)
+constexpr float BOUND_LOG2 = 64.0f;
+constexpr int KSLOT = STEP * D;      // K tile: 64 keys x 128 B, chunk c of row r at c ^ ((r ^ (r >> 3)) & 7)
+constexpr int VSLOT = D * STEP * 2;  // V^T tile: 128 d x 64 keys x 2 B, chunk c of row d at c ^ vsw(d)
+constexpr int NRING = 4;             // slots of the K ring and of the V^T ring
 
-// Step j (64 keys) reads K(j) and V^T(j) from ring slot j % 4 and first loads K(j+2), V^T(j+2) into slot
-// (j+2) % 4, last read in step j-2 (every wave has passed the end-of-step barrier of step j-1). A slot
-// holds K: 64 keys x 128 B (chunk c of row r at c ^ ((r ^ (r >> 3)) & 7)), then V^T: 128 d x 64 keys x
-// 2 B (chunk c of row r at c ^ vsw(r)). Steps past Sk are not run; the ragged last step is a separate
-// instantiation, so the full steps carry no key mask.
+// Step j reads K(j) and V^T(j) from ring slot u = (j - j0) % 4 and first copies K(j+2), V^T(j+2) into slot
+// (u + 2) % 4, last read in step j-2 (every wave has passed the end-of-step barrier of step j-1). Steps past Sk
+// are not run; the ragged last step is a separate instantiation, so the full steps carry no key mask.
 // SPLIT: bid < npair runs the first half of the steps of id nmain + bid, bid >= npair the second half of id
 // nmain + bid - npair, and each writes its unnormalised O, running max and row sum to the tail partials.
-constexpr int FWD_SLOT = STEP * D + D * STEP * 2;
 template <bool SPLIT>
-__device__ __forceinline__ void fwd_body(const FwdArgs& a, const int bid, int8_t* ring, float* kscale) {
-  constexpr int KB = STEP * D, SLOT = FWD_SLOT;
+__device__ __forceinline__ void fwd_body(const FwdArgs& a, const int bid, int8_t* kring, int8_t* vring,
+                                         float2* kscale) {
   const int half = SPLIT ? bid / a.npair : 0;
   const int id = SPLIT ? a.nmain + bid - half * a.npair : bid;
   const int h = id / a.nqb, qb = id - h * a.nqb;
@@ -193,68 +226,76 @@ __device__ __forceinline__ void fwd_body(const FwdArgs& a, const int bid, int8_t
 #pragma unroll
     for (int ds = 0; ds < 4; ++ds) qf[ds] = qin ? *reinterpret_cast<const v4i*>(qp + ds * 32) : v4i{0, 0, 0, 0};
   }
-  const float qscale = (qin ? a.qs[static_cast<int64_t>(h) * (a.Sqpad / BLK) + (q >> 7)] : 0.0f) * a.scale_log2;
-  const int nkb = static_cast<int>(a.Skpad / BLK);
-  for (int i = tid; i < nkb; i += FWD_NT) kscale[i] = a.ks[static_cast<int64_t>(h) * nkb + i];
-
-  const int8_t* kbase = a.k8 + static_cast<int64_t>(h) * a.Skpad * D;
-  const uint16_t* vbase = a.vt + static_cast<int64_t>(h) * D * a.Skpad;
-  // Loads go global -> LDS directly (lane l of a wave writes LDS base + 16*l), so the XOR swizzle is
-  // applied on the global side. K slot: 512 chunk positions (64 rows x 8), loaded by waves 0-7 (one
-  // instruction each); V^T slot: 1024 positions (128 rows x 8), waves 0-7 fill positions 64w + lane and
-  // waves 8-11 positions 512 + 64*(2(w-8) + i) + lane. Every wave issues exactly two loads per step.
-  const int8_t* src0;
-  const int8_t* src1;
-  int dst0, dst1;  // byte offsets inside a slot
+  // a wave's 32 queries lie in one 128-query scale block, all below Sqpad or all past it: the scale is uniform
+  const float qscale = uniform((qin ? a.qs[static_cast<int64_t>(h) * (a.Sqpad / BLK) + (q >> 7)] : 0.0f) * a.scale_log2);
+  // |q8 . k8| <= |q8| |k8|: the wave's largest query norm (each lane's 64 codes plus the partner lane's 64),
+  // pushed up past the roundings of the bound below, times the query scale
+  float qbound;
   {
-    auto kpos = [&](int p, const int8_t*& src, int& dst) {
-      const int row = p >> 3, pc = p & 7;
-      src = kbase + row * 128 + ((pc ^ ((row ^ (row >> 3)) & 7)) << 4);
-      dst = p * 16;
-    };
-    auto vpos = [&](int p, const int8_t*& src, int& dst) {
-      const int d = p >> 3, pc = p & 7;
-      src = reinterpret_cast<const int8_t*>(vbase + static_cast<int64_t>(d) * a.Skpad + ((pc ^ vsw(d)) << 3));
-      dst = KB + p * 16;
-    };
-    if (wave < 8) {
-      kpos(wave * 64 + lane, src0, dst0);
-      vpos(wave * 64 + lane, src1, dst1);
-    } else {
-      vpos(512 + (2 * (wave - 8)) * 64 + lane, src0, dst0);
-      vpos(512 + (2 * (wave - 8) + 1) * 64 + lane, src1, dst1);
-    }
+    int n2 = 0;
+#pragma unroll
+    for (int ds = 0; ds < 4; ++ds)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) n2 = __builtin_amdgcn_sdot4(qf[ds][e], qf[ds][e], n2, false);
+    n2 += __shfl_xor(n2, 32, 64);
+#pragma unroll
+    for (int o = 1; o < 32; o <<= 1) n2 = max(n2, __shfl_xor(n2, o, 64));
+    qbound = uniform(qscale * (sqrtf(static_cast<float>(n2)) * 1.0001f));
   }
-  // per-step advance of the two sources: K rows move 64 keys x 128 B, V^T columns 64 keys x 2 B
-  const int64_t adv0 = wave < 8 ? STEP * D : STEP * 2, adv1 = STEP * 2;
-  // steps that hold keys below Sk; the key side is padded to 128, so nsteps * 64 <= Skpad
+  const int nkb = static_cast<int>(a.Skpad / BLK);
+  for (int i = tid; i < nkb; i += FWD_NT) {
+    const float ksc = a.ks[static_cast<int64_t>(h) * nkb + i];
+    kscale[i] = make_float2(ksc, ksc * a.kn[static_cast<int64_t>(h) * nkb + i]);
+  }
+
+  // Copies go global -> LDS directly (lane l of a wave writes LDS base + 16*l), so the XOR swizzles are applied on
+  // the global side. K slot: 512 chunk positions (64 rows x 8), one copy each for waves 0-7; V^T slot: 1024
+  // positions (128 rows x 8), waves 0-7 one copy each (positions 64w + lane), waves 8-11 two each (positions
+  // 512 + 64(2(w-8) + i) + lane). Position p of a slot is its byte 16p. Each copy is a per-step scalar base plus a
+  // fixed lane offset.
+  const int8_t* kbase = a.k8 + static_cast<int64_t>(h) * a.Skpad * D;
+  const int8_t* vbase = reinterpret_cast<const int8_t*>(a.vt + static_cast<int64_t>(h) * D * a.Skpad);
+  auto kpos = [&](int p) { const int row = p >> 3, pc = p & 7; return row * 128 + ((pc ^ ((row ^ (row >> 3)) & 7)) << 4); };
+  auto vpos = [&](int p) {
+    const int d = p >> 3, pc = p & 7;
+    return static_cast<int>(d * a.Skpad * 2 + ((pc ^ vsw(d)) << 4));
+  };
+  const bool kwave = wave < 8;
+  const uint32_t go0 = static_cast<uint32_t>(kwave ? kpos(wave * 64 + lane) : vpos(512 + 2 * (wave - 8) * 64 + lane));
+  const uint32_t go1 = static_cast<uint32_t>(kwave ? vpos(wave * 64 + lane) : vpos(512 + (2 * (wave - 8) + 1) * 64 + lane));
+  const uint32_t ds0 = static_cast<uint32_t>(kwave ? wave * 1024 : 8192 + 2 * (wave - 8) * 1024);
+  const uint32_t ds1 = static_cast<uint32_t>(kwave ? wave * 1024 : 8192 + (2 * (wave - 8) + 1) * 1024);
+  const uint32_t kring_lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(kring));
+  const uint32_t vring_lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(vring));
   const int nfull = static_cast<int>(a.Sk / STEP), rem = static_cast<int>(a.Sk % STEP);
   const int nsteps = nfull + (rem > 0);
   // steps [j0, j1) of this workgroup; a split's first half holds only full steps (nsteps / 2 <= nfull)
   const int j0 = half ? nsteps / 2 : 0, j1 = SPLIT && !half ? nsteps / 2 : nsteps;
-  // wave-uniform LDS bases (lane 0's offsets) of the two copies inside slot 0
-  const uint32_t ring_lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(ring));
-  const uint32_t dbase0 = ring_lds + __builtin_amdgcn_readfirstlane(dst0);
-  const uint32_t dbase1 = ring_lds + __builtin_amdgcn_readfirstlane(dst1);
   auto load_step = [&](int j) __attribute__((always_inline)) {
-    const uint32_t so = static_cast<uint32_t>(j & 3) * SLOT;
-    j = min(j, nsteps - 1);  // clamped: every step issues the same two loads; the copy lands unread
-    lds_dma16(src0 + adv0 * j, dbase0 + so);
-    lds_dma16(src1 + adv1 * j, dbase1 + so);
+    const uint32_t u = static_cast<uint32_t>(j - j0) & (NRING - 1);
+    const int jj = min(j, nsteps - 1);  // clamped: every step issues the same copies; the copy lands unread
+    const int8_t* vb = vbase + static_cast<int64_t>(jj) * (STEP * 2);
+    if (kwave) {
+      lds_dma16_s(kbase + static_cast<int64_t>(jj) * KSLOT, go0, kring_lds + u * KSLOT + ds0);
+      lds_dma16_s(vb, go1, vring_lds + u * VSLOT + ds1);
+    } else {
+      lds_dma16_s(vb, go0, vring_lds + u * VSLOT + ds0);
+      lds_dma16_s(vb, go1, vring_lds + u * VSLOT + ds1);
+    }
   };
 
-  // Lane parts of the LDS read addresses inside a slot. K fragment (kb, ds): row kb*32 + l32, chunk
+  // Lane parts of the LDS read addresses inside slot 0. K fragment (kb, ds): row kb*32 + l32, chunk
   // 2ds + g, stored at chunk ^ ((row ^ (row >> 3)) & 7) = (2ds ^ 4kb) ^ y with y = (g ^ l32 ^ (l32 >> 3)) & 7,
-  // so the 8 reads use 4 lane offsets koff[(2ds ^ 4kb) / 2] plus the immediate kb * 4096. V^T fragment
-  // (kb, m, db): row db*32 + l32, chunk 4kb + 2m + g at chunk ^ vsw(l32): 4 lane offsets voff[2kb + m]
-  // plus the immediate KB + db * 4096.
+  // so the 8 reads use 4 lane offsets koff[(2ds ^ 4kb) / 2] plus the slot's u*KSLOT and the immediate kb*4096. V^T
+  // fragment (kb, m, db): row db*32 + l32, chunk 4kb + 2m + g at chunk ^ vsw(l32): 4 lane offsets voff[2kb + m]
+  // plus u*VSLOT and the immediate db*4096.
   uint32_t koff[4], voff[4];
   {
     const int y = (g ^ l32 ^ (l32 >> 3)) & 7;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      koff[i] = ring_lds + l32 * 128 + (((2 * i) ^ y) << 4);
-      voff[i] = ring_lds + l32 * 128 + (((2 * i + g) ^ vsw(l32)) << 4);
+      koff[i] = kring_lds + l32 * 128 + (((2 * i) ^ y) << 4);
+      voff[i] = vring_lds + l32 * 128 + (((2 * i + g) ^ vsw(l32)) << 4);
     }
   }
 
@@ -271,17 +312,13 @@ __device__ __forceinline__ void fwd_body(const FwdArgs& a, const int bid, int8_t
 #pragma unroll
   for (int r = 0; r < 16; ++r) magic[r] = MAGIC_I;
 
-  // S^T[key][query] = K8 . Q8^T of step j: lane (l32, g) of s[kb] holds query l32 and step keys
+  // S^T[key][query] = K8 . Q8^T of the step in slot U: lane (l32, g) of s[kb] holds query l32 and step keys
   // kb*32 + 8*(r/4) + 4*g + r%4
   v16i s[2];
-  auto qk = [&](const int j) __attribute__((always_inline)) {
-    const uint32_t so = static_cast<uint32_t>(j & 3) * SLOT;
+  auto qk = [&](const uint32_t u) __attribute__((always_inline)) {
     uint32_t ka[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) ka[i] = koff[i] + so;
-#ifdef RH3_SETPRIO
-    __builtin_amdgcn_s_setprio(1);
-#endif
+    for (int i = 0; i < 4; ++i) ka[i] = koff[i] + u * KSLOT;
 #pragma unroll
     for (int ds = 0; ds < 4; ++ds) {
 #pragma unroll
@@ -290,26 +327,29 @@ __device__ __forceinline__ void fwd_body(const FwdArgs& a, const int bid, int8_t
         s[kb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf, qf[ds], ds == 0 ? magic : s[kb], 0, 0, 0);
       }
     }
-#ifdef RH3_SETPRIO
-    __builtin_amdgcn_s_setprio(0);
-#endif
   };
   // online softmax of step j's scores and O^T += V^T(j) . P^T; TAIL steps hold 1..63 keys below Sk
   uint32_t pk[2][8];  // P of the current step, bf16 pairs, the B operand of the P.V MFMAs
   auto softmax = [&](const int j, auto tail) __attribute__((always_inline)) {
     constexpr bool TAIL = decltype(tail)::value;
-    // c > 0, so the step's max score is c * (max int32 accumulator over the valid keys); a tail step
-    // holds key j*64, so every query's max covers at least one key
     const int nvalid = TAIL ? static_cast<int>(a.Sk - static_cast<int64_t>(j) * STEP) : STEP;
-    int mi = INT_MIN;
+    const float2 kk = kscale[j >> 1];
+    const float c = qscale * kk.x;
+    // Every logit of the step is at most qbound * kk.y (Cauchy-Schwarz on the codes, in the exp2 domain). While
+    // that is below mref + 64 for all the wave's queries the step needs no max; otherwise scan the step's
+    // scores (c > 0, so the max score is c * the max int32 accumulator over the valid keys; a tail step holds key
+    // j*64, so every query's max covers at least one key) and move mref if the max passed it by 2^8.
+    float mt = -INFINITY;
+    if (__builtin_amdgcn_ballot_w64(qbound * kk.y > mref + BOUND_LOG2) != 0) {
+      int mi = INT_MIN;
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+      for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int r = 0; r < 16; ++r)
-        if (!TAIL || kb * 32 + 8 * (r >> 2) + 4 * g + (r & 3) < nvalid) mi = max(mi, s[kb][r]);
-    mi = max_halves(mi);
-    const float c = qscale * kscale[j >> 1];
-    const float mt = static_cast<float>(mi - MAGIC_I) * c;
+        for (int r = 0; r < 16; ++r)
+          if (!TAIL || kb * 32 + 8 * (r >> 2) + 4 * g + (r & 3) < nvalid) mi = max(mi, s[kb][r]);
+      mi = max_halves(mi);
+      mt = static_cast<float>(mi - MAGIC_I) * c;
+    }
     if (__builtin_amdgcn_ballot_w64(mt > mref + RESCALE_LOG2) != 0) {
       const float mnew = fmaxf(mref, mt);
       const float alpha = __builtin_amdgcn_exp2f(mref - mnew);
@@ -323,7 +363,7 @@ __device__ __forceinline__ void fwd_body(const FwdArgs& a, const int bid, int8_t
     // the accumulator holds the bits of 1.5*2^23 + acc, so fma(bits, c, nb) = acc c - mref with the constant
     // nb = -1.5*2^23 c - mref rounded once: the same rounding error for every score of this query and step
     const float nb = fmaf(-MAGIC_F, c, -mref);
-    // P = 2^(t - mref) in bf16 (P <= 2^8); keys past Sk get P = 0 (lane mask on the packed words)
+    // P = 2^(t - mref) in bf16 (P < 2^64); keys past Sk get P = 0 (lane mask on the packed words)
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -349,15 +389,11 @@ __device__ __forceinline__ void fwd_body(const FwdArgs& a, const int bid, int8_t
       for (int w = 0; w < 8; ++w)
         lrow = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2bf, pk[kb][w]), ones, lrow, false);
   };
-  // O^T[d][query] += V^T(j) . P^T
-  auto pv = [&](const int j) __attribute__((always_inline)) {
-    const uint32_t so = static_cast<uint32_t>(j & 3) * SLOT;
+  // O^T[d][query] += V^T . P^T of the step in slot u
+  auto pv = [&](const uint32_t u) __attribute__((always_inline)) {
     uint32_t va[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) va[i] = voff[i] + so;
-#ifdef RH3_SETPRIO
-    __builtin_amdgcn_s_setprio(1);
-#endif
+    for (int i = 0; i < 4; ++i) va[i] = voff[i] + u * VSLOT;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
@@ -367,44 +403,35 @@ __device__ __forceinline__ void fwd_body(const FwdArgs& a, const int bid, int8_t
         const v8bf pf = __builtin_bit_cast(v8bf, pw);
 #pragma unroll
         for (int db = 0; db < 4; ++db) {
-          const v4i vw = lds_read16(va[2 * kb + m] + KB + db * 4096);
+          const v4i vw = lds_read16(va[2 * kb + m] + db * 4096);
           o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, vw), pf, o[db], 0, 0, 0);
         }
       }
     }
-#ifdef RH3_SETPRIO
-    __builtin_amdgcn_s_setprio(0);
-#endif
   };
 
-  // Barrier B_j ends the use of ring slot j. Every wave runs qk(0), softmax(0), pv(0), qk(1), ... and meets
-  // B_j at one of three places, by phase: 0 after pv(j), 1 after qk(j), 2 after softmax(j). Between B_(j-1)
-  // and B_j a phase-0 wave runs qk(j) softmax(j) pv(j), a phase-1 wave softmax(j-1) pv(j-1) qk(j), a phase-2
-  // wave pv(j-1) qk(j) softmax(j): the three waves of a SIMD (one of each) rotate through MFMA, VALU, MFMA
-  // work, so one of them is on the VALU while the other two feed the MFMA pipe. Each wave issues the two
-  // loads of step j+2 right after B_(j-1), into slot (j+2) % 4, whose last readers (pv(j-2) of phases 1
-  // and 2) ran before B_(j-1); before B_j it waits for its loads of step j+1 (vmcnt(2) leaves the two
-  // issued after B_(j-1) in flight), so slot j+1 is complete past B_j.
-  const int phase = (ATT_PHASES >> (4 * (wave >> 2))) & 0xF;
+  // Barrier B_j ends the use of ring slot j. Waves 0-3 and 8-11 meet B_j after pv(j); waves 4-7 (one per SIMD)
+  // meet it after qk(j+1), half a step behind, so their softmax runs while the other two waves of the SIMD issue
+  // MFMAs. Each wave issues the copies of step j+2 right after B_(j-1), into the slot whose last readers (pv(j-2)
+  // of the lagging waves) ran before B_(j-1); before B_j it waits for its copies of step j+1 (vmcnt(2) leaves the
+  // two issued after B_(j-1) in flight), so slot j+1 is complete past B_j.
+  const bool lag = (wave >> 2) == 1;
   auto barrier = [&]() __attribute__((always_inline)) {
     asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
   };
   auto step = [&](const int j, auto tail) __attribute__((always_inline)) {
-    if (phase == 0) load_step(j + 2);
-    qk(j);
-    if (phase == 1) {
+    const uint32_t slot = static_cast<uint32_t>(j - j0) & (NRING - 1);
+    if (!lag) load_step(j + 2);
+    qk(slot);
+    if (lag) {
       barrier();
       load_step(j + 3);
     }
     softmax(j, tail);
-    if (phase == 2) {
-      barrier();
-      load_step(j + 3);
-    }
-    pv(j);
-    if (phase == 0) barrier();
+    pv(slot);
+    if (!lag) barrier();
   };
 
   load_step(j0);
@@ -413,11 +440,11 @@ __device__ __forceinline__ void fwd_body(const FwdArgs& a, const int bid, int8_t
   // wait of its own inside the loop (gfx9 s_waitcnt: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8])
   __builtin_amdgcn_s_waitcnt(0x0f70);
   __syncthreads();
-  if (phase != 0) load_step(j0 + 2);
+  if (lag) load_step(j0 + 2);
   const int jf = min(j1, nfull);
   for (int j = j0; j < jf; ++j) step(j, std::false_type{});
   if (rem > 0 && j1 == nsteps) step(nfull, std::true_type{});
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no global->LDS load outlives the workgroup
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no global->LDS copy outlives the workgroup
 
   const float lt = lrow + __shfl_xor(lrow, 32, 64);
   if constexpr (SPLIT) {
@@ -450,15 +477,15 @@ __device__ __forceinline__ void fwd_body(const FwdArgs& a, const int bid, int8_t
 }
 
 // One launch: the unsplit workgroups first, then the split halves, which take CUs as the last unsplit
-// workgroups finish. The LDS ring and scale table are declared once, shared by both bodies.
+// workgroups finish. The LDS rings and scale table are declared once, shared by both bodies.
 __global__ void __launch_bounds__(FWD_NT, 1) attn_fwd_kernel(const FwdArgs a) {
-  __shared__ __attribute__((aligned(16))) int8_t ring[4 * FWD_SLOT];
-  __shared__ float kscale[4096];  // per-128-key-block K scales of this head (Skpad/128 <= 4096)
+  __shared__ __attribute__((aligned(16))) int8_t ring[NRING * (KSLOT + VSLOT)];
+  __shared__ float2 kscale[4096];  // per-128-key-block (K scale, K scale x key-norm bound) of this head
   const int bid = static_cast<int>(blockIdx.x);
   if (bid < a.nmain)
-    fwd_body<false>(a, bid, ring, kscale);
+    fwd_body<false>(a, bid, ring, ring + NRING * KSLOT, kscale);
   else
-    fwd_body<true>(a, bid - a.nmain, ring, kscale);
+    fwd_body<true>(a, bid - a.nmain, ring, ring + NRING * KSLOT, kscale);
 }
 
 // Merge of the two key halves of a split workgroup: m = max(m0, m1), O = (O0 2^(m0-m) + O1 2^(m1-m)) / l with
@@ -529,10 +556,9 @@ int prepass(const uint16_t* q, int64_t q_ss, int64_t q_sh, const uint16_t* k, in
     // a fill kernel, not hipMemsetAsync, so the call stays safe inside a captured HIP graph
     hipLaunchKernelGGL(zero_kernel, dim3((H * D + 255) / 256), dim3(256), 0, st, w.kmean, H * D);
   }
-  launch_quant(dim3(H, sqp / BLK), st, q, q_ss, q_sh, Sq, sqp, rq,
-                     static_cast<const float*>(nullptr), w.q8, w.qs);
-  launch_quant(dim3(H, skp / BLK), st, k, k_ss, k_sh, Sk, skp, rk, mean, w.k8,
-                     w.ks);
+  launch_quant(dim3(H, sqp / BLK), st, q, q_ss, q_sh, Sq, sqp, rq, static_cast<const float*>(nullptr), w.q8, w.qs,
+               nullptr);
+  launch_quant(dim3(H, skp / BLK), st, k, k_ss, k_sh, Sk, skp, rk, mean, w.k8, w.ks, w.kn);
   hipLaunchKernelGGL(vt_kernel, dim3(H, skp / 64), dim3(256), 0, st, v, v_ss, v_sh, Sk, skp, w.vt);
   return launch_status("attention prepass");
 }
@@ -551,7 +577,7 @@ int forward(const Work& w, int64_t Sq, int64_t Sk, int64_t H, float scale, uint1
   const int npair = w.tail && nwg > cus && last > 0 && 2 * last <= cus && last <= attn_ws::TAIL_MAX && nsteps >= 8
                         ? static_cast<int>(last) : 0;
   const int nmain = static_cast<int>(nwg - npair);
-  const FwdArgs f{w.q8, w.qs, w.k8, w.ks, w.vt, out, o_ss, o_sh, Sq, Sk, pad(Sq), pad(Sk),
+  const FwdArgs f{w.q8, w.qs, w.k8, w.ks, w.kn, w.vt, out, o_ss, o_sh, Sq, Sk, pad(Sq), pad(Sk),
                   scale * 1.4426950408889634f, nqb, nmain, npair, w.tail};
   hipLaunchKernelGGL(attn_fwd_kernel, dim3(static_cast<uint32_t>(nmain + 2 * npair)), dim3(FWD_NT), 0, st, f);
   if (npair > 0)
@@ -628,8 +654,7 @@ extern "C" int rh3_attention_prepass_qkv(const uint16_t* k, int64_t k_ss, int64_
   } else {
     hipLaunchKernelGGL(zero_kernel, dim3((H * D + 255) / 256), dim3(256), 0, stream, w.kmean, H * D);
   }
-  launch_quant(dim3(H, skp / BLK), stream, k, k_ss, k_sh, S, skp, rk, mean, w.k8,
-                     w.ks);
+  launch_quant(dim3(H, skp / BLK), stream, k, k_ss, k_sh, S, skp, rk, mean, w.k8, w.ks, w.kn);
   hipLaunchKernelGGL(vt_kernel, dim3(H, skp / 64), dim3(256), 0, stream, v, v_ss, v_sh, S, skp, w.vt);
   if (int e = launch_status("attention prepass_qkv")) return e;
   ptrs[0] = w.q8; ptrs[1] = w.qs; ptrs[2] = w.k8; ptrs[3] = w.ks; ptrs[4] = w.kmean; ptrs[5] = w.vt;

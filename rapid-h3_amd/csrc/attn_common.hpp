@@ -130,6 +130,18 @@ __device__ __forceinline__ void lds_dma16(const void* gptr, uint32_t lds_base) {
                : "memory");
 }
 
+// The same copy addressed as a wave-uniform 64-bit base in SGPRs plus a 32-bit per-lane byte offset (the
+// saddr form): a kernel that walks a tile sequence advances the base with scalar adds and keeps the lane
+// offsets fixed, so the per-step address arithmetic costs no vector instructions.
+__device__ __forceinline__ void lds_dma16_s(const void* sbase, uint32_t voff, uint32_t lds_base) {
+  uint32_t saved;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2\n\t"
+               "s_nop 0\n\ts_mov_b32 m0, %0"
+               : "=&s"(saved)
+               : "v"(voff), "s"(sbase), "s"(lds_base)
+               : "memory");
+}
+
 }  // namespace
 }  // namespace attn
 }  // namespace rh3

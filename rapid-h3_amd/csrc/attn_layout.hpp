@@ -27,6 +27,7 @@ __host__ __device__ inline int64_t fwd_blocks(int64_t Sq, int64_t H) { return (S
 
 struct Work {
   int8_t* q8; float* qs; int8_t* k8; float* ks; float* kmean; double* part; uint16_t* vt;
+  float* kn;    // [H][Skpad/128]: per 128-key block, an upper bound of the largest L2 norm of a key's int8 codes
   float* tail;  // [2][npair][FWD_BQ][TAIL_ROW] partials of the split last round; null when not reserved
   int64_t bytes;
 };
@@ -44,6 +45,7 @@ inline Work layout(void* base, int64_t Sq, int64_t Sk, int64_t H) {
   w.kmean = reinterpret_cast<float*>(take(H * D * 4));
   w.part = reinterpret_cast<double*>(take(H * nchunk * D * 8));
   w.vt = reinterpret_cast<uint16_t*>(take(H * D * skp * 2));
+  w.kn = reinterpret_cast<float*>(take(H * (skp / BLK) * 4));
   // only a grid larger than TAIL_MAX workgroups can leave a last round worth splitting
   const int64_t nwg = fwd_blocks(Sq, H);
   w.tail = nwg > TAIL_MAX ? reinterpret_cast<float*>(take(int64_t{2} * TAIL_MAX * FWD_BQ * TAIL_ROW * 4)) : nullptr;

@@ -876,9 +876,9 @@ extern "C" int rh3_attention_workspace_layout(int numerics, int64_t Sq, int64_t 
   auto off = [&](const void* p) { return static_cast<int64_t>(static_cast<const char*>(p) - b); };
   if (numerics == 0) {
     const attn_ws::Work w = attn_ws::layout(b, Sq, Sk, H);
-    const void* ps[7] = {w.q8, w.qs, w.k8, w.ks, w.kmean, w.part, w.vt};
-    for (int i = 0; i < 7; ++i) offsets[i] = off(ps[i]);
-    offsets[7] = w.bytes;
+    const void* ps[8] = {w.q8, w.qs, w.k8, w.ks, w.kmean, w.part, w.vt, w.kn};
+    for (int i = 0; i < 8; ++i) offsets[i] = off(ps[i]);
+    offsets[8] = w.bytes;
     return RH3_OK;
   }
   RH3_REQUIRE(numerics == 1, "attention_workspace_layout: numerics %d (0 per-block, 1 production)", numerics);

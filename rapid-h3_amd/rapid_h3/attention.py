@@ -319,7 +319,7 @@ def _blk_views(ws, ptrs, sq, sk, h):
 def workspace_offsets(numerics, sq, sk, h):
     """Byte offsets of the workspace arrays (rh3_attention_workspace_layout), as a dict."""
     import ctypes
-    names = (("q8", "qs", "k8", "ks", "kmean", "part", "vt", "bytes") if numerics == 0 else
+    names = (("q8", "qs", "k8", "ks", "kmean", "part", "vt", "kn", "bytes") if numerics == 0 else
              ("q8", "qs", "k8", "ks", "side", "vt", "kmean", "vmean", "vscale", "kpart", "vsum", "vmax", "vmin",
               "bytes"))
     offs = (ctypes.c_int64 * len(names))()
