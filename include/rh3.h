@@ -190,6 +190,18 @@ int rh3_int8_attention(const uint16_t* q, int64_t q_ss, int64_t q_sh,
                        uint16_t* out, int64_t o_ss, int64_t o_sh,
                        void* workspace, int64_t workspace_bytes, hipStream_t stream);
 
+/* rh3_int8_attention without a workspace argument, for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart in the
+ * reference. The pre-pass operands live in a 64 MiB device array of the library, one per GPU, held until the
+ * process ends; sizes whose operands need more (rh3_attention_workspace_bytes less the split partials, roughly
+ * 512 bytes per token and head) fail with RH3_EINVAL. The call allocates nothing and calls no allocating
+ * routine. All calls on one GPU share the array: calls that overlap there (two streams, two host threads) race. */
+int rh3_int8_attention_noalloc(const uint16_t* q, int64_t q_ss, int64_t q_sh,
+                               const uint16_t* k, int64_t k_ss, int64_t k_sh,
+                               const uint16_t* v, int64_t v_ss, int64_t v_sh,
+                               int64_t Sq, int64_t Sk, int64_t H, float scale, int smooth_k,
+                               uint16_t* out, int64_t o_ss, int64_t o_sh, hipStream_t stream);
+
 /* Same, with the per-head RMSNorm (weights qw/kw [128] bf16, eps) and split-half RoPE (table
  * tab [S, rot/2, 2, 2] bf16 = (cos, -sin, sin, cos), rot 96 or 128) applied to raw q and k inside
  * the pre-pass. Self-attention only (Sq == Sk == S).

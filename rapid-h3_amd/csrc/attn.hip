@@ -18,6 +18,7 @@
 //   K and Vt tiles (8 + 16 KiB per step) go through a 4-slot LDS ring with XOR-swizzled 16-byte chunks.
 //   With one workgroup per CU the grid runs in rounds; a last round at most half full runs as two key
 //   halves per workgroup (fp32 partials), merged by attn_combine_kernel.
+#include <mutex>
 #include <type_traits>
 
 #include "attn_common.hpp"
@@ -596,7 +597,69 @@ int check_rr(const char* name, const uint16_t* tab, int rot, const uint16_t* qw,
 }  // namespace
 }  // namespace rh3
 
+// ------------------------------------------------------------------ allocation-free variant
+// The workspace of rh3_int8_attention_noalloc: a file-scope device array, one copy per GPU for the life of the
+// process. Host code never passes `scratch` itself (in host code the name is only a stand-in): each device's
+// address comes from hipGetSymbolAddress once, with that device current, and is kept in g_scratch.
+constexpr int64_t NOALLOC_SCRATCH_BYTES = int64_t{64} << 20;
+static __device__ __align__(256) char scratch[NOALLOC_SCRATCH_BYTES];
+
+namespace rh3 {
+namespace {
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void* g_scratch[MAX_DEVICES] = {};
+
+// this GPU's scratch address: the device of the stream (the current device for the null stream)
+int scratch_of(hipStream_t stream, void** out) {
+  int cur = 0;
+  RH3_REQUIRE(hipGetDevice(&cur) == hipSuccess, "int8_attention_noalloc: no current HIP device");
+  int dev = cur;
+  if (stream) RH3_REQUIRE(hipStreamGetDevice(stream, &dev) == hipSuccess, "int8_attention_noalloc: bad stream");
+  RH3_REQUIRE(dev >= 0 && dev < MAX_DEVICES, "int8_attention_noalloc: device %d beyond %d", dev, MAX_DEVICES);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    if (dev != cur) RH3_REQUIRE(hipSetDevice(dev) == hipSuccess, "int8_attention_noalloc: hipSetDevice(%d)", dev);
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (dev != cur) (void)hipSetDevice(cur);
+    RH3_REQUIRE(e == hipSuccess && p, "int8_attention_noalloc: hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                hipGetErrorString(e));
+    g_scratch[dev] = p;
+  }
+  *out = g_scratch[dev];
+  return RH3_OK;
+}
+}  // namespace
+}  // namespace rh3
+
 using namespace rh3;
+
+// rh3_int8_attention without a workspace argument: the pre-pass operands live in this GPU's 64 MiB scratch array,
+// and the main kernel runs every workgroup whole (no split last round, whose partials would need more room). The
+// pre-pass writes every element the main kernel reads, so nothing is cleared first. Calls that overlap on one GPU
+// (two streams, or two host threads) share the array and race.
+extern "C" int rh3_int8_attention_noalloc(const uint16_t* q, int64_t q_ss, int64_t q_sh, const uint16_t* k,
+                                          int64_t k_ss, int64_t k_sh, const uint16_t* v, int64_t v_ss, int64_t v_sh,
+                                          int64_t Sq, int64_t Sk, int64_t H, float scale, int smooth_k, uint16_t* out,
+                                          int64_t o_ss, int64_t o_sh, hipStream_t stream) {
+  clear_error();
+  if (int e = check_qkv("int8_attention_noalloc", q, q_ss, q_sh, k, k_ss, k_sh, v, v_ss, v_sh, Sq, Sk, H)) return e;
+  RH3_REQUIRE(out && (reinterpret_cast<uintptr_t>(out) & 7) == 0 && o_ss % 4 == 0 && o_sh % 4 == 0,
+              "int8_attention_noalloc: out must be 8-byte aligned with strides multiple of 4");
+  const int64_t need = layout(nullptr, Sq, Sk, H, false).bytes;
+  RH3_REQUIRE(need <= NOALLOC_SCRATCH_BYTES,
+              "int8_attention_noalloc: Sq=%lld Sk=%lld H=%lld needs %lld bytes of scratch, beyond its %lld-byte maximum "
+              "(rh3_int8_attention takes a workspace of any size)", (long long)Sq, (long long)Sk, (long long)H,
+              (long long)need, (long long)NOALLOC_SCRATCH_BYTES);
+  void* base = nullptr;
+  if (int e = scratch_of(stream, &base)) return e;
+  const Work w = layout(base, Sq, Sk, H, false);
+  const RR none{nullptr, nullptr, 0.f, 0};
+  if (int e = prepass(q, q_ss, q_sh, k, k_ss, k_sh, v, v_ss, v_sh, Sq, Sk, H, none, none, smooth_k, w, stream))
+    return e;
+  return forward(w, Sq, Sk, H, scale, out, o_ss, o_sh, stream);
+}
 
 extern "C" int64_t rh3_attention_workspace_bytes(int64_t Sq, int64_t Sk, int64_t H) {
   if (Sq <= 0 || Sk <= 0 || H <= 0) return 0;

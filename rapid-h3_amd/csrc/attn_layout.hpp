@@ -32,7 +32,8 @@ struct Work {
   int64_t bytes;
 };
 
-inline Work layout(void* base, int64_t Sq, int64_t Sk, int64_t H) {
+// split false: no room for the split-last-round partials (the main kernel then runs every workgroup whole)
+inline Work layout(void* base, int64_t Sq, int64_t Sk, int64_t H, bool split = true) {
   const int64_t sqp = pad(Sq), skp = pad(Sk), nchunk = nchunks(Sk);
   char* p = static_cast<char*>(base);
   int64_t off = 0;
@@ -48,7 +49,8 @@ inline Work layout(void* base, int64_t Sq, int64_t Sk, int64_t H) {
   w.kn = reinterpret_cast<float*>(take(H * (skp / BLK) * 4));
   // only a grid larger than TAIL_MAX workgroups can leave a last round worth splitting
   const int64_t nwg = fwd_blocks(Sq, H);
-  w.tail = nwg > TAIL_MAX ? reinterpret_cast<float*>(take(int64_t{2} * TAIL_MAX * FWD_BQ * TAIL_ROW * 4)) : nullptr;
+  w.tail = split && nwg > TAIL_MAX ? reinterpret_cast<float*>(take(int64_t{2} * TAIL_MAX * FWD_BQ * TAIL_ROW * 4))
+                                   : nullptr;
   w.bytes = off;
   return w;
 }

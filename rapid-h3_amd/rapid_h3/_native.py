@@ -40,6 +40,7 @@ SIGNATURES = {
     "rh3_gemm_fp8": ([_P, _I, _P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _P], _C),
     "rh3_attention_workspace_bytes": ([_I, _I, _I], ctypes.c_int64),
     "rh3_int8_attention": ([_P, _I, _I, _P, _I, _I, _P, _I, _I, _I, _I, _I, _F, _C, _P, _I, _I, _P, _I, _P], _C),
+    "rh3_int8_attention_noalloc": ([_P, _I, _I, _P, _I, _I, _P, _I, _I, _I, _I, _I, _F, _C, _P, _I, _I, _P], _C),
     "rh3_int8_attention_rr": ([_P, _I, _I, _P, _I, _I, _P, _I, _I, _I, _I, _P, _C, _P, _P, _F, _F, _C, _P, _I, _I,
                                _P, _I, _P], _C),
     "rh3_attention_forward": ([_I, _I, _I, _F, _P, _I, _I, _P, _I, _P], _C),

@@ -43,6 +43,9 @@ def test_argument_validation_without_gpu():
     st = lib.rh3_int8_attention(fake, 128, 128, fake, 128, 128, fake, 128, 128, 10, 10, 1, 0.1, 1, fake, 128, 128,
                                 fake, 16, None)
     assert st == 1 and "workspace" in nat.last_error()
+    st = lib.rh3_int8_attention_noalloc(fake, 128, 128, fake, 128, 128, fake, 128, 128, 1 << 19, 1 << 19, 1, 0.1, 1,
+                                        fake, 128, 128, None)
+    assert st == 1 and "beyond its" in nat.last_error()
     st = lib.rh3_int8_attention_rr(fake, 128, 128, fake, 128, 128, fake, 128, 128, 10, 1, fake, 64, fake, fake,
                                    1e-5, 0.1, 1, fake, 128, 128, fake, 1 << 30, None)
     assert st == 1 and "rot_dim" in nat.last_error()
