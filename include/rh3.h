@@ -27,6 +27,7 @@ extern "C" {
 
 #define RH3_DTYPE_BF16 1
 #define RH3_DTYPE_F32 2
+#define RH3_DTYPE_F16 3
 
 /* Message of the last failed call on this thread ("" if none). */
 const char* rh3_last_error(void);
@@ -112,6 +113,17 @@ int rh3_convrot_f32(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t 
 int rh3_fake_nvfp4(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t K, uint16_t* out, int64_t ldo,
                    float* amax_ws, hipStream_t stream);
 
+/* Quantizer of any float input (bf16, fp16 or fp32 rows; x_dtype RH3_DTYPE_*), for what the fused quantizers
+ * above do not take: the reference's torch path casts any float with .float() (kernels.py:57-82). mode 0: per-row
+ * int8, s[m] = max(amax_m / 127, 1e-12), q = clamp(rint(x / s), +-127); mode 1: per-row FP8, s[m] = max(amax_m /
+ * 448, 1e-12), q = e4m3(clamp(x / s, +-448)); mode 2: FP8 with one scale per tensor (the fp8_tensor mode,
+ * kernels.py:64-66, :125-128), s[0] = max(amax / 448, 1e-12), amax_ws one float of caller scratch. IEEE quotient.
+ * q [M, K] int8 / e4m3 bytes (row stride ldq).
+ * replaces kernels.quantize_weight / quantize_rows and the fp8_tensor quantization of kernels.linear for
+ * non-bf16 inputs */
+int rh3_quant_any(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t K, int mode,
+                  void* q, int64_t ldq, float* s, float* amax_ws, hipStream_t stream);
+
 /* replaces kernels.quantize_weight(w, "int8_rot") (kernels.py:62-72): convrot(w) (exact, rounded to
  * fp32), then per-row s = max(amax/127, 1e-12), q = round(w_rot / s); w [N, K] bf16 or fp32 */
 int rh3_quant_weight_rot_i8(const void* w, int w_dtype, int64_t ldw, int64_t N, int64_t K,
@@ -142,6 +154,15 @@ int rh3_gemm_i8_swiglu(const int8_t* xq, int64_t ldx, const float* xs, const int
 int rh3_gemm_i8_gated(const int8_t* xq, int64_t ldx, const float* xs, const int8_t* wq, int64_t ldw,
                       const float* ws, const uint16_t* gate, uint16_t* resid, int64_t ldr,
                       int64_t M, int64_t N, int64_t K, hipStream_t stream);
+
+/* Gated residual with a gate row per output row (per-token modulation), in place:
+ * resid[m,n] = bf16_RNE(fma(bf16(y), gate[gidx[m], n], resid[m,n])); gate [R, ldg] bf16 (16-byte aligned,
+ * ldg >= N, ldg % 8 == 0), gidx [M] int32 rows of it.
+ * replaces the per-token branch of _fused_block's gated residual, h3._mod_gate(x, gate, int8_gemm(...),
+ * segments) for segments whose row is a tensor (__init__.py:242-245) */
+int rh3_gemm_i8_gated_rows(const int8_t* xq, int64_t ldx, const float* xs, const int8_t* wq, int64_t ldw,
+                           const float* ws, const uint16_t* gate, int64_t ldg, const int32_t* gidx,
+                           uint16_t* resid, int64_t ldr, int64_t M, int64_t N, int64_t K, hipStream_t stream);
 
 /* Verification: the raw int32 accumulators acc [M, N] (row stride ldc) of the same kernel.
  * No reference counterpart as an entry point: it exposes the s32 accumulator of

@@ -8,6 +8,7 @@ TEST INFRASTRUCTURE ONLY (see oracle/numerics.py).
   * SwiGLU          g, u = bf16(acc * xs * ws) over the swiglu_perm interleave; h = bf16((g*sigmoid(g))*u)
                     fp8_rowwise.cu:24-107 (VisitorSwigluStore), cutlass_fp8.py:55-62
   * gated residual  r = bf16_RNE(fma(fp32(bf16(acc * xs * ws)), gate[n], r))      fp8_rowwise.cu:333-389
+                    (per-token gate rows: gate[rows[m], n], the _mod_gate branch of __init__.py:244-245)
 
 The int8 product is computed as a float64 matrix product of the int8 codes: every partial sum is an
 integer below K * 127^2 < 2^53, so float64 BLAS gives the exact int32 accumulator (and is fast).
@@ -78,6 +79,15 @@ def int8_gemm_gated_residual(xq, xs, wq, ws, gate, resid):
     g = bf16_to_f32(gate).reshape(1, -1)
     r = bf16_to_f32(resid)
     return f32_to_bf16(fma_f32(y, np.broadcast_to(g, y.shape), r))
+
+
+def int8_gemm_gated_residual_rows(xq, xs, wq, ws, gate, rows, resid):
+    """The gated residual with a gate row per token (the per-token modulation branch of _fused_block,
+    __init__.py:244-245, h3._mod_gate with _mod_row's bf16 rounding): r[m] = bf16(fma(y[m], gate[rows[m]], r[m]))."""
+    y = bf16_to_f32(int8_gemm(xq, xs, wq, ws))
+    g = bf16_to_f32(gate)[np.asarray(rows)]
+    r = bf16_to_f32(resid)
+    return f32_to_bf16(fma_f32(y, g, r))
 
 
 def fp8_gemm(xq, xs, wq, ws, bias=None):

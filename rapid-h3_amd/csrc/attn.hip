@@ -18,6 +18,7 @@
 //   K and Vt tiles (8 + 16 KiB per step) go through a 4-slot LDS ring with XOR-swizzled 16-byte chunks.
 //   With one workgroup per CU the grid runs in rounds; a last round at most half full runs as two key
 //   halves per workgroup (fp32 partials), merged by attn_combine_kernel.
+#include <cstdlib>
 #include <mutex>
 #include <type_traits>
 
@@ -514,12 +515,10 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(const float* __restri
     r[4 * i + 2] = (x.z * a0 + y.z * a1) * il;
     r[4 * i + 3] = (x.w * a0 + y.w * a1) * il;
   }
-  uint4 w;
-  w.x = pk_bf16(r[0], r[1]);
-  w.y = pk_bf16(r[2], r[3]);
-  w.z = pk_bf16(r[4], r[5]);
-  w.w = pk_bf16(r[6], r[7]);
-  *reinterpret_cast<uint4*>(out + q * o_ss + static_cast<int64_t>(h) * o_sh + 8 * c) = w;
+  // two 8-byte stores, the alignment the entry points require of out (its strides are multiples of 4 elements)
+  uint16_t* op = out + q * o_ss + static_cast<int64_t>(h) * o_sh + 8 * c;
+  *reinterpret_cast<uint2*>(op) = make_uint2(pk_bf16(r[0], r[1]), pk_bf16(r[2], r[3]));
+  *reinterpret_cast<uint2*>(op + 4) = make_uint2(pk_bf16(r[4], r[5]), pk_bf16(r[6], r[7]));
 }
 
 // ------------------------------------------------------------------ host
@@ -575,7 +574,13 @@ int forward(const Work& w, int64_t Sq, int64_t Sk, int64_t H, float scale, uint1
   const int cus = device_cus();
   const int64_t last = cus > 0 ? nwg % cus : 0;
   const int64_t nsteps = (Sk + STEP - 1) / STEP;
-  const int npair = w.tail && nwg > cus && last > 0 && 2 * last <= cus && last <= attn_ws::TAIL_MAX && nsteps >= 8
+  // The split changes how a split workgroup's keys are summed (two fp32 halves merged), so a head's output can
+  // differ in the last bits with the grid (H, Sq, the CU count). RH3_ATTN_SPLIT=0 turns it off for callers that
+  // need the same bits on every grid.
+  const char* env = getenv("RH3_ATTN_SPLIT");
+  const bool split_ok = !(env && env[0] == '0');
+  const int npair = split_ok && w.tail && nwg > cus && last > 0 && 2 * last <= cus && last <= attn_ws::TAIL_MAX &&
+                            nsteps >= 8
                         ? static_cast<int>(last) : 0;
   const int nmain = static_cast<int>(nwg - npair);
   const FwdArgs f{w.q8, w.qs, w.k8, w.ks, w.kn, w.vt, out, o_ss, o_sh, Sq, Sk, pad(Sq), pad(Sk),
@@ -728,6 +733,12 @@ extern "C" int rh3_attention_forward(int64_t Sq, int64_t Sk, int64_t H, float sc
                                      int64_t o_sh, void* workspace, int64_t workspace_bytes, hipStream_t stream) {
   clear_error();
   RH3_REQUIRE(Sq > 0 && Sk > 0 && H > 0, "attention_forward: sizes must be positive");
+  // the limits check_qkv applies to the pre-pass that filled the workspace (the main kernel's K-scale table
+  // holds pad(Sk)/128 <= 4096 entries)
+  RH3_REQUIRE(pad(Sq) / BLK < 65536 && H < 65536, "attention_forward: Sq=%lld exceeds the 8,388,480-token grid limit",
+              (long long)Sq);
+  RH3_REQUIRE(pad(Sk) / BLK <= 4096, "attention_forward: Sk=%lld exceeds the 524288-key limit of the attention kernel",
+              (long long)Sk);
   RH3_REQUIRE(out && (reinterpret_cast<uintptr_t>(out) & 7) == 0 && o_ss % 4 == 0 && o_sh % 4 == 0,
               "attention_forward: out must be 8-byte aligned with strides multiple of 4");
   const Work w = layout(workspace, Sq, Sk, H);

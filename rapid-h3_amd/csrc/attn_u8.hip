@@ -361,9 +361,6 @@ struct U8Args {
 };
 
 constexpr int U8_WAVES = 8, U8_NT = U8_WAVES * 64, U8_BQ = U8_WAVES * 32;
-#ifndef U8_LAG_MASK
-#define U8_LAG_MASK 2  // bit i set: waves 4i..4i+3 (one per SIMD) run half a tile behind
-#endif
 
 typedef __attribute__((address_space(3))) const v4i lds_v4i_u8;
 typedef __attribute__((address_space(3))) const float lds_f32_u8;
@@ -688,7 +685,7 @@ __global__ void __launch_bounds__(U8_NT, 1) attn_u8_kernel(const U8Args a) {
   // wave issues its copies of tile j+2 right after B_(j-1), into slot (j+2) % 4, whose last reader
   // (softmax_pv(j-2) of a lagging wave) ran before B_(j-1); before B_j it waits for its copies of tile j+1
   // (vmcnt(n) leaves the n issued after B_(j-1) in flight), so slot j+1 is complete past B_j.
-  const bool lag = (U8_LAG_MASK >> (wave >> 2)) & 1;
+  const bool lag = (wave >> 2) == 1;  // waves 4-7 (one per SIMD) run half a tile behind
   auto barrier = [&]() __attribute__((always_inline)) {
     if (side_wave) asm volatile("s_waitcnt vmcnt(5)" ::: "memory");
     else asm volatile("s_waitcnt vmcnt(4)" ::: "memory");

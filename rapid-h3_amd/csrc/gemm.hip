@@ -5,6 +5,7 @@
 //   EPI_PLAIN   out = bf16(y [+ bias[n]])
 //   EPI_SWIGLU  g, u = bf16(y) over the swiglu_perm interleave; h = bf16((g * sigmoid(g)) * u) at n / 2
 //   EPI_GATED   resid = bf16(fma(bf16(y), gate[n], resid))     (in place)
+//   EPI_GATED_ROWS  the same with gate[gidx[m]][n], a gate table row per output row (per-token modulation)
 //   EPI_ACC     raw int32 accumulators (verification)
 //   EPI_QKV     the qkv projection with the attention pre-pass partly fused (the reference's config 3xx,
 //               fp8_rowwise.cu:108-272): the 256x256 tile (two heads of q, k or v, 256 tokens = one statistics
@@ -37,22 +38,19 @@ typedef int v8i __attribute__((ext_vector_type(8)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 
-enum Epi { EPI_PLAIN = 0, EPI_SWIGLU = 1, EPI_GATED = 2, EPI_ACC = 3, EPI_QKV = 4 };
+enum Epi { EPI_PLAIN = 0, EPI_SWIGLU = 1, EPI_GATED = 2, EPI_ACC = 3, EPI_QKV = 4, EPI_GATED_ROWS = 5 };
 
 constexpr int BM = 256, BN = 256, BK = 64;
-// NW waves in a 2 (m) x NW/2 (n) grid, 128 x (512 / NW) outputs per wave. NW = 8: 2 waves per SIMD hide
-// each other's LDS and barrier latency. NW = 4: one wave per SIMD with 128 x 128 outputs (accumulators in
-// AGPRs), which reads 8 fragments per 16 MFMAs instead of 6 per 8 and so takes a third less LDS bandwidth
-// per MFMA.
+// NW waves in a 2 (m) x NW/2 (n) grid, 128 x (512 / NW) outputs per wave. The library builds NW = 8 (GEMM_NW):
+// 2 waves per SIMD hide each other's LDS and barrier latency. (One wave per SIMD with 128 x 128 outputs, NW = 4,
+// reads a third less LDS per MFMA but measured slower; its branches below are not instantiated.)
+constexpr int GEMM_NW = 8;
 template <int NW>
 struct Cfg {
   static constexpr int NT = NW * 64, WM = 128, WN = BN / (NW / 2), TI = WN / 32, TJ = WM / 32;
   static constexpr int LOADS = 2 * (BM * BK / 16) / NT;  // global->LDS loads per wave per k-step (both operands)
 };
-#ifndef RH3_GEMM_GROUP_M
-#define RH3_GEMM_GROUP_M 4
-#endif
-constexpr int GROUP_M = RH3_GEMM_GROUP_M;
+constexpr int GROUP_M = 4;
 constexpr int TILE_BYTES = BM * BK;  // per operand per stage (BM == BN)
 
 // EPI_QKV operands (pointers into the attention workspace of the chosen numerics)
@@ -83,6 +81,8 @@ struct GemmArgs {
   int64_t M, N, K;
   int tiles_m, tiles_n;
   QkvPrep qp;
+  const int32_t* gidx;  // EPI_GATED_ROWS: gate table row of each output row (the gate is [R, ldg] bf16)
+  int64_t ldg;
 };
 
 // 16-byte chunk c (0..3) of LDS row r: rows r, r+1 share a 128-byte line; the XOR keeps 16
@@ -136,22 +136,16 @@ struct Mma<true> {  // e4m3: 1 MFMA of k = 64 per step, 32-byte fragments (two 1
   __device__ static float val(const acc_t& c, int r) { return c[r]; }
 };
 
-#ifndef RH3_GEMM_NW
-#define RH3_GEMM_NW 8
-#endif
-#ifndef RH3_GEMM_PERSIST
-#define RH3_GEMM_PERSIST 1  // 0: one workgroup per tile for every epilogue
-#endif
 
 template <bool FP8, int EPI, int NW>
-__global__ void __launch_bounds__(RH3_GEMM_NW * 64, RH3_GEMM_NW / 4) gemm_kernel(const GemmArgs a) {
-  static_assert(NW == RH3_GEMM_NW, "one wave count per build");
+__global__ void __launch_bounds__(GEMM_NW * 64, GEMM_NW / 4) gemm_kernel(const GemmArgs a) {
+  static_assert(NW == GEMM_NW, "the launch bounds are those of the built wave count");
   using MM = Mma<FP8>;
   using acc_t = typename MM::acc_t;
   constexpr int NT = Cfg<NW>::NT, WM = Cfg<NW>::WM, WN = Cfg<NW>::WN, TI = Cfg<NW>::TI, TJ = Cfg<NW>::TJ;
-  // loads per operand per wave per k-step (from the macro: an array sized by a template-dependent
+  // loads per operand per wave per k-step (from GEMM_NW, not NW: an array sized by a template-dependent
   // constant makes clang's host pass drop the kernel's launch stub)
-  constexpr int NL = (BM * BK / 16) / (RH3_GEMM_NW * 64);
+  constexpr int NL = (BM * BK / 16) / (GEMM_NW * 64);
   static_assert(NL == Cfg<NW>::LOADS / 2, "load count");
   // 4-stage ring, each stage its own LDS object {x tile, w tile} (2 x 16 KiB) named statically: the
   // asynchronous global->LDS loads into one stage then provably do not alias the reads of another
@@ -234,16 +228,10 @@ __global__ void __launch_bounds__(RH3_GEMM_NW * 64, RH3_GEMM_NW / 4) gemm_kernel
     for (int j = 0; j < TJ; ++j) fb[j] = MM::load(stg, wm * WM + j * 32 + l32, ks, g);
   };
   auto mma_all = [&](const typename MM::frag_t* fa, const typename MM::frag_t* fb) __attribute__((always_inline)) {
-#ifdef RH3_GEMM_SETPRIO
-    __builtin_amdgcn_s_setprio(1);
-#endif
 #pragma unroll
     for (int i = 0; i < TI; ++i)
 #pragma unroll
       for (int j = 0; j < TJ; ++j) acc[i][j] = MM::mma(fa[i], fb[j], acc[i][j]);
-#ifdef RH3_GEMM_SETPRIO
-    __builtin_amdgcn_s_setprio(0);
-#endif
   };
   // k-step kt, reading stage cur; loads step kt+3 into nxt3 (the stage of step kt-1, whose readers all
   // passed the previous step's barrier). int8 (two k = 32 halves): the fragments of half 0 were read at
@@ -584,6 +572,7 @@ __global__ void __launch_bounds__(RH3_GEMM_NW * 64, RH3_GEMM_NW / 4) gemm_kernel
     if constexpr (EPI == EPI_GATED) {
       if (nok) unpack8(*reinterpret_cast<const uint4*>(a.gate + n), gv);
     }
+    (void)gv;
 #pragma unroll 4
     for (int it = 0; it < WM / RPI; ++it) {
       const int row = it * RPI + lane / CPR;
@@ -592,9 +581,11 @@ __global__ void __launch_bounds__(RH3_GEMM_NW * 64, RH3_GEMM_NW / 4) gemm_kernel
       if (m >= a.M || !nok) continue;
       if constexpr (EPI == EPI_PLAIN) {
         *reinterpret_cast<uint4*>(static_cast<uint16_t*>(a.out) + m * a.ldo + n) = v;
-      } else if constexpr (EPI == EPI_GATED) {
+      } else if constexpr (EPI == EPI_GATED || EPI == EPI_GATED_ROWS) {
         uint16_t* rp = static_cast<uint16_t*>(a.out) + m * a.ldo + n;
         float yv[8], rv[8];
+        if constexpr (EPI == EPI_GATED_ROWS)
+          unpack8(*reinterpret_cast<const uint4*>(a.gate + static_cast<int64_t>(a.gidx[m]) * a.ldg + n), gv);
         unpack8(v, yv);
         unpack8(*reinterpret_cast<const uint4*>(rp), rv);
         uint4 o;
@@ -833,7 +824,7 @@ __global__ void __launch_bounds__(512, 2) gemm_persistent_kernel(const GemmArgs 
         // the residual segments of this row block (gated): issued before the staging so their latency
         // runs under it
         uint4 rres[TI][2];
-        if constexpr (EPI == EPI_GATED) {
+        if constexpr (EPI == EPI_GATED || EPI == EPI_GATED_ROWS) {
 #pragma unroll
           for (int i = 0; i < TI; ++i)
 #pragma unroll
@@ -878,9 +869,17 @@ __global__ void __launch_bounds__(512, 2) gemm_persistent_kernel(const GemmArgs 
             if (m < a.M && n < a.N) {
               if constexpr (EPI == EPI_PLAIN) {
                 *reinterpret_cast<uint4*>(static_cast<uint16_t*>(a.out) + m * a.ldo + n) = v;
-              } else if constexpr (EPI == EPI_GATED) {
-                const float4 g0 = *reinterpret_cast<const float4*>(bg_s + (n - n0));
-                const float4 g1 = *reinterpret_cast<const float4*>(bg_s + (n - n0) + 4);
+              } else if constexpr (EPI == EPI_GATED || EPI == EPI_GATED_ROWS) {
+                float4 g0, g1;
+                if constexpr (EPI == EPI_GATED) {
+                  g0 = *reinterpret_cast<const float4*>(bg_s + (n - n0));
+                  g1 = *reinterpret_cast<const float4*>(bg_s + (n - n0) + 4);
+                } else {  // this row's gate row, from global memory (per-token modulation)
+                  float gv[8];
+                  unpack8(*reinterpret_cast<const uint4*>(a.gate + static_cast<int64_t>(a.gidx[m]) * a.ldg + n), gv);
+                  g0 = make_float4(gv[0], gv[1], gv[2], gv[3]);
+                  g1 = make_float4(gv[4], gv[5], gv[6], gv[7]);
+                }
                 float yv[8], rv[8];
                 unpack8(v, yv);
                 unpack8(rres[i][it], rv);
@@ -919,18 +918,18 @@ int run(GemmArgs a, hipStream_t st, const char* name) {
   a.tiles_n = static_cast<int>((a.N + BN - 1) / BN);
   const int64_t nb = static_cast<int64_t>(a.tiles_m) * a.tiles_n;
   RH3_REQUIRE(nb < (1ll << 31), "%s: too many tiles", name);
-  if constexpr (EPI != EPI_QKV && RH3_GEMM_NW == 8) {
+  if constexpr (EPI != EPI_QKV) {
     const int64_t nk = a.K / BK;
     const int cus = device_cus();
     // the persistent kernel's 32-bit lane offsets reach 255 rows of either operand
     const bool off32 = 255 * a.ldx + 64 < (1ll << 32) && 255 * a.ldw + 64 < (1ll << 32);
-    if (RH3_GEMM_PERSIST && nk % 4 == 0 && nk >= 8 && cus > 0 && off32) {
+    if (nk % 4 == 0 && nk >= 8 && cus > 0 && off32) {
       const int64_t grid = nb < cus ? nb : cus;  // one workgroup per CU (the LDS use admits no second)
       hipLaunchKernelGGL((gemm_persistent_kernel<FP8, EPI>), dim3(static_cast<unsigned>(grid)), dim3(512), 0, st, a);
       return launch_status(name);
     }
   }
-  hipLaunchKernelGGL((gemm_kernel<FP8, EPI, RH3_GEMM_NW>), dim3(static_cast<unsigned>(nb)), dim3(RH3_GEMM_NW * 64), 0,
+  hipLaunchKernelGGL((gemm_kernel<FP8, EPI, GEMM_NW>), dim3(static_cast<unsigned>(nb)), dim3(GEMM_NW * 64), 0,
                      st, a);
   return launch_status(name);
 }
@@ -975,6 +974,22 @@ extern "C" int rh3_gemm_i8_swiglu(const int8_t* xq, int64_t ldx, const float* xs
   RH3_REQUIRE(M == 0 || N == 0 || (xs && ws_perm && aligned16(ws_perm)), "gemm_i8_swiglu: scales required");
   GemmArgs a{xq, ldx, wq_perm, ldw, xs, ws_perm, nullptr, nullptr, out, ldo, M, N, K, 0, 0};
   return run<false, EPI_SWIGLU>(a, stream, "gemm_i8_swiglu");
+}
+
+extern "C" int rh3_gemm_i8_gated_rows(const int8_t* xq, int64_t ldx, const float* xs, const int8_t* wq, int64_t ldw,
+                                      const float* ws, const uint16_t* gate, int64_t ldg, const int32_t* gidx,
+                                      uint16_t* resid, int64_t ldr, int64_t M, int64_t N, int64_t K,
+                                      hipStream_t stream) {
+  clear_error();
+  if (int e = check("gemm_i8_gated_rows", xq, ldx, wq, ldw, resid, ldr, M, N, K, N)) return e;
+  RH3_REQUIRE(M == 0 || N == 0 || (xs && ws && gate && gidx && aligned16(ws) && aligned16(gate)),
+              "gemm_i8_gated_rows: scales, gate table and row indices required (ws, gate 16-byte aligned)");
+  RH3_REQUIRE(ldg >= N && ldg % 8 == 0, "gemm_i8_gated_rows: gate row stride %lld invalid (need >= N, multiple of 8)",
+              (long long)ldg);
+  GemmArgs a{xq, ldx, wq, ldw, xs, ws, nullptr, gate, resid, ldr, M, N, K, 0, 0};
+  a.gidx = gidx;
+  a.ldg = ldg;
+  return run<false, EPI_GATED_ROWS>(a, stream, "gemm_i8_gated_rows");
 }
 
 extern "C" int rh3_gemm_i8_gated(const int8_t* xq, int64_t ldx, const float* xs, const int8_t* wq, int64_t ldw,

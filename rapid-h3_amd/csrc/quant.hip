@@ -208,9 +208,6 @@ __global__ void __launch_bounds__(256) quant_rows_kernel(const QuantArgs a) {
 // each wavefront then quantizes RPW rows from LDS; a row with another table index reads its values from
 // global memory. Same arithmetic and order as quant_rows_kernel<NCH, KIND_NORMMOD>.
 constexpr int NM_RPW = 8;
-#ifndef RH3_QUANT_SPLIT
-#define RH3_QUANT_SPLIT 1  // 0: rows wider than 4096 on quant_rows_kernel (one wavefront per row)
-#endif  // rows per wavefront
 template <int NCH, typename TabT>
 __global__ void __launch_bounds__(256) quant_normmod_lds_kernel(const QuantArgs a) {
   extern __shared__ float4 nm_lds[];   // [K/4] scale, [K/4] shift, [K/8] weight (bf16 x 8 per uint4)
@@ -447,7 +444,7 @@ __global__ void __launch_bounds__(256) quant_rows_split_kernel(const QuantArgs a
 template <int KIND, bool FP8, typename TabT>
 int launch(const QuantArgs& a, hipStream_t st, const char* name) {
   if (a.M == 0) return RH3_OK;
-  if (KIND == KIND_PLAIN && a.K > 4096 && a.K <= 16384 && a.M < (1ll << 31) && RH3_QUANT_SPLIT) {
+  if (KIND == KIND_PLAIN && a.K > 4096 && a.K <= 16384 && a.M < (1ll << 31)) {
     const dim3 grid(static_cast<unsigned>(a.M)), block(256);
     if (a.K <= 8192) hipLaunchKernelGGL((quant_rows_split_kernel<4, FP8>), grid, block, 0, st, a);
     else hipLaunchKernelGGL((quant_rows_split_kernel<8, FP8>), grid, block, 0, st, a);
@@ -654,4 +651,103 @@ extern "C" int rh3_fake_nvfp4(const void* x, int x_dtype, int64_t ldx, int64_t M
                        out, ldo, am);
   }
   return launch_status("fake_nvfp4");
+}
+
+// ---------------------------------------------------------------- quantizer of any float input
+// Inputs the fused quantizers do not take: fp16 / fp32 rows and FP8 with one scale per tensor. The reference's
+// torch path (kernels.py:57-82, :125-128) casts with .float(), takes the absmax, s = max(amax / QMAX, 1e-12) and
+// q = round(x / s) clamped (int8) or e4m3(clamp(x / s)) (FP8), with the IEEE quotient. One workgroup per row;
+// per-element code (these are load-time or verification paths, not the per-step quantizers).
+namespace rh3 {
+namespace {
+
+template <int DT>
+__device__ __forceinline__ float ld_any(const void* p, int64_t i) {
+  if constexpr (DT == RH3_DTYPE_F32) return static_cast<const float*>(p)[i];
+  else if constexpr (DT == RH3_DTYPE_F16) return static_cast<float>(static_cast<const _Float16*>(p)[i]);
+  else return bf2f(static_cast<const uint16_t*>(p)[i]);
+}
+
+template <int DT>
+__global__ void __launch_bounds__(256) absmax_any_kernel(const void* __restrict__ x, int64_t ldx, int64_t M, int64_t K,
+                                                         unsigned int* __restrict__ amax) {
+  __shared__ float red[4];
+  float m = 0.0f;
+  const int64_t n = M * K;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n; i += static_cast<int64_t>(gridDim.x) * 256)
+    m = fmaxf(m, fabsf(ld_any<DT>(x, (i / K) * ldx + i % K)));
+  m = wave_max(m);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) atomicMax(amax, __float_as_uint(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]))));
+}
+
+// MODE 0: int8 per row; 1: FP8 per row; 2: FP8 per tensor (amax from absmax_any_kernel)
+template <int DT, int MODE>
+__global__ void __launch_bounds__(256) quant_any_kernel(const void* __restrict__ x, int64_t ldx, int64_t K,
+                                                        uint8_t* __restrict__ q, int64_t ldq, float* __restrict__ s,
+                                                        const unsigned int* __restrict__ amax_t) {
+  __shared__ float red[4];
+  const int64_t r = blockIdx.x;
+  const int tid = threadIdx.x;
+  float amax;
+  if constexpr (MODE == 2) {
+    amax = __uint_as_float(*amax_t);
+  } else {
+    float m = 0.0f;
+    for (int64_t k = tid; k < K; k += 256) m = fmaxf(m, fabsf(ld_any<DT>(x, r * ldx + k)));
+    m = wave_max(m);
+    if ((tid & 63) == 0) red[tid >> 6] = m;
+    __syncthreads();
+    amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  }
+  const float sc = fmaxf(amax / (MODE == 0 ? 127.0f : 448.0f), 1e-12f);
+  if (tid == 0 && (MODE != 2 || r == 0)) s[MODE == 2 ? 0 : r] = sc;
+  for (int64_t k = tid; k < K; k += 256) {
+    const float t = ld_any<DT>(x, r * ldx + k) / sc;
+    q[r * ldq + k] = MODE == 0 ? static_cast<uint8_t>(static_cast<int8_t>(fminf(fmaxf(rintf(t), -127.0f), 127.0f)))
+                               : static_cast<uint8_t>(fp8_e4m3(fminf(fmaxf(t, -448.0f), 448.0f)));
+  }
+}
+
+template <int DT>
+int launch_any(const void* x, int64_t ldx, int64_t M, int64_t K, int mode, void* q, int64_t ldq, float* s,
+               float* amax_ws, hipStream_t st) {
+  uint8_t* qb = static_cast<uint8_t*>(q);
+  if (mode == 0) {
+    hipLaunchKernelGGL((quant_any_kernel<DT, 0>), dim3(static_cast<unsigned>(M)), dim3(256), 0, st, x, ldx, K, qb, ldq, s,
+                       nullptr);
+  } else if (mode == 1) {
+    hipLaunchKernelGGL((quant_any_kernel<DT, 1>), dim3(static_cast<unsigned>(M)), dim3(256), 0, st, x, ldx, K, qb, ldq, s,
+                       nullptr);
+  } else {
+    unsigned int* am = reinterpret_cast<unsigned int*>(amax_ws);
+    hipLaunchKernelGGL(fill_zero_kernel, dim3(1), dim3(1), 0, st, am);
+    const unsigned grid = static_cast<unsigned>(std::min<int64_t>((M * K + 255) / 256, 4096));
+    hipLaunchKernelGGL(absmax_any_kernel<DT>, dim3(grid), dim3(256), 0, st, x, ldx, M, K, am);
+    hipLaunchKernelGGL((quant_any_kernel<DT, 2>), dim3(static_cast<unsigned>(M)), dim3(256), 0, st, x, ldx, K, qb, ldq, s,
+                       am);
+  }
+  return launch_status("quant_any");
+}
+
+}  // namespace
+}  // namespace rh3
+
+extern "C" int rh3_quant_any(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t K, int mode, void* q,
+                             int64_t ldq, float* s, float* amax_ws, hipStream_t stream) {
+  using namespace rh3;
+  clear_error();
+  RH3_REQUIRE(M >= 0 && K >= 0 && M < (1ll << 31), "quant_any: bad sizes M=%lld K=%lld", (long long)M, (long long)K);
+  RH3_REQUIRE(mode >= 0 && mode <= 2, "quant_any: mode %d (0 int8 rows, 1 fp8 rows, 2 fp8 tensor)", mode);
+  if (M == 0 || K == 0) return RH3_OK;
+  RH3_REQUIRE(x && q && s && (mode != 2 || amax_ws), "quant_any: null pointer");
+  RH3_REQUIRE(ldx >= K && ldq >= K, "quant_any: row strides (%lld, %lld) must be >= K=%lld", (long long)ldx,
+              (long long)ldq, (long long)K);
+  switch (x_dtype) {
+    case RH3_DTYPE_BF16: return launch_any<RH3_DTYPE_BF16>(x, ldx, M, K, mode, q, ldq, s, amax_ws, stream);
+    case RH3_DTYPE_F32: return launch_any<RH3_DTYPE_F32>(x, ldx, M, K, mode, q, ldq, s, amax_ws, stream);
+    case RH3_DTYPE_F16: return launch_any<RH3_DTYPE_F16>(x, ldx, M, K, mode, q, ldq, s, amax_ws, stream);
+    default: RH3_REQUIRE(false, "quant_any: x_dtype %d (1 bf16, 2 fp32, 3 fp16)", x_dtype);
+  }
 }

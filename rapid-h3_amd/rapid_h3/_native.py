@@ -30,11 +30,13 @@ SIGNATURES = {
     "rh3_norm_mod_rot_quant_i8": ([_P, _I, _I, _I, _P, _F, _P, _P, _P, _C, _I, _P, _I, _P, _P], _C),
     "rh3_rot_quant_heads_i8": ([_P, _I, _I, _I, _I, _P, _I, _P, _P], _C),
     "rh3_convrot_f32": ([_P, _C, _I, _I, _I, _P, _I, _P], _C),
+    "rh3_quant_any": ([_P, _C, _I, _I, _I, _C, _P, _I, _P, _P, _P], _C),
     "rh3_quant_weight_rot_i8": ([_P, _C, _I, _I, _I, _P, _I, _P, _P], _C),
     "rh3_fake_nvfp4": ([_P, _C, _I, _I, _I, _P, _I, _P, _P], _C),
     "rh3_gemm_i8": ([_P, _I, _P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _P], _C),
     "rh3_gemm_i8_swiglu": ([_P, _I, _P, _P, _I, _P, _P, _I, _I, _I, _I, _P], _C),
     "rh3_gemm_i8_gated": ([_P, _I, _P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _P], _C),
+    "rh3_gemm_i8_gated_rows": ([_P, _I, _P, _P, _I, _P, _P, _I, _P, _P, _I, _I, _I, _I, _P], _C),
     "rh3_gemm_i8_acc": ([_P, _I, _P, _I, _P, _I, _I, _I, _I, _P], _C),
     "rh3_gemm_i8_qkv": ([_P, _I, _P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _P, _C, _P, _P, _F, _C, _C, _P, _I, _P], _C),
     "rh3_gemm_fp8": ([_P, _I, _P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _P], _C),
@@ -71,6 +73,7 @@ SIGNATURES = {
 
 RH3_DTYPE_BF16 = 1
 RH3_DTYPE_F32 = 2
+RH3_DTYPE_F16 = 3
 
 _lib = None
 

@@ -60,11 +60,15 @@ def row_index(segments, s, device):
 
 def gemm_gated(xq, xs, qw, x, gate, segments):
     """x += gate[row] * (xq @ W^T) per modality segment, in the GEMM epilogue (__init__.py:242-251).
-    gate: [R, N] table (bf16 or fp32); each segment's row is rounded to bf16 like _mod_row."""
+    gate: [R, N] table (bf16 or fp32), rounded to bf16 like _mod_row. A segment's row is an int (one gate row for
+    the segment) or a tensor of per-token rows (the reference's _mod_gate branch, __init__.py:244-245), which runs
+    the per-row gate epilogue."""
+    gate2 = gate.reshape(-1, gate.shape[-1])
     for a, b, row in segments:
         if torch.is_tensor(row):
-            raise NotImplementedError("per-token gate rows: the reference falls back to _mod_gate here")
-        g = gate[int(row)].to(torch.bfloat16).reshape(-1).contiguous()
+            _gemm.int8_gemm_gated_residual_rows(xq[a:b], xs[a:b], qw.q, qw.scale, gate2, row, x[a:b])
+            continue
+        g = gate2[int(row)].to(torch.bfloat16).reshape(-1).contiguous()
         _gemm.int8_gemm_gated_residual(xq[a:b], xs[a:b], qw.q, qw.scale, g, x[a:b])
     return x
 
@@ -170,3 +174,20 @@ def fused_block(x, w: BlockWeights, mod, segments, rope_tab, idx=None, mark=None
     x = gemm_gated(hq, hs, w.fc2, x, gate_mlp, segments)
     tick("gemm_down_gated")
     return x
+
+
+def fused_mlp(x, fc1, fc2, recipe="int8_rot", trace=None):
+    """The reference's _fused_mlp (__init__.py:170-183) for a block whose attention linears are not all quantized:
+    h = fc1(x) ([.., 2F] bf16, gate | up), then the SwiGLU-prologue quantizer (silu(gate) * up, rotated for int8_rot)
+    straight into the fc2 GEMM, so silu(gate) * up is never written in bf16. fc1: a QuantLinear or any callable;
+    fc2: a QuantLinear (its cached QWeight) or a QWeight. Like the reference, fc2's bias is not applied here.
+    trace: optional dict that receives the intermediates h, hq, hs."""
+    hdn = fc1(x)
+    shape = hdn.shape
+    q = _quant.swiglu_rot_quant_rows_i8 if recipe == "int8_rot" else _quant.swiglu_quant_rows_i8
+    xq, xs = q(hdn.reshape(-1, shape[-1]).contiguous())
+    if trace is not None:
+        trace.update(h=hdn, hq=xq, hs=xs)
+    qw = fc2.qweight_for() if hasattr(fc2, "qweight_for") else fc2
+    y = _gemm.int8_gemm(xq, xs, qw.q, qw.scale)
+    return y.reshape(*shape[:-1], y.shape[-1])

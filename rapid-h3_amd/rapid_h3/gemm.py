@@ -85,6 +85,26 @@ def int8_gemm_gated_residual(xq, xs, wq, ws, gate, resid, config=6):
     return resid
 
 
+def int8_gemm_gated_residual_rows(xq, xs, wq, ws, gate, rows, resid):
+    """resid[m, :] += bf16(xq @ wq^T * xs * ws)[m, :] * gate[rows[m], :], in place: the gated residual with one gate
+    table row per token (per-token modulation, _fused_block's tensor-row segments, __init__.py:242-245). gate [R, N]
+    (rounded to bf16 like _mod_row), rows [M] integer indices into it."""
+    _check(xq, wq, torch.int8, "int8_gemm_gated_residual_rows")
+    m, k = xq.shape
+    n = wq.shape[0]
+    if resid.shape != (m, n) or resid.dtype != torch.bfloat16 or resid.stride(1) != 1:
+        raise RuntimeError("int8_gemm_gated_residual_rows: resid must be bf16 [M, N] with unit column stride")
+    xs, ws = _vec(xs, m, "gated xs"), _vec(ws, n, "gated ws")
+    gate = gate.to(torch.bfloat16).reshape(-1, n).contiguous()
+    rows = rows.reshape(-1).to(device=xq.device, dtype=torch.int32).contiguous()
+    if rows.numel() != m:
+        raise RuntimeError("int8_gemm_gated_residual_rows: one gate row index per token required")
+    nat.call("rh3_gemm_i8_gated_rows", nat.ptr(xq), xq.stride(0), nat.ptr(xs), nat.ptr(wq), wq.stride(0),
+             nat.ptr(ws), nat.ptr(gate), gate.stride(0), nat.ptr(rows), nat.ptr(resid), resid.stride(0), m, n, k,
+             nat.stream(xq.device))
+    return resid
+
+
 def swiglu_perm(n2, device):
     """Row order for an fc1 weight [gate (F rows) | up (F rows)] so each 8-row group is
     [gate 4j..4j+3 | up 4j..4j+3] (cutlass_fp8.swiglu_perm, cutlass_fp8.py:55-62)."""

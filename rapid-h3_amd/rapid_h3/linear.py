@@ -2,9 +2,10 @@
 without ComfyUI: a replacement forward for one Linear that runs kernels.linear on librh3's kernels.
 
 What it keeps from the reference:
-  * the quantized weight is made once and cached; it is remade when the weight changes (the reference
-    keys its cache by ComfyUI's patches_uuid, :123-135; here the key is the weight tensor's identity,
-    storage pointer and version counter, which change when the weight is replaced or updated in place);
+  * the quantized weight is made once and cached; it is remade when the weight changes. The reference keys
+    its cache by ComfyUI's patches_uuid (:123-135): a caller that has such an id passes patch_id (a callable
+    returning it), and the key is (patch_id(), device); without one the key is the weight tensor's identity,
+    storage pointer and version counter, which change when the weight is replaced or updated in place;
   * an already-quantized Comfy int8_convrot weight (int8 [N, K] codes rotated with group 256 plus a
     per-row scale) is adopted as is in int8_rot mode (:107-114), see from_quantized;
   * the bias is added in x.dtype after the GEMM (:158-159);
@@ -12,7 +13,7 @@ What it keeps from the reference:
   * measure_every = n > 0 records the relative L2 error against F.linear every n calls into
     stats[name] (:139-165).
 What it does not keep: ComfyUI's cast context for off-GPU / LoRA weights, and the F.linear path for CPU
-or non-16-bit inputs (:147-148), which here raise: no CPU path.
+or fp32 inputs (:147-148), which here raise: no CPU path. fp16 activations take kernels.linear's path for them.
 """
 import torch
 
@@ -20,10 +21,11 @@ from . import kernels
 
 
 class QuantLinear:
-    def __init__(self, weight, bias=None, mode="int8_rot", name="linear", measure_every=0, stats=None):
+    def __init__(self, weight, bias=None, mode="int8_rot", name="linear", measure_every=0, stats=None, patch_id=None):
         if mode not in kernels.MODES or mode == "bf16":
             raise ValueError(f"QuantLinear: mode {mode!r} (one of {kernels.MODES[1:]})")
         self.weight, self.bias, self.mode, self.name = weight, bias, mode, name
+        self.patch_id = patch_id
         self.measure_every = int(measure_every)
         self.stats = {} if stats is None else stats
         self.qweight, self.cache_key, self.calls = None, None, 0
@@ -39,6 +41,8 @@ class QuantLinear:
 
     def _key(self):
         w = self.weight
+        if self.patch_id is not None:
+            return ("patch", self.patch_id(), str(w.device))
         return (id(w), w.data_ptr(), w._version, str(w.device))
 
     def qweight_for(self):
@@ -52,8 +56,8 @@ class QuantLinear:
         return self.qweight
 
     def __call__(self, x):
-        if not x.is_cuda or x.dtype != torch.bfloat16:
-            raise TypeError(f"QuantLinear {self.name}: bf16 GPU activations only (no CPU path), got {x.dtype} "
+        if not x.is_cuda or x.dtype not in (torch.bfloat16, torch.float16):
+            raise TypeError(f"QuantLinear {self.name}: bf16 / fp16 GPU activations only (no CPU path), got {x.dtype} "
                             f"on {x.device}")
         qw = self.qweight_for()
         shape = x.shape

@@ -180,6 +180,27 @@ def _dtype_code(t, name):
     raise TypeError(f"{name}: bf16 or fp32 input, got {t.dtype}")
 
 
+def quant_any(x, mode):
+    """Quantization of a 2-D GPU tensor of any float dtype (bf16, fp16, fp32) on rh3_quant_any, the reference's torch
+    path semantics (kernels.py:57-82, :125-128): mode "int8" / "fp8" one scale per row -> (q, s [M, 1] fp32);
+    "fp8_tensor" one scale for the tensor -> (q, s [] fp32). IEEE quotient; codes int8 or float8_e4m3fn."""
+    if x.ndim != 2 or not x.is_cuda:
+        raise AssertionError("quant_any: x must be a 2-D GPU tensor (no CPU path)")
+    codes = {torch.bfloat16: nat.RH3_DTYPE_BF16, torch.float32: nat.RH3_DTYPE_F32, torch.float16: nat.RH3_DTYPE_F16}
+    if x.dtype not in codes:
+        raise TypeError(f"quant_any: float input (bf16, fp16, fp32), got {x.dtype}")
+    if x.stride(1) != 1:
+        x = x.contiguous()
+    m, k = x.shape
+    mo = {"int8": 0, "fp8": 1, "fp8_tensor": 2}[mode]
+    q = torch.empty((m, k), device=x.device, dtype=torch.int8 if mo == 0 else torch.uint8)
+    s = torch.empty((1, 1) if mo == 2 else (m, 1), device=x.device, dtype=torch.float32)
+    amax = torch.empty(1, device=x.device, dtype=torch.float32) if mo == 2 else None
+    nat.call("rh3_quant_any", nat.ptr(x), codes[x.dtype], x.stride(0), m, k, mo, nat.ptr(q), q.stride(0), nat.ptr(s),
+             nat.ptr(amax), nat.stream(x.device))
+    return (q if mo == 0 else q.view(FP8)), (s.reshape(()) if mo == 2 else s)
+
+
 def convrot_f32(x):
     """x [M, K] (bf16 or fp32, GPU) @ blockdiag(H256)^T as fp32, the exact product rounded once."""
     if x.ndim != 2 or x.stride(1) != 1 or not x.is_cuda:

@@ -43,6 +43,8 @@ def test_argument_validation_without_gpu():
     st = lib.rh3_int8_attention(fake, 128, 128, fake, 128, 128, fake, 128, 128, 10, 10, 1, 0.1, 1, fake, 128, 128,
                                 fake, 16, None)
     assert st == 1 and "workspace" in nat.last_error()
+    st = lib.rh3_attention_forward(10, (1 << 19) + 1, 1, 0.1, fake, 128, 128, fake, 1 << 40, None)
+    assert st == 1 and "524288-key limit" in nat.last_error()
     st = lib.rh3_int8_attention_noalloc(fake, 128, 128, fake, 128, 128, fake, 128, 128, 1 << 19, 1 << 19, 1, 0.1, 1,
                                         fake, 128, 128, None)
     assert st == 1 and "beyond its" in nat.last_error()
@@ -116,11 +118,15 @@ def test_dropin_modules_keep_reference_names():
                                     "attention_rr_bias"])):
         for n in names:
             assert hasattr(mod, n), f"{mod.__name__}.{n}"
+    for n in ("int8_attention", "int8_attention_rr", "int8_attention_rr_bias", "int8_prepass", "int8_attention_pre",
+              "int8_prepass_pre"):
+        assert callable(getattr(attn_int8.ext(), n)), n
+    assert attn_int8.CONFIG == int(os.environ.get("RAPIDH3_ATTN_CONFIG", "0"))   # the reference's default 0
     import torch
     p = cutlass_fp8.swiglu_perm(16, "cpu")
     assert p.tolist() == [0, 1, 2, 3, 8, 9, 10, 11, 4, 5, 6, 7, 12, 13, 14, 15]
-    with pytest.raises(ValueError):
-        kernels.quantize_rows(torch.zeros(2, 8, dtype=torch.bfloat16), "bogus")
+    with pytest.raises(RuntimeError, match="GPU"):             # no CPU path
+        kernels.quantize_rows(torch.zeros(2, 8, dtype=torch.bfloat16), "int8_rowwise")
 
 
 def test_override_host_logic():

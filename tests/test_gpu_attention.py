@@ -109,13 +109,14 @@ def test_attention_strided_out(dev):
     assert rel_l2(got, ref) < TOL
 
 
-@pytest.mark.parametrize("sk,head_major", [(2600, False), (1100, True)])
+@pytest.mark.parametrize("sk,head_major", [(2600, False), (1100, True), (2600, "padded")])
 def test_attention_split_tail(dev, sk, head_major):
     """A grid whose last round (one workgroup of 384 queries per CU) is at most half full: those workgroups
     run as two key halves, each writing fp32 partials, merged by attn_combine_kernel. H is chosen from the
     device's CU count so that 7 query blocks x H heads leave 16..cus/2 workgroups in the last round; the
     heads holding them and head 0 (unsplit) against the oracle. Self-attention with [S, H, D] output, and
-    cross-attention (1,100 keys: 18 steps, the last ragged) into a head-major [1, H, S, D] buffer."""
+    cross-attention (1,100 keys: 18 steps, the last ragged) into a head-major [1, H, S, D] buffer, and an output
+    view whose head stride is 4 mod 8 elements (132: the merge kernel's stores must not assume 16-byte alignment)."""
     import torch
     from rapid_h3 import attention
     cus = torch.cuda.get_device_properties(0).multi_processor_count
@@ -127,7 +128,11 @@ def test_attention_split_tail(dev, sk, head_major):
     q = _bf(rng.standard_normal((s, h, 128)))
     k = _bf(rng.standard_normal((sk, h, 128)) + 2.0 * rng.standard_normal((1, h, 128)))
     v = _bf(rng.standard_normal((sk, h, 128)))
-    if head_major:
+    if head_major == "padded":
+        o = torch.empty(s, h, 132, dtype=torch.bfloat16, device=dev)
+        attention.attention(to_dev(q, dev), to_dev(k, dev), to_dev(v, dev), out=o[:, :, :128])
+        out = bf16_to_f32(to_np(o[:, :, :128]))
+    elif head_major:
         o = torch.empty(1, h, s, 128, dtype=torch.bfloat16, device=dev)
         attention.attention(to_dev(q, dev), to_dev(k, dev), to_dev(v, dev), out=o[0].transpose(0, 1))
         out = bf16_to_f32(to_np(o[0].transpose(0, 1)))
@@ -143,6 +148,31 @@ def test_attention_split_tail(dev, sk, head_major):
             if i // nqb == hh:
                 r0, r1 = (i % nqb) * 384, min((i % nqb + 1) * 384, s)
                 assert rel_l2(out[r0:r1, hh], ref[r0:r1]) < TOL, (hh, i % nqb)
+
+
+def test_attention_split_switch(dev, monkeypatch):
+    """RH3_ATTN_SPLIT=0 runs the last round whole: the same grid as test_attention_split_tail with and without the
+    split gives outputs within the tolerance of each other (the split sums each key half in fp32 and merges, so the
+    bits may differ), and the unsplit output also against the oracle."""
+    import torch
+    from rapid_h3 import attention
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    s, nqb = 2600, 7
+    h = next(hh for hh in range(1, 100000) if nqb * hh > cus and 16 <= (nqb * hh) % cus <= min(cus // 2, 128))
+    rng = np.random.default_rng(77)
+    q = _bf(rng.standard_normal((s, h, 128)))
+    k = _bf(rng.standard_normal((s, h, 128)) + 2.0 * rng.standard_normal((1, h, 128)))
+    v = _bf(rng.standard_normal((s, h, 128)))
+    args = (to_dev(q, dev), to_dev(k, dev), to_dev(v, dev))
+    split = bf16_to_f32(to_np(attention.attention(*args)))
+    monkeypatch.setenv("RH3_ATTN_SPLIT", "0")
+    whole = bf16_to_f32(to_np(attention.attention(*args)))
+    monkeypatch.delenv("RH3_ATTN_SPLIT")
+    assert rel_l2(split, whole) < TOL
+    hh = h - 1                                               # the last head holds split workgroups
+    q8, qs, k8, ks, _ = oa.prepass(q[:, hh:hh + 1], k[:, hh:hh + 1])
+    ref = oa.attention_from_codes(q8, qs, k8, ks, v[:, hh:hh + 1], 128 ** -0.5)[:s, 0]
+    assert rel_l2(whole[:, hh], ref) < TOL
 
 
 def test_attention_full_size_sampled(dev):

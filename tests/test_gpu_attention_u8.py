@@ -61,6 +61,36 @@ def test_u8_prepass_golden(dev, golden):
     assert np.array_equal(to_np(pc["q8"]), g["q8"]) and np.array_equal(to_np(pc["qs"]), g["qs"])
 
 
+def test_ext_int8_prepass_golden(dev, golden):
+    """attn_int8.ext().int8_prepass, the reference extension's verification entry (attn_int8.cu:2692-2704, called
+    by _rr_check, __init__.py:342-343): the operand list [q8, qs, k8, ks, ksb, vt, vscale, vmean] bit-exact against
+    the oracle, with and without the fused RMSNorm + RoPE; the default config 0 of attn_int8.attention runs the
+    same production numerics."""
+    from rapid_h3 import attn_int8
+    g = golden("attention_u8")
+    q, k, v = (to_dev(g[n], dev) for n in ("q", "k", "v"))
+    s = g["q"].shape[0]
+    tab, qw, kw = _rr(g, dev, s)
+    ext = attn_int8.ext()
+    for pre, args in (("", ()), ("r", (tab, qw, kw, 1e-5))):
+        ops = ext.int8_prepass(q, k, v, *args, config=94)
+        assert len(ops) == 8
+        pp = dict(zip(("q8", "qs", "k8", "ks", "ksb", "vt", "vscale", "vmean"), ops))
+        pp["kmean"] = None
+        for n in ("q8", "qs", "k8", "ks", "ksb"):
+            assert np.array_equal(to_np(pp[n]), g[pre + n]), pre + n
+        vpre = ""
+        assert np.array_equal(to_np(pp["vscale"]), g[vpre + "vscale"]) and np.array_equal(to_np(pp["vmean"]),
+                                                                                          g[vpre + "vmean"])
+        vt = to_np(pp["vt"])
+        keys = _perm_keys_u8(vt.shape[2])
+        vpad = np.zeros((vt.shape[2],) + g["v8"].shape[1:], np.int8)
+        vpad[:s] = g["v8"]
+        assert np.array_equal(vt, vpad[keys].transpose(1, 2, 0))
+    got = bf16_to_f32(to_np(attn_int8.attention(q, k, v)))                 # config None -> RAPIDH3_ATTN_CONFIG / 0
+    assert attn_int8.CONFIG != 0 or rel_l2(got, bf16_to_f32(g["out"])) < TOL
+
+
 def test_u8_forward_golden(dev, golden):
     """Every public route to the production kernel: attention(config), attention_rr (default config 94),
     cross-attention, no rotation / no V smoothing, and the text bias."""

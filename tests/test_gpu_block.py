@@ -36,12 +36,21 @@ def _setup(rng):
     return _bf(x), ws, norms, mod, tab
 
 
-@pytest.mark.parametrize("recipe,fuse_qkv", [("int8_rowwise", True), ("int8_rot", True), ("int8_rowwise", False)])
-def test_fused_block_chain(dev, recipe, fuse_qkv):
+@pytest.mark.parametrize("recipe,fuse_qkv,tokrows", [("int8_rowwise", True, False), ("int8_rot", True, False),
+                                                      ("int8_rowwise", False, False), ("int8_rowwise", False, True)])
+def test_fused_block_chain(dev, recipe, fuse_qkv, tokrows):
+    """tokrows: the second segment carries per-token modulation rows (a LongTensor row, the _mod_gate branch of
+    __init__.py:244-245): its quantizers index the tables per token and its gated residuals run the per-row gate
+    epilogue."""
+    import torch
     from rapid_h3 import gemm, kernels
     from rapid_h3.block import BlockWeights, fused_block
     rng = np.random.default_rng(21 if recipe == "int8_rot" else 20)
     x0, ws, norms, mod, tab = _setup(rng)
+    segments = SEGMENTS
+    if tokrows:
+        segments = [(0, 200, 0), (200, S, rng.integers(0, R, S - 200))]
+    segs_dev = [(a, b, torch.from_numpy(r).to(dev) if isinstance(r, np.ndarray) else r) for a, b, r in segments]
     # weights: GPU quantization equals the oracle's
     qw, oqw = {}, {}
     for name, w in ws.items():
@@ -57,14 +66,24 @@ def test_fused_block_chain(dev, recipe, fuse_qkv):
     modd = tuple(to_dev(m, dev) for m in mod)
     x = to_dev(x0, dev)
     tr = {}
-    out = fused_block(x, w, modd, SEGMENTS, to_dev(tab, dev).view(1, S, 1, 48, 2, 2), trace=tr, fuse_qkv=fuse_qkv)
+    out = fused_block(x, w, modd, segs_dev, to_dev(tab, dev).view(1, S, 1, 48, 2, 2), trace=tr, fuse_qkv=fuse_qkv)
     T = {k: to_np(v) for k, v in tr.items()}
 
     rot = recipe == "int8_rot"
     norm_q = oq.norm_mod_rot_quant_rows_i8 if rot else oq.norm_mod_quant_rows_i8
     heads_q = oq.rot_quant_heads_i8 if rot else oq.heads_quant_rows_i8
     rows_q = oq.rot_quant_rows_i8 if rot else (lambda h: oq.quantize_rows(h, "int8_rowwise"))
-    idx = np.concatenate([np.full(b - a, r, np.int32) for a, b, r in SEGMENTS])
+    idx = np.concatenate([np.asarray(r, np.int32) if isinstance(r, np.ndarray) else np.full(b - a, r, np.int32)
+                          for a, b, r in segments])
+
+    def gated(xq, xs, wq, ws_, gate, resid):
+        out_ = resid.copy()
+        for a, b, r in segments:
+            if isinstance(r, np.ndarray):
+                out_[a:b] = og.int8_gemm_gated_residual_rows(xq[a:b], xs[a:b], wq, ws_, _bf(gate), r, resid[a:b])
+            else:
+                out_[a:b] = og.int8_gemm_gated_residual(xq[a:b], xs[a:b], wq, ws_, _bf(gate[r]), resid[a:b])
+        return out_
     shift_msa, scale_msa, gate_msa, shift_mlp, scale_mlp, gate_mlp = mod
 
     # 1. RMSNorm + modulation quantizer
@@ -85,9 +104,7 @@ def test_fused_block_chain(dev, recipe, fuse_qkv):
     oq_, os_ = heads_q(o)
     assert np.array_equal(T["oq"], oq_) and np.array_equal(T["os"], os_)
     # 5. out-proj GEMM + gated residual per segment (gate row rounded to bf16, __init__.py:242-251)
-    xa = x0.copy()
-    for a, b, r in SEGMENTS:
-        xa[a:b] = og.int8_gemm_gated_residual(T["oq"][a:b], T["os"][a:b], *oqw["out"], _bf(gate_msa[r]), xa[a:b])
+    xa = gated(T["oq"], T["os"], *oqw["out"], gate_msa, x0)
     assert np.array_equal(T["x_attn"], xa)
     # 6. second RMSNorm + modulation quantizer
     q2, s2 = norm_q(T["x_attn"], norms["norm2"], 1e-6, idx, shift_mlp, scale_mlp)
@@ -101,9 +118,7 @@ def test_fused_block_chain(dev, recipe, fuse_qkv):
     hq, hs = rows_q(T["h"])
     assert np.array_equal(T["hq"], hq) and np.array_equal(T["hs"], hs)
     # 9. FFN-down GEMM + gated residual per segment -> the block output
-    xf = T["x_attn"].copy()
-    for a, b, r in SEGMENTS:
-        xf[a:b] = og.int8_gemm_gated_residual(T["hq"][a:b], T["hs"][a:b], *oqw["fc2"], _bf(gate_mlp[r]), xf[a:b])
+    xf = gated(T["hq"], T["hs"], *oqw["fc2"], gate_mlp, T["x_attn"])
     assert np.array_equal(to_np(out), xf)
     assert out.data_ptr() == x.data_ptr()          # in place, like the reference's residual stream
 

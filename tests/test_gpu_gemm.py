@@ -115,6 +115,27 @@ def test_gemm_persistent_epilogues(dev, m, n, k):
     assert og.rel_l2(got, bf16_to_f32(og.fp8_gemm(fq, xs, fwq, ws))) < 1e-2
 
 
+@pytest.mark.parametrize("m,n,k", [(4500, 4112, 512), (300, 264, 128)])
+def test_gemm_gated_rows(dev, m, n, k):
+    """The gated residual with a gate row per token (per-token modulation) bit-exact against the oracle, on the
+    persistent kernel (K 512) and on the one-tile-per-workgroup kernel (K 128); rows index a 7-row table."""
+    import torch
+    from rapid_h3 import gemm
+    rng = np.random.default_rng(m + k)
+    xq = np.clip(np.rint(rng.standard_normal((m, k)) * 30), -127, 127).astype(np.int8)
+    wq = np.clip(np.rint(rng.standard_normal((n, k)) * 30), -127, 127).astype(np.int8)
+    xs = (rng.random((m, 1)) * 1e-3 + 1e-4).astype(np.float32)
+    ws = (rng.random((1, n)) * 1e-3 + 1e-4).astype(np.float32)
+    tab = _bf(rng.standard_normal((7, n)))
+    rows = rng.integers(0, 7, m)
+    resid = _bf(rng.standard_normal((m, n)))
+    rt = to_dev(resid, dev)
+    r = gemm.int8_gemm_gated_residual_rows(to_dev(xq, dev), to_dev(xs, dev), to_dev(wq, dev), to_dev(ws, dev),
+                                           to_dev(tab, dev), torch.from_numpy(rows).to(dev), rt)
+    assert r is rt
+    assert np.array_equal(to_np(rt), og.int8_gemm_gated_residual_rows(xq, xs, wq, ws, tab, rows, resid))
+
+
 def test_gemm_rejects_bad_shapes(dev):
     import torch
     from rapid_h3 import gemm

@@ -50,6 +50,47 @@ def test_quant_linear_adopts_convrot_and_refuses_cpu(dev):
         QuantLinear(w, mode="bf16")
 
 
+@pytest.mark.parametrize("dtype", ["float32", "float16", "bfloat16"])
+def test_quantize_any_dtype_against_torch(dev, dtype):
+    """quantize_weight / quantize_rows / linear for weights and activations of any float dtype, against the
+    reference's own torch formulas run on the CPU (kernels.py:57-82, :125-137): int8 and FP8 row-wise codes and
+    scales bit-exact, fp8_tensor codes and its scalar scale bit-exact, and for non-bf16 x the int8_rowwise output
+    (acc * sa * ws).to(x.dtype) bit-exact (fp8_rowwise within rel-L2 1e-2: its product is fp32-accumulated)."""
+    import torch
+    from rapid_h3 import kernels
+    dt = getattr(torch, dtype)
+    g = torch.Generator(device="cpu").manual_seed(9)
+    w = (0.02 * torch.randn(136, 320, generator=g)).to(dt)
+    x = torch.randn(77, 320, generator=g).to(dt)
+    wf = w.float()
+    for mode in ("int8_rowwise", "fp8_rowwise"):
+        qw = kernels.quantize_weight(w.to(dev), mode)
+        qmax = 127.0 if mode == "int8_rowwise" else 448.0
+        s = (wf.abs().amax(dim=1, keepdim=True) / qmax).clamp_min(1e-12)
+        ref = ((wf / s).round().clamp(-127, 127).to(torch.int8) if mode == "int8_rowwise"
+               else (wf / s).clamp(-448, 448).to(torch.float8_e4m3fn))
+        assert torch.equal(qw.q.cpu().view(torch.int8), ref.view(torch.int8)) and torch.equal(qw.scale.cpu(), s.t())
+    qt = kernels.quantize_weight(w.to(dev), "fp8_tensor")
+    st = (wf.abs().amax() / 448.0).clamp_min(1e-12)
+    assert qt.scale.shape == () and qt.scale.item() == st.item()
+    assert torch.equal(qt.q.cpu().view(torch.int8), (wf / st).clamp(-448, 448).to(torch.float8_e4m3fn).view(torch.int8))
+    xq, sa = kernels.quantize_rows(x.to(dev), "int8_rowwise")
+    sx = (x.abs().amax(dim=-1, keepdim=True).float() / 127.0).clamp_min(1e-12)
+    assert torch.equal(sa.cpu(), sx)
+    assert torch.equal(xq.cpu(), (x.float() / sx).round().clamp(-127, 127).to(torch.int8))
+    if dt != torch.bfloat16:
+        qw = kernels.quantize_weight(w.to(dev), "int8_rowwise")
+        y = kernels.linear(x.to(dev), qw, "int8_rowwise")
+        ref = (torch._int_mm(xq.cpu(), qw.q.cpu().t().contiguous()).float() * sx * qw.scale.cpu()).to(dt)
+        assert y.dtype == dt and torch.equal(y.cpu(), ref)
+        qf = kernels.quantize_weight(w.to(dev), "fp8_rowwise")
+        yf = kernels.linear(x.to(dev), qf, "fp8_rowwise")
+        exact = x.float() @ w.float().t()
+        assert yf.dtype == dt and float((yf.cpu().float() - exact).norm() / exact.norm()) < 0.05
+        with pytest.raises(ValueError):
+            kernels.linear(x.to(dev), qw, "int8_rot")            # the reference's torch path has no int8_rot
+
+
 def test_c1_linear_full_size(dev):
     """BASELINE config C1, the reference's CPU-runnable case (bench/int8_bench.py:37-47): X [4096, 3072]
     ~ N(0, 1) with 31 of its channels (1 %) x20, W [3072, 3072] ~ N(0, 0.02), seed 0, generated on the CPU.

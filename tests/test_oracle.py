@@ -315,6 +315,24 @@ def test_gemm_epilogues_match_torch(golden):
     assert np.array_equal(g["gated"], np_bf16(r))
 
 
+def test_gated_rows_matches_torch_gather(golden):
+    """Per-token gate rows: torch's addcmul_ with the gate table gathered by row index (_mod_gate of tensor rows);
+    a table whose rows are all the segment's row reduces to the per-segment epilogue."""
+    g = golden("gemm")
+    m, n = g["resid"].shape
+    rng = np.random.default_rng(5)
+    tab = f32_to_bf16(rng.standard_normal((5, n)).astype(np.float32))
+    rows = rng.integers(0, 5, m)
+    y = (torch.from_numpy(g["acc"]).float() * torch.from_numpy(g["xs"]) * torch.from_numpy(g["ws"])).to(torch.bfloat16)
+    r = t_bf16(g["resid"]).clone()
+    r.addcmul_(y, t_bf16(tab)[torch.from_numpy(rows)])
+    got = og.int8_gemm_gated_residual_rows(g["xq"], g["xs"], g["wq"], g["ws"], tab, rows, g["resid"])
+    assert np.array_equal(got, np_bf16(r))
+    one = np.broadcast_to(g["gate"].reshape(1, -1), (3, n))
+    assert np.array_equal(og.int8_gemm_gated_residual_rows(g["xq"], g["xs"], g["wq"], g["ws"], one, np.full(m, 1),
+                                                           g["resid"]), g["gated"])
+
+
 def test_swiglu_perm_and_epilogue(golden):
     p = og.swiglu_perm(32)
     assert sorted(p) == list(range(32))
