@@ -9,8 +9,12 @@ value = algorithmic int8-MFMA work of the block (4 GEMMs 2*M*N*K + attention 4*S
 TOPS, inputs and weights resident in HBM before the timed region. Synthetic data: activations N(0,1)
 with 1 % of channels x20, weights N(0, 0.02) random init, modulation and norm weights random.
 
-    python bench.py [--gpus 1] [--steps 3] [--warmup 1] [--tokens 145152] [--no-cpu] [--recipe int8_rot]
-                    [--attn-config 94] [--model h3]
+    python bench.py [--gpus 1] [--steps 3] [--warmup 1] [--tokens 145152] [--no-cpu] [--no-side]
+                    [--recipe int8_rot] [--attn-config 94] [--model h3]
+
+After the timed block (outside the timed region): the C3 FP8 GEMMs at the three C2 shapes and hipBLASLt's int8
+GEMM (torch._int_mm) beside this build's at the four block shapes (fp8_gemm_c3, int8_gemm_vs_hipblaslt), and the
+CPU baseline (cpu_baseline) on the same block's inputs.
 
 --model h3 runs the same block at MiniMax-H3's own shapes (hidden 5376, 56 x 128 heads, FFN 14336,
 S = 44,992 by default), the shapes of the reference's published GB10 numbers; the default (c2) is the
@@ -31,9 +35,10 @@ METRIC = "INT8 attn + W8A8 GEMM TOPS (frac of MFMA peak) at 145k tokens; ms/DiT 
 PEAK_INT8_TOPS = 5033.0        # MI355X dense int8 MFMA
 PEAK_BF16_TFLOPS = 2517.0      # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
+PEAK_FP8_TFLOPS = 5033.0       # MI355X dense OCP-FP8 MFMA
 D = 128
 MODELS = {  # hidden, heads, FFN width, default tokens
-    "c2": (3072, 24, 8192, 145152),    # BASELINE configs C2 / C4: 36 x 48 x 84 latent patches
+    "c2": (3072, 24, 8192, 145152),    # BASELINE.json configs C2 / C4: 36 x 48 x 84 latent patches
     "h3": (5376, 56, 14336, 44992),    # MiniMax-H3 (the reference's bench/microbench.py:15, docs/kernels.md:405)
 }
 HIDDEN, HEADS, FFN, _ = MODELS["c2"]
@@ -96,47 +101,182 @@ def setup(m, device, recipe="int8_rowwise"):
     return x, w, mod, segments, tab
 
 
-def cpu_baseline(m):
-    """The CPU oracle (numpy port of the reference's PyTorch path) on a bounded sample of the same
-    block: every quantizer and GEMM at 16,384 of the M tokens, attention for 2,048 query rows x all S
-    keys x 1 head (about 10 s of CPU work together), each extrapolated linearly to the full block."""
+def _cpu_threads():
+    """Threads for the CPU baseline: every core this process may run on (os.sched_getaffinity; on the GPU box that
+    is the job's share, where os.cpu_count() counts the whole host), set for torch and numpy's BLAS alike."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    import torch
+    torch.set_num_threads(n)
+    try:
+        from threadpoolctl import threadpool_limits
+        threadpool_limits(n)
+    except Exception:  # noqa: BLE001
+        pass
+    return n
+
+
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _median_time(fn, runs=5, warmup=1):
+    for _ in range(warmup):
+        fn()
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    ts.sort()
+    return ts[len(ts) // 2]
+
+
+def cpu_baseline(m, x, w, mod, segments, tab, trace):
+    """The CPU baseline: the build's CPU restatement of the reference's PyTorch path (oracle/, a
+    numpy port: kernels.quantize_rows / quantize_weight, the exact int32 product, the (acc * xs) * ws epilogues, the
+    per-block attention emulation), on the host cores of the GPU box, median of 5 runs after 1 warm-up.
+      * C1 (X [4096, 3072] with 1 % outlier channels, W [3072, 3072] ~ N(0, 0.02), seed 0): measured in full;
+      * the block: every quantizer and GEMM of the timed DiT block on its first MS tokens, and the attention of
+        head 0 for the first R query rows against all keys (the pre-pass of that head in full), on the GPU leg's own
+        inputs (x, the block's int8 weights, its modulation, and the qkv / o / h of a traced run of the same block),
+        extrapolated to the block: token phases x M / MS, attention rows x S / R x H, the pre-pass x H."""
     import numpy as np
+    import torch
     from oracle import attn as oa
     from oracle import gemm as og
     from oracle import quant as oq
     from oracle.numerics import f32_to_bf16
-    try:
-        from threadpoolctl import threadpool_info
-        cores = max([i.get("num_threads", 1) for i in threadpool_info()] + [1])
-    except Exception:  # noqa: BLE001
-        cores = os.cpu_count()
-    rng = np.random.default_rng(0)
-    ms = 16384
-    t_gemm = 0.0
-    x = f32_to_bf16(rng.standard_normal((ms, HIDDEN)).astype(np.float32))
-    for n, k in ((3 * HEADS * D, HIDDEN), (HIDDEN, HEADS * D), (2 * FFN, HIDDEN), (HIDDEN, FFN)):
-        a = x if k == HIDDEN else f32_to_bf16(rng.standard_normal((ms, k)).astype(np.float32))
-        wq, ws = oq.quantize_weight(f32_to_bf16((0.02 * rng.standard_normal((n, k))).astype(np.float32)))
-        t0 = time.perf_counter()
-        xq, xs = oq.quantize_rows(a)
+    threads = _cpu_threads()
+
+    def host(t):
+        t = t.detach().cpu()
+        return t.view(torch.int16).numpy().view(np.uint16) if t.dtype == torch.bfloat16 else t.numpy()
+
+    # C1 in full, generated on the CPU as BASELINE.json's config C1 (seed 0)
+    g = torch.Generator().manual_seed(0)
+    x1 = torch.randn(4096, 3072, generator=g)
+    x1[:, torch.randperm(3072, generator=g)[:31]] *= 20
+    w1 = 0.02 * torch.randn(3072, 3072, generator=g)
+    x1b, w1b = host(x1.to(torch.bfloat16)), host(w1.to(torch.bfloat16))
+
+    def c1():
+        xq, xs = oq.quantize_rows(x1b)
+        wq, ws = oq.quantize_weight(w1b)
         og.int8_gemm(xq, xs, wq, ws)
-        t_gemm += time.perf_counter() - t0
-    rows, s = 2048, m
-    q = f32_to_bf16(rng.standard_normal((s, 1, D)).astype(np.float32))
-    k = f32_to_bf16(rng.standard_normal((s, 1, D)).astype(np.float32))
-    v = f32_to_bf16(rng.standard_normal((s, 1, D)).astype(np.float32))
-    t0 = time.perf_counter()
-    q8, qs, k8, ks, _ = oa.prepass(q[:rows], k)
-    oa.attention_from_codes(q8, qs, k8, ks, v, D ** -0.5, rows=np.arange(rows))
-    t_attn = time.perf_counter() - t0
+    t_c1 = _median_time(c1)
+    ops_c1 = 2 * 4096 * 3072 * 3072
+
+    # the block sample on the GPU leg's inputs
+    ms, rows = 256, 128
+    T = {k: v for k, v in trace.items()}
+    idx = np.zeros(ms, np.int32)
+    for a, b, r in segments:
+        lo, hi = max(a, 0), min(b, ms)
+        if lo < hi:
+            idx[lo:hi] = int(r)
+    mods = [host(t.float()) for t in mod]
+    xs_ = host(x[:ms])
+    xa = host(T["x_attn"][:ms])
+    nw1, nw2 = host(w.norm1_w), host(w.norm2_w)
+    wts = {n: (host(getattr(w, n).q), host(getattr(w, n).scale)) for n in ("qkv", "out", "fc1_perm", "fc2")}
+    oqs = {n: host(T[n][:ms]) for n in ("xq1", "xs1", "oq", "os", "xq2", "xs2", "hq", "hs")}
+    o_h = host(T["o"][0][:, :ms])                                          # [H, ms, 128] head-major
+    h_ = host(T["h"][:ms])
+    s = x.shape[0]
+    qkv0 = T["qkv"].view(s, 3, HEADS, D)[:, :, 0]                           # head 0 of the raw projection
+    q0, k0, v0 = host(qkv0[:rows, 0]).reshape(rows, 1, D), host(qkv0[:, 1]).reshape(s, 1, D), host(qkv0[:, 2])
+    v0 = v0.reshape(s, 1, D)
+    tabh = host(tab.reshape(s, 48, 2, 2))
+    rr = (tabh, host(w.q_norm_w), host(w.k_norm_w), w.qk_eps)
+
+    def token_phases():
+        oq.norm_mod_quant_rows_i8(xs_, nw1, w.eps, idx, mods[0], mods[1])
+        og.int8_gemm(oqs["xq1"], oqs["xs1"], *wts["qkv"])
+        oq.heads_quant_rows_i8(o_h)
+        og.int8_gemm_gated_residual(oqs["oq"], oqs["os"], *wts["out"], f32_to_bf16(mods[2][0]), xa)
+        oq.norm_mod_quant_rows_i8(xa, nw2, w.eps, idx, mods[3], mods[4])
+        og.int8_gemm_swiglu(oqs["xq2"], oqs["xs2"], *wts["fc1_perm"])
+        oq.quantize_rows(h_, "int8_rowwise")
+        og.int8_gemm_gated_residual(oqs["hq"], oqs["hs"], *wts["fc2"], f32_to_bf16(mods[5][0]), xa)
+
+    pre = {}
+
+    def prepass():
+        pre["ops"] = oa.prepass(np.concatenate([q0, np.zeros((s - rows, 1, D), np.uint16)]), k0, rr=rr)
+
+    def attn_rows():
+        q8, qs, k8, ks, _ = pre["ops"]
+        oa.attention_from_codes(q8, qs, k8, ks, v0, D ** -0.5, rows=np.arange(rows))
+
+    t_tok = _median_time(token_phases)
+    t_pre = _median_time(prepass)
+    t_att = _median_time(attn_rows)
     gemms, attn_ops = block_ops(m)
-    t_full = t_gemm * (m / ms) + t_attn * (s / rows) * HEADS
+    t_block = t_tok * (m / ms) + t_pre * HEADS + t_att * (s / rows) * HEADS
     total = sum(gemms.values()) + attn_ops
-    return {"value": round(total / t_full / 1e12, 4), "unit": "TOPS", "cores": int(cores), "kind": "port",
-            "sample": (f"oracle quantizers+4 GEMMs at M={ms} (x{m / ms:.1f}) and attention {rows} query rows x "
-                       f"{s} keys x 1 head (x{s / rows * HEADS:.0f}); {t_gemm + t_attn:.1f} s measured, "
-                       f"{t_full:.0f} s extrapolated per block"),
-            "seconds_per_block": round(t_full, 1)}
+    return {"value": round(total / t_block / 1e12, 4), "unit": "TOPS", "cores": int(threads), "kind": "port",
+            "cpu_model": _cpu_model(), "os_cpu_count": os.cpu_count(), "runs": "median of 5 after 1 warm-up",
+            "c1_measured": {"ms": round(t_c1 * 1e3, 1), "tops": round(ops_c1 / t_c1 / 1e12, 4),
+                            "workload": "C1 W8A8 linear, 4096 x 3072 x 3072, in full"},
+            "sample": (f"oracle (numpy) on the GPU leg's inputs: the block's 4 quantizers + 4 GEMMs on its first {ms} "
+                       f"tokens ({t_tok:.2f} s, x{m / ms:.0f}), head 0's pre-pass over all {s} keys ({t_pre:.2f} s, "
+                       f"x{HEADS}) and its attention for {rows} query rows ({t_att:.2f} s, x{s / rows * HEADS:.0f}); "
+                       f"extrapolated to the block; C1 measured in full"),
+            "seconds_per_block": round(t_block, 1)}
+
+
+def gemm_side_measurements(m, device, reps=5):
+    """C3 FP8 (OCP e4m3) row-wise GEMMs at the three C2 shapes (rh3_gemm_fp8, bf16 out) and hipBLASLt's int8 GEMM
+    (torch._int_mm, int32 out, no epilogue) at the four C2 block shapes, each the mean of reps launches timed
+    with events on torch's current stream, codes uniform random (the GEMMs' speed does not depend on values)."""
+    import torch
+    from rapid_h3 import gemm
+    g = torch.Generator(device=device).manual_seed(1)
+    shapes = {"qkv": (3 * HEADS * D, HIDDEN), "up": (2 * FFN, HIDDEN), "down": (HIDDEN, FFN), "out": (HIDDEN, HEADS * D)}
+
+    def timeit(fn):
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+    fp8, vendor = {}, {}
+    xs = torch.rand(m, 1, device=device, generator=g) * 1e-3
+    for name, (n, k) in shapes.items():
+        ws = torch.rand(1, n, device=device, generator=g) * 1e-3
+        ops = 2 * m * n * k
+        if name != "out":
+            xq = torch.randint(0, 256, (m, k), device=device, dtype=torch.uint8, generator=g)
+            xq[(xq & 0x7F) == 0x7F] = 0
+            wq = torch.randint(0, 256, (n, k), device=device, dtype=torch.uint8, generator=g)
+            wq[(wq & 0x7F) == 0x7F] = 0
+            xf, wf = xq.view(torch.float8_e4m3fn), wq.view(torch.float8_e4m3fn)
+            t = timeit(lambda: gemm.fp8_gemm(xf, xs, wf, ws))
+            fp8[name] = {"ms": round(t, 3), "tflops": round(ops / t / 1e9, 1), "frac_fp8_peak": round(ops / t / 1e9 / PEAK_FP8_TFLOPS, 4),
+                         "shape": [m, n, k]}
+            del xq, wq, xf, wf
+        xi = torch.randint(-127, 128, (m, k), device=device, dtype=torch.int8, generator=g)
+        wi = torch.randint(-127, 128, (n, k), device=device, dtype=torch.int8, generator=g)
+        wt = wi.t()
+        tv = timeit(lambda: torch._int_mm(xi, wt))
+        to = timeit(lambda: gemm.int8_gemm(xi, xs, wi, ws))
+        vendor[name] = {"int_mm_ms": round(tv, 3), "int_mm_tops": round(ops / tv / 1e9, 1),
+                        "rh3_plain_ms": round(to, 3), "rh3_plain_tops": round(ops / to / 1e9, 1), "shape": [m, n, k]}
+        del xi, wi, wt
+        torch.cuda.empty_cache()
+    return fp8, vendor
 
 
 def traffic_from_profile():
@@ -216,6 +356,8 @@ def main():
     ap.add_argument("--model", default="c2", choices=tuple(MODELS),
                     help="c2: hidden 3072, 24 heads, FFN 8192 (the metric's); h3: 5376, 56, 14336")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-side", action="store_true",
+                    help="skip the C3 FP8 GEMMs and the hipBLASLt int8 GEMM comparison after the timed block")
     ap.add_argument("--recipe", default="int8_rowwise", choices=("int8_rowwise", "int8_rot"),
                     help="int8_rowwise (the configuration the metric names) or the reference's int8_rot")
     ap.add_argument("--attn-config", type=int, default=None,
@@ -327,8 +469,18 @@ def main():
                      "avg_launch_ms": round(t_attn, 3)},
         "wall_s_timed": round(wall, 2),
     }
+    if not a.no_side and ac is None and a.model == "c2":
+        fp8, vendor = gemm_side_measurements(m, dev)
+        out["fp8_gemm_c3"] = fp8
+        out["int8_gemm_vs_hipblaslt"] = vendor
     if not a.no_cpu:
-        out["cpu_baseline"] = cpu_baseline(m)
+        # one traced run of the same block supplies the intermediate tensors the CPU sample starts from
+        x_in = x.clone()
+        tr = {}
+        fused_block(x, w, mod, segments, tab, attn_config=ac, trace=tr, **fq)
+        torch.cuda.synchronize()
+        out["cpu_baseline"] = cpu_baseline(m, x_in, w, mod, segments, tab, tr)
+        del tr
     print(json.dumps(out), flush=True)
 
 

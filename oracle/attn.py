@@ -104,24 +104,24 @@ def prepass(q, k, rr=None, smooth_k=True):
     return q8, qs, k8, ks, km
 
 
-def attention_from_codes(q8, qs, k8, ks, v, scale, rows=None, heads=None):
+def attention_from_codes(q8, qs, k8, ks, v, scale, rows=None, heads=None, out_dtype=F32):
     """Attention on the INT8 operands, float64 softmax: out[s, h] = softmax_j(scale * qs*ks * q8.k8) v.
     q8/k8 [H, Spad, D] int8; qs/ks [H, Spad/128]; v [S, H, D] bf16 bits (or fp32). Sk is v's S
     (cross-attention: q8 may have another length). rows: query indices to evaluate (default all).
-    Returns fp32 [len(rows), len(heads), D]."""
+    Returns [len(rows), len(heads), D] in out_dtype (fp32; np.float64 keeps the float64 result)."""
     vf = _as_f32(v).astype(np.float64)
     sk = vf.shape[0]
     hh = range(q8.shape[0]) if heads is None else heads
     sq = q8.shape[1] if rows is None else None
     rows = np.arange(sq) if rows is None else np.asarray(rows)
-    out = np.zeros((len(rows), len(hh), D), F32)
+    out = np.zeros((len(rows), len(hh), D), out_dtype)
     for hi, h in enumerate(hh):
         qd = q8[h, rows].astype(np.float64) * np.repeat(qs[h], BLOCK)[rows][:, None]
         kd = k8[h, :sk].astype(np.float64) * np.repeat(ks[h], BLOCK)[:sk][:, None]
         lg = (qd @ kd.T) * scale
         lg -= lg.max(axis=1, keepdims=True)
         p = np.exp(lg)
-        out[:, hi] = ((p @ vf[:, h]) / p.sum(axis=1, keepdims=True)).astype(F32)
+        out[:, hi] = ((p @ vf[:, h]) / p.sum(axis=1, keepdims=True)).astype(out_dtype)
     return out
 
 

@@ -123,11 +123,14 @@ def test_fused_block_chain(dev, recipe, fuse_qkv, tokrows):
     assert out.data_ptr() == x.data_ptr()          # in place, like the reference's residual stream
 
 
-@pytest.mark.parametrize("text_bias", [None, (150, 1.25)])
-def test_fused_block_production_attention(dev, text_bias):
+@pytest.mark.parametrize("text_bias,fuse_qkv", [(None, False), ((150, 1.25), False), (None, True), ((150, 1.25), True)])
+def test_fused_block_production_attention(dev, text_bias, fuse_qkv):
     """The block chain with the reference's production attention (attn_config 94, its 194 preset): the
     attention stage matches the oracle's tile-by-tile emulation on the GPU's own qkv (with and without the
-    text bias), and the head-major quantizer that follows consumes it bit-exactly."""
+    text bias), and the head-major quantizer that follows consumes it bit-exactly. fuse_qkv: the QKV GEMM's epilogue
+    writes the per-token H128-rotated Q operands and the K / V statistics (the reference's config 3xx route); its
+    Q codes and scales are checked bit for bit against the oracle's pre-pass of the same qkv, and its K / V columns
+    against the oracle GEMM."""
     from rapid_h3 import gemm, kernels
     from rapid_h3.block import BlockWeights, fused_block
     rng = np.random.default_rng(22)
@@ -140,7 +143,8 @@ def test_fused_block_production_attention(dev, text_bias):
                      k_norm_w=to_dev(norms["kn"], dev), heads=HEADS, eps=1e-6, qk_eps=1e-6)
     tr = {}
     fused_block(to_dev(x0, dev), w, tuple(to_dev(m, dev) for m in mod), SEGMENTS,
-                to_dev(tab, dev).view(1, S, 1, 48, 2, 2), trace=tr, attn_config=94, text_bias=text_bias)
+                to_dev(tab, dev).view(1, S, 1, 48, 2, 2), trace=tr, attn_config=94, text_bias=text_bias,
+                fuse_qkv=fuse_qkv)
     T = {k: to_np(v) for k, v in tr.items()}
     qkv_ref = og.int8_gemm(T["xq1"], T["xs1"], *[o for o in (to_np(qw["qkv"].q), to_np(qw["qkv"].scale))])
     assert np.array_equal(T["qkv"][:, HID:], qkv_ref[:, HID:])

@@ -452,6 +452,30 @@ def test_attention_oracles_agree_with_sdpa():
     assert og.rel_l2(outn, ex) > og.rel_l2(out, ex)
 
 
+def test_attention_from_codes_against_sdpa_on_dequantized_codes():
+    """attention_from_codes pinned to 1e-10 (float64) against torch's SDPA in float64 on the dequantized operands
+    q8 * qs[block], k8 * ks[block]: three query and three key blocks of 128 tokens whose scales differ by up to 40x,
+    cross-attention with a ragged key count and sampled rows, so a wrong block index (a scale taken from a neighbour
+    block), a transposed operand or a dropped scale moves the result far past the bound."""
+    rng = np.random.default_rng(13)
+    h, sq, sk = 2, 384, 300                                    # 3 query blocks; keys 300 of 384 padded
+    q8 = rng.integers(-127, 128, (h, sq, 128)).astype(np.int8)
+    k8 = rng.integers(-127, 128, (h, 384, 128)).astype(np.int8)
+    k8[:, sk:] = 0
+    qs = np.array([[0.002, 0.02, 0.08], [0.05, 0.004, 0.01]], np.float32)
+    ks = np.array([[0.001, 0.04, 0.01], [0.03, 0.002, 0.02]], np.float32)
+    v = rng.standard_normal((sk, h, 128)).astype(np.float32)
+    scale = 128 ** -0.5
+    rows = np.array([0, 5, 127, 128, 200, 255, 256, 383])
+    got = oa.attention_from_codes(q8, qs, k8, ks, v, scale, rows=rows, out_dtype=np.float64)
+    qd = torch.from_numpy(q8.astype(np.float64) * np.repeat(qs, 128, axis=1)[..., None])
+    kd = torch.from_numpy(k8[:, :sk].astype(np.float64) * np.repeat(ks, 128, axis=1)[:, :sk, None])
+    vd = torch.from_numpy(v.astype(np.float64)).transpose(0, 1)
+    ref = torch.nn.functional.scaled_dot_product_attention(qd[None], kd[None], vd[None], scale=scale)[0]  # [H, Sq, D]
+    ref = ref.numpy().transpose(1, 0, 2)[rows]
+    assert np.abs(got - ref).max() <= 1e-10 * np.abs(ref).max()
+
+
 def test_golden_fixtures_regenerate(golden):
     """The committed fixtures are what the oracle computes today (guards silent oracle drift)."""
     g = golden("attention")
