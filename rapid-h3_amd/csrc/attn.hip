@@ -203,6 +203,21 @@ constexpr int KSLOT = STEP * D;      // K tile: 64 keys x 128 B, chunk c of row 
 constexpr int VSLOT = D * STEP * 2;  // V^T tile: 128 d x 64 keys x 2 B, chunk c of row d at c ^ vsw(d)
 constexpr int NRING = 4;             // slots of the K ring and of the V^T ring
 
+// Issue order of a run of N (LDS read, MFMA) pairs: the first READ_AHEAD reads, then each MFMA followed by the
+// next read, then the last MFMAs, so every operand is read READ_AHEAD MFMAs (>= 96 pipe cycles) before its use.
+// Left alone, the scheduler places each read right before its MFMA and waits for it there.
+constexpr int READ_AHEAD = 3;
+template <int N>
+__device__ __forceinline__ void read_ahead() {
+  __builtin_amdgcn_sched_group_barrier(0x100, READ_AHEAD, 0);  // 0x100: LDS reads
+#pragma unroll
+  for (int i = 0; i < N - READ_AHEAD; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);          // 0x008: MFMA
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+  }
+  __builtin_amdgcn_sched_group_barrier(0x008, READ_AHEAD, 0);
+}
+
 // Step j reads K(j) and V^T(j) from ring slot u = (j - j0) % 4 and first copies K(j+2), V^T(j+2) into slot
 // (u + 2) % 4, last read in step j-2 (every wave has passed the end-of-step barrier of step j-1). Steps past Sk
 // are not run; the ragged last step is a separate instantiation, so the full steps carry no key mask.
@@ -329,6 +344,7 @@ __device__ __forceinline__ void fwd_body(const FwdArgs& a, const int bid, int8_t
         s[kb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf, qf[ds], ds == 0 ? magic : s[kb], 0, 0, 0);
       }
     }
+    read_ahead<8>();
   };
   // online softmax of step j's scores and O^T += V^T(j) . P^T; TAIL steps hold 1..63 keys below Sk
   uint32_t pk[2][8];  // P of the current step, bf16 pairs, the B operand of the P.V MFMAs
@@ -410,14 +426,12 @@ __device__ __forceinline__ void fwd_body(const FwdArgs& a, const int bid, int8_t
         }
       }
     }
+    read_ahead<16>();
   };
 
-  // Barrier B_j ends the use of ring slot j. Waves 0-3 and 8-11 meet B_j after pv(j); waves 4-7 (one per SIMD)
-  // meet it after qk(j+1), half a step behind, so their softmax runs while the other two waves of the SIMD issue
-  // MFMAs. Each wave issues the copies of step j+2 right after B_(j-1), into the slot whose last readers (pv(j-2)
-  // of the lagging waves) ran before B_(j-1); before B_j it waits for its copies of step j+1 (vmcnt(2) leaves the
-  // two issued after B_(j-1) in flight), so slot j+1 is complete past B_j.
-  const bool lag = (wave >> 2) == 1;
+  // Barrier B_j ends the use of ring slot j: every wave meets it after pv(j). Each wave issues the copies of step
+  // j+2 right after B_(j-1), into the slot last read in step j-2; before B_j it waits for its copies of step j+1
+  // (vmcnt(2) leaves the two issued in step j in flight), so slot j+1 is complete past B_j.
   auto barrier = [&]() __attribute__((always_inline)) {
     asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
     __builtin_amdgcn_s_barrier();
@@ -425,15 +439,11 @@ __device__ __forceinline__ void fwd_body(const FwdArgs& a, const int bid, int8_t
   };
   auto step = [&](const int j, auto tail) __attribute__((always_inline)) {
     const uint32_t slot = static_cast<uint32_t>(j - j0) & (NRING - 1);
-    if (!lag) load_step(j + 2);
+    load_step(j + 2);
     qk(slot);
-    if (lag) {
-      barrier();
-      load_step(j + 3);
-    }
     softmax(j, tail);
     pv(slot);
-    if (!lag) barrier();
+    barrier();
   };
 
   load_step(j0);
@@ -442,7 +452,6 @@ __device__ __forceinline__ void fwd_body(const FwdArgs& a, const int bid, int8_t
   // wait of its own inside the loop (gfx9 s_waitcnt: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8])
   __builtin_amdgcn_s_waitcnt(0x0f70);
   __syncthreads();
-  if (lag) load_step(j0 + 2);
   const int jf = min(j1, nfull);
   for (int j = j0; j < jf; ++j) step(j, std::false_type{});
   if (rem > 0 && j1 == nsteps) step(nfull, std::true_type{});
