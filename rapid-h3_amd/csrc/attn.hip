@@ -203,21 +203,6 @@ constexpr int KSLOT = STEP * D;      // K tile: 64 keys x 128 B, chunk c of row 
 constexpr int VSLOT = D * STEP * 2;  // V^T tile: 128 d x 64 keys x 2 B, chunk c of row d at c ^ vsw(d)
 constexpr int NRING = 4;             // slots of the K ring and of the V^T ring
 
-// Issue order of a run of N (LDS read, MFMA) pairs: the first READ_AHEAD reads, then each MFMA followed by the
-// next read, then the last MFMAs, so every operand is read READ_AHEAD MFMAs (>= 96 pipe cycles) before its use.
-// Left alone, the scheduler places each read right before its MFMA and waits for it there.
-constexpr int READ_AHEAD = 3;
-template <int N>
-__device__ __forceinline__ void read_ahead() {
-  __builtin_amdgcn_sched_group_barrier(0x100, READ_AHEAD, 0);  // 0x100: LDS reads
-#pragma unroll
-  for (int i = 0; i < N - READ_AHEAD; ++i) {
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);          // 0x008: MFMA
-    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-  }
-  __builtin_amdgcn_sched_group_barrier(0x008, READ_AHEAD, 0);
-}
-
 // Step j reads K(j) and V^T(j) from ring slot u = (j - j0) % 4 and first copies K(j+2), V^T(j+2) into slot
 // (u + 2) % 4, last read in step j-2 (every wave has passed the end-of-step barrier of step j-1). Steps past Sk
 // are not run; the ragged last step is a separate instantiation, so the full steps carry no key mask.
@@ -344,7 +329,7 @@ __device__ __forceinline__ void fwd_body(const FwdArgs& a, const int bid, int8_t
         s[kb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf, qf[ds], ds == 0 ? magic : s[kb], 0, 0, 0);
       }
     }
-    read_ahead<8>();
+    read_ahead<8, 3>();
   };
   // online softmax of step j's scores and O^T += V^T(j) . P^T; TAIL steps hold 1..63 keys below Sk
   uint32_t pk[2][8];  // P of the current step, bf16 pairs, the B operand of the P.V MFMAs
@@ -426,7 +411,7 @@ __device__ __forceinline__ void fwd_body(const FwdArgs& a, const int bid, int8_t
         }
       }
     }
-    read_ahead<16>();
+    read_ahead<16, 3>();
   };
 
   // Barrier B_j ends the use of ring slot j: every wave meets it after pv(j). Each wave issues the copies of step

@@ -142,6 +142,20 @@ __device__ __forceinline__ void lds_dma16_s(const void* sbase, uint32_t voff, ui
                : "memory");
 }
 
+// Issue order of a run of N (LDS read, MFMA) pairs: the first A reads, then each MFMA followed by the next read,
+// then the last A MFMAs, so that every operand is read A MFMAs (>= 32 A pipe cycles) before its use. Left alone,
+// the scheduler places each read right before its MFMA and waits for it there.
+template <int N, int A>
+__device__ __forceinline__ void read_ahead() {
+  __builtin_amdgcn_sched_group_barrier(0x100, A, 0);  // 0x100: LDS reads
+#pragma unroll
+  for (int i = 0; i < N - A; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 0x008: MFMA
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+  }
+  __builtin_amdgcn_sched_group_barrier(0x008, A, 0);
+}
+
 }  // namespace
 }  // namespace attn
 }  // namespace rh3

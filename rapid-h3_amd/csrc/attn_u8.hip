@@ -484,6 +484,7 @@ __global__ void __launch_bounds__(U8_NT, 1) attn_u8_kernel(const U8Args a) {
         const v4i kf = *reinterpret_cast<lds_v4i_u8*>(static_cast<uintptr_t>(ka[ds ^ (2 * (kb & 1))] + kb * 4096));
         s[kb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf, qf[ds], ds == 0 ? magic : s[kb], 0, 0, 0);
       }
+    read_ahead<16, 3>();
   };
 
   auto softmax_pv = [&](const int j) __attribute__((always_inline)) {
