@@ -115,33 +115,6 @@ __device__ __forceinline__ int max_halves(int v) {
   return max(static_cast<int>(r[0]), static_cast<int>(r[1]));
 }
 
-// Global -> LDS copy of 16 bytes per lane: lane l of the wave writes LDS byte offset lds_base + 16*l
-// (M0 holds the wave-uniform base). Issued from inline assembly so that the compiler adds no wait of
-// its own for it: the calling kernel accounts for these loads itself (s_waitcnt vmcnt) and issues no
-// other vector-memory loads while they are in flight. M0 is a reserved register, so the statement
-// restores the value it found; gfx9 requires one wait state between writing M0 and an LDS DMA that
-// reads it.
-__device__ __forceinline__ void lds_dma16(const void* gptr, uint32_t lds_base) {
-  uint32_t saved;
-  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off\n\t"
-               "s_nop 0\n\ts_mov_b32 m0, %0"
-               : "=&s"(saved)
-               : "v"(gptr), "s"(lds_base)
-               : "memory");
-}
-
-// The same copy addressed as a wave-uniform 64-bit base in SGPRs plus a 32-bit per-lane byte offset (the
-// saddr form): a kernel that walks a tile sequence advances the base with scalar adds and keeps the lane
-// offsets fixed, so the per-step address arithmetic costs no vector instructions.
-__device__ __forceinline__ void lds_dma16_s(const void* sbase, uint32_t voff, uint32_t lds_base) {
-  uint32_t saved;
-  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2\n\t"
-               "s_nop 0\n\ts_mov_b32 m0, %0"
-               : "=&s"(saved)
-               : "v"(voff), "s"(sbase), "s"(lds_base)
-               : "memory");
-}
-
 // Issue order of a run of N (LDS read, MFMA) pairs: the first A reads, then each MFMA followed by the next read,
 // then the last A MFMAs, so that every operand is read A MFMAs (>= 32 A pipe cycles) before its use. Left alone,
 // the scheduler places each read right before its MFMA and waits for it there.

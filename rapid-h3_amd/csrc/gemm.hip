@@ -671,12 +671,15 @@ __global__ void __launch_bounds__(512, 2) gemm_persistent_kernel(const GemmArgs 
     }
   };
   const int nk = static_cast<int>(a.K / BK);
+  // the saddr form: the tile base + k0 in scalar registers, the lane offsets fixed (no vector address arithmetic)
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
   auto gload = [&](int kt, int8_t* stg) __attribute__((always_inline)) {
     const int64_t k0 = static_cast<int64_t>(kt) * BK;
+    const uint32_t dst = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(stg)) + NL * wv * 1024;
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
-      __builtin_amdgcn_global_load_lds(xb + k0 + xo[i], stg + (NL * wave + i) * 1024, 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(wb + k0 + wo[i], stg + TILE_BYTES + (NL * wave + i) * 1024, 16, 0, 0);
+      lds_dma16_s(xb + k0, xo[i], dst + i * 1024);
+      lds_dma16_s(wb + k0, wo[i], dst + TILE_BYTES + i * 1024);
     }
   };
 
@@ -713,14 +716,27 @@ __global__ void __launch_bounds__(512, 2) gemm_persistent_kernel(const GemmArgs 
   };
   // one k-step reading stage cur, after first loading k-step kload of the current pointers into nxt3 (the
   // stage of the previous k-step, whose readers all passed the previous barrier); as in gemm_kernel
+  // issue order of a half step (int8): one MFMA, then each of the 6 fragment reads of the other half followed
+  // by an MFMA, then the last one, so that the reads go out under the MFMAs instead of after them
+  auto interleave = [&]() __attribute__((always_inline)) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);    // 0x008: MFMA
+#pragma unroll
+    for (int i = 0; i < TI + TJ; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 0x100: LDS read
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, TI * TJ - TI - TJ - 1, 0);
+  };
   auto step = [&](const int kload, const int8_t* cur, const int8_t* nxt1, int8_t* nxt3) __attribute__((always_inline)) {
     gload(kload, nxt3);
     if constexpr (MM::KSUB == 2) {
       load_frags(cur, 1, fa1, fb1);
       mma_all(fa0, fb0);
+      interleave();
       sync_next();
       load_frags(nxt1, 0, fa0, fb0);
       mma_all(fa1, fb1);
+      interleave();
     } else {
       load_frags(cur, 0, fa1, fb1);
       mma_all(fa1, fb1);
