@@ -82,9 +82,11 @@ __device__ __forceinline__ float rint_div(float x, float s, float inv) {
   return n;
 }
 
-// 8 int8 codes clamp(rint(x[e] / s), -127, 127) packed little-endian into two words: the multiply by
-// inv = 1/s decides every lane except those within 2^-12 of a half-integer, and one wave-wide vote per
-// 8 values sends only those through the IEEE division (bit-identical to rint_div element by element).
+// 8 int8 codes rint(x[e] / s) packed little-endian into two words: the multiply by inv = 1/s decides every lane
+// except those within 2^-12 of a half-integer, and one wave-wide vote per 8 values sends only those through the
+// IEEE division (bit-identical to rint_div element by element). The callers' scales are max(amax / 127, floor)
+// with amax = max|x|, so |x / s| <= 127 (1 + 2^-23) and every code lies in [-127, 127] without a clamp; the
+// code n then becomes the low byte of the float bits of n + 1.5 * 2^23 (exact), packed by byte permutes.
 __device__ __forceinline__ uint2 quant8_i8(const float* x, float s, float inv) {
   float n[8];
   bool need = false;
@@ -103,20 +105,42 @@ __device__ __forceinline__ uint2 quant8_i8(const float* x, float s, float inv) {
   }
   uint32_t b[8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) b[e] = static_cast<uint32_t>(static_cast<int32_t>(fminf(fmaxf(n[e], -127.0f), 127.0f))) & 0xffu;
-  return make_uint2(b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24), b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24));
+  for (int e = 0; e < 8; ++e) b[e] = __float_as_uint(n[e] + 12582912.0f);
+  return make_uint2(__builtin_amdgcn_perm(b[1], b[0], 0x0c0c0400u) | __builtin_amdgcn_perm(b[3], b[2], 0x04000c0cu),
+                    __builtin_amdgcn_perm(b[5], b[4], 0x0c0c0400u) | __builtin_amdgcn_perm(b[7], b[6], 0x04000c0cu));
 }
 
 // ---------------------------------------------------------------- device: wavefront reductions
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+// Butterflies over lane distances 32, 16, ..., 1: at distance d every lane combines its value with lane l ^ d's.
+// The partners come from VALU lane moves, not the LDS crossbar: v_permlane32_swap / v_permlane16_swap (the two
+// halves of the result are a lane's own value and its partner's), DPP row_ror:8 (l ^ 8 within a 16-lane row),
+// row_half_mirror then quad_perm [3,2,1,0] (l ^ 7, then ^ 3: l ^ 4), quad_perm [2,3,0,1] (l ^ 2) and
+// [1,0,3,2] (l ^ 1). The additions pair the same lanes as the shuffle butterfly, so the sums keep its bits.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, true));
+}
+template <typename Op>
+__device__ __forceinline__ float wave_butterfly(float v, Op op) {
+  {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_int(v), __float_as_int(v), false, false);
+    v = op(__int_as_float(r[0]), __int_as_float(r[1]));
+  }
+  {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_int(v), __float_as_int(v), false, false);
+    v = op(__int_as_float(r[0]), __int_as_float(r[1]));
+  }
+  v = op(v, dpp_mov<0x128>(v));                   // row_ror:8
+  v = op(v, dpp_mov<0x1B>(dpp_mov<0x141>(v)));    // row_half_mirror, quad_perm [3,2,1,0]
+  v = op(v, dpp_mov<0x4E>(v));                    // quad_perm [2,3,0,1]
+  v = op(v, dpp_mov<0xB1>(v));                    // quad_perm [1,0,3,2]
   return v;
 }
-__device__ __forceinline__ float wave_sum_tree(float v) {  // lane distances 32, 16, ..., 1 (fixed order)
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v = v + __shfl_xor(v, o, 64);
-  return v;
+__device__ __forceinline__ float wave_max(float v) {
+  return wave_butterfly(v, [](float a, float b) { return fmaxf(a, b); });
+}
+__device__ __forceinline__ float wave_sum_tree(float v) {  // lane distances 32, 16, ..., 1 (fixed pairing)
+  return wave_butterfly(v, [](float a, float b) { return a + b; });
 }
 
 // ---------------------------------------------------------------- device: global -> LDS copies
