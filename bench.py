@@ -310,6 +310,33 @@ def traffic_probe(m):
     print(f"traffic probe: attn_fwd_kernel S={m} H={HEADS} D={D}; copy 1073741824 B", flush=True)
 
 
+def quant_probe(m, recipe):
+    """Workload of the rocprofv3 passes behind profiles/quant_traffic.md: each activation quantizer of one block
+    three times at the bench shape (RMSNorm + modulation of x [m, hidden], the head-major attention output [H, m, 128],
+    the FFN hidden h [m, FFN]), then the plain 2^30-byte device copy that calibrates FETCH_SIZE / WRITE_SIZE."""
+    import torch
+    from rapid_h3.block import _QUANTIZERS, row_index
+    dev = torch.device("cuda:0")
+    x, w, mod, segments, _ = setup(m, dev, recipe)
+    norm_mod_q, heads_q, rows_q = _QUANTIZERS[recipe]
+    idx = row_index(segments, m, dev)
+    g = torch.Generator(device=dev).manual_seed(1)
+    o = torch.randn(HEADS, m, D, generator=g, device=dev).to(torch.bfloat16)
+    hh = torch.randn(m, FFN, generator=g, device=dev).to(torch.bfloat16)
+    src = torch.ones(2 ** 29, dtype=torch.bfloat16, device=dev)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        norm_mod_q(x, w.norm1_w, w.eps, idx, mod[0], mod[1])
+        heads_q(o)
+        rows_q(hh)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    print(f"quant probe: norm+mod [{m}, {HIDDEN}], heads [{HEADS}, {m}, {D}], rows [{m}, {FFN}] ({recipe}); "
+          "copy 1073741824 B", flush=True)
+
+
 def pmc_summary(path):
     """Per-kernel table of a rocprofv3 --pmc counter CSV (pmc_counter_collection.csv) holding GRBM_GUI_ACTIVE and
     SQ_VALU_MFMA_BUSY_CYCLES: average duration, the shader clock the kernel ran at (GRBM_GUI_ACTIVE sums one
@@ -366,6 +393,8 @@ def main():
     ap.add_argument("--fuse-qkv", type=int, default=None, choices=(0, 1),
                     help="1: the QKV GEMM epilogue writes the attention's Q operands and K/V statistics "
                          "(gemm.int8_gemm_qkv); 0: plain QKV GEMM + the full pre-pass; default: the block's")
+    ap.add_argument("--quant-probe", action="store_true",
+                    help="run only the block's three activation quantizers + a 1 GiB copy (workload of the --pmc passes)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="run only the attention kernel + a 1 GiB copy (workload of the --pmc passes)")
     a = ap.parse_args()
@@ -379,6 +408,9 @@ def main():
         a.tokens = m_default
     if a.traffic_probe:
         traffic_probe(a.tokens)
+        return
+    if a.quant_probe:
+        quant_probe(a.tokens, a.recipe)
         return
     import torch
     from rapid_h3.block import PHASES, fused_block

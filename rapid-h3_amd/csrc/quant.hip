@@ -165,12 +165,16 @@ __global__ void __launch_bounds__(256) quant_rows_kernel(const QuantArgs a) {
     }
   }
   float amax = 0.0f;
+  if constexpr (RAW) {  // on the raw bf16 words: magnitude bits, two per 32-bit lane
+    uint32_t m2 = 0;
 #pragma unroll
-  for (int j = 0; j < NCH; ++j) {
-    float x[8];
-    vals(j, x);
+    for (int j = 0; j < NCH; ++j) m2 = absmax8_bf16(m2, raw[j]);
+    amax = amax_of_pair(m2);
+  } else {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(x[e]));
+    for (int j = 0; j < NCH; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) amax = max3_abs(amax, v[j][e], v[j][e + 1]);
   }
   amax = wave_max(amax);
   if (RAW) {
@@ -210,10 +214,10 @@ __global__ void __launch_bounds__(256) quant_rows_kernel(const QuantArgs a) {
 constexpr int NM_RPW = 8;
 template <int NCH, typename TabT>
 __global__ void __launch_bounds__(256) quant_normmod_lds_kernel(const QuantArgs a) {
-  extern __shared__ float4 nm_lds[];   // [K/4] scale, [K/4] shift, [K/8] weight (bf16 x 8 per uint4)
+  extern __shared__ float4 nm_lds[];   // [K] 1 + scale, [K] shift, [K] weight (fp32)
   float* sc_s = reinterpret_cast<float*>(nm_lds);
   float* sh_s = sc_s + a.K;
-  uint16_t* w_s = reinterpret_cast<uint16_t*>(sh_s + a.K);
+  float* w_s = sh_s + a.K;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t r0 = static_cast<int64_t>(blockIdx.x) * 4 * NM_RPW;
   const int32_t idx0 = a.idx[r0];
@@ -225,8 +229,14 @@ __global__ void __launch_bounds__(256) quant_normmod_lds_kernel(const QuantArgs 
       sh_s[c + e] = tab_load<TabT>(a.shift, t0 + c + e);
     }
   }
-  for (int64_t c = threadIdx.x * 8; c < a.K; c += 256 * 8)
-    *reinterpret_cast<uint4*>(w_s + c) = a.w ? *reinterpret_cast<const uint4*>(a.w + c) : make_uint4(0, 0, 0, 0);
+  // without a weight the staged row is 1.0 (x * 1 is x exactly), so the row loop multiplies unconditionally
+  for (int64_t c = threadIdx.x * 8; c < a.K; c += 256 * 8) {
+    float wv[8] = {1, 1, 1, 1, 1, 1, 1, 1};
+    if (a.w) unpack8(*reinterpret_cast<const uint4*>(a.w + c), wv);
+    float4* d = reinterpret_cast<float4*>(w_s + c);
+    d[0] = make_float4(wv[0], wv[1], wv[2], wv[3]);
+    d[1] = make_float4(wv[4], wv[5], wv[6], wv[7]);
+  }
   auto load_raw = [&](int64_t m, uint4* raw) __attribute__((always_inline)) {
 #pragma unroll
     for (int j = 0; j < NCH; ++j) {
@@ -261,7 +271,11 @@ __global__ void __launch_bounds__(256) quant_normmod_lds_kernel(const QuantArgs 
       const int64_t c = 512 * j + 8 * lane;
       if (c < a.K) {
         float wv[8], sc[8], sh[8];
-        if (a.w) unpack8(*reinterpret_cast<const uint4*>(w_s + c), wv);
+        {
+          const float4* pw = reinterpret_cast<const float4*>(w_s + c);
+          const float4 w0 = pw[0], w1 = pw[1];
+          wv[0] = w0.x; wv[1] = w0.y; wv[2] = w0.z; wv[3] = w0.w; wv[4] = w1.x; wv[5] = w1.y; wv[6] = w1.z; wv[7] = w1.w;
+        }
         if (im == idx0) {
           const float4* ps = reinterpret_cast<const float4*>(sc_s + c);
           const float4* ph = reinterpret_cast<const float4*>(sh_s + c);
@@ -278,7 +292,7 @@ __global__ void __launch_bounds__(256) quant_normmod_lds_kernel(const QuantArgs 
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           float y = v[j][e] * rstd;
-          if (a.w) y = y * wv[e];
+          y = y * wv[e];
           v[j][e] = y * sc[e] + sh[e];
         }
       }
@@ -287,7 +301,7 @@ __global__ void __launch_bounds__(256) quant_normmod_lds_kernel(const QuantArgs 
 #pragma unroll
     for (int j = 0; j < NCH; ++j)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[j][e]));
+      for (int e = 0; e < 8; e += 2) amax = max3_abs(amax, v[j][e], v[j][e + 1]);
     amax = wave_max(amax);
     const float s = fmaxf(amax / 127.0f, 1e-12f);
     const float inv = 1.0f / s;
@@ -402,15 +416,10 @@ __global__ void __launch_bounds__(256) quant_rows_split_kernel(const QuantArgs a
     const int64_t c = 512 * (4 * i + wave) + 8 * lane;
     raw[i] = c < a.K ? ld_stream16(a.x + m * a.ldx + c) : make_uint4(0, 0, 0, 0);
   }
-  float amax = 0.0f;
+  uint32_t m2 = 0;  // on the raw bf16 words: magnitude bits, two per 32-bit lane
 #pragma unroll
-  for (int i = 0; i < NCHW; ++i) {
-    float x[8];
-    unpack8(raw[i], x);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(x[e]));
-  }
-  amax = wave_max(amax);
+  for (int i = 0; i < NCHW; ++i) m2 = absmax8_bf16(m2, raw[i]);
+  float amax = wave_max(amax_of_pair(m2));
   if (lane == 0) wmax[wave] = amax;
   // the raw words are unpacked again below rather than kept as floats
 #pragma unroll
@@ -450,10 +459,10 @@ int launch(const QuantArgs& a, hipStream_t st, const char* name) {
     else hipLaunchKernelGGL((quant_rows_split_kernel<8, FP8>), grid, block, 0, st, a);
     return launch_status(name);
   }
-  // up to 6144 columns the staged rows fit in 60 KB of LDS
+  // up to 6144 columns the staged table and weight rows fit in 72 KB of LDS
   if (KIND == KIND_NORMMOD && !FP8 && a.K <= 6144 && a.K % 8 == 0) {
     const dim3 grid(static_cast<unsigned>((a.M + 4 * NM_RPW - 1) / (4 * NM_RPW))), block(256);
-    const size_t lds = static_cast<size_t>(a.K) * (4 + 4 + 2);
+    const size_t lds = static_cast<size_t>(a.K) * (4 + 4 + 4);
     const int64_t nch = (a.K + 511) / 512;
     if (nch <= 2) hipLaunchKernelGGL((quant_normmod_lds_kernel<2, TabT>), grid, block, lds, st, a);
     else if (nch <= 4) hipLaunchKernelGGL((quant_normmod_lds_kernel<4, TabT>), grid, block, lds, st, a);

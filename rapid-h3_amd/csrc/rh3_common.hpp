@@ -120,6 +120,32 @@ template <int CTRL>
 __device__ __forceinline__ float dpp_mov(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, true));
 }
+// max(a, b) and max(m, |a|, |b|) as single instructions: fmaxf in the kernels' IEEE mode first quiets each operand
+// (an extra v_max per operand), which finite values do not need
+__device__ __forceinline__ float fmax_nc(float a, float b) {
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+__device__ __forceinline__ float max3_abs(float m, float a, float b) {
+  float r;
+  asm("v_max3_f32 %0, %1, |%2|, |%3|" : "=v"(r) : "v"(m), "v"(a), "v"(b));
+  return r;
+}
+// running max of |x| over 8 bf16 held as raw words: the magnitude bits (sign cleared) order like the values, so
+// two 16-bit integer maxima per word track both halves (m2 holds two bf16 magnitudes); amax_of_pair gives the float
+__device__ __forceinline__ uint32_t absmax8_bf16(uint32_t m2, const uint4 r) {
+  typedef short v2s __attribute__((ext_vector_type(2)));
+  const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    m2 = __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(v2s, m2), __builtin_bit_cast(v2s, w[i] & 0x7fff7fffu)));
+  return m2;
+}
+__device__ __forceinline__ float amax_of_pair(uint32_t m2) {
+  return __uint_as_float((m2 > (m2 << 16) ? m2 : m2 << 16) & 0xffff0000u);
+}
+
 template <typename Op>
 __device__ __forceinline__ float wave_butterfly(float v, Op op) {
   {
@@ -137,7 +163,7 @@ __device__ __forceinline__ float wave_butterfly(float v, Op op) {
   return v;
 }
 __device__ __forceinline__ float wave_max(float v) {
-  return wave_butterfly(v, [](float a, float b) { return fmaxf(a, b); });
+  return wave_butterfly(v, [](float a, float b) { return fmax_nc(a, b); });
 }
 __device__ __forceinline__ float wave_sum_tree(float v) {  // lane distances 32, 16, ..., 1 (fixed pairing)
   return wave_butterfly(v, [](float a, float b) { return a + b; });
