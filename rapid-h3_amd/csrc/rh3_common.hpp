@@ -82,34 +82,6 @@ __device__ __forceinline__ float rint_div(float x, float s, float inv) {
   return n;
 }
 
-// 8 int8 codes rint(x[e] / s) packed little-endian into two words: the multiply by inv = 1/s decides every lane
-// except those within 2^-12 of a half-integer, and one wave-wide vote per 8 values sends only those through the
-// IEEE division (bit-identical to rint_div element by element). The callers' scales are max(amax / 127, floor)
-// with amax = max|x|, so |x / s| <= 127 (1 + 2^-23) and every code lies in [-127, 127] without a clamp; the
-// code n then becomes the low byte of the float bits of n + 1.5 * 2^23 (exact), packed by byte permutes.
-__device__ __forceinline__ uint2 quant8_i8(const float* x, float s, float inv) {
-  float n[8];
-  bool need = false;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const float t = x[e] * inv;
-    n[e] = rintf(t);
-    need |= fabsf(t - n[e]) > 0.5f - 0x1p-12f;
-  }
-  if (__builtin_amdgcn_ballot_w64(need) != 0) {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float t = x[e] * inv;
-      if (fabsf(t - n[e]) > 0.5f - 0x1p-12f) n[e] = rintf(x[e] / s);
-    }
-  }
-  uint32_t b[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) b[e] = __float_as_uint(n[e] + 12582912.0f);
-  return make_uint2(__builtin_amdgcn_perm(b[1], b[0], 0x0c0c0400u) | __builtin_amdgcn_perm(b[3], b[2], 0x04000c0cu),
-                    __builtin_amdgcn_perm(b[5], b[4], 0x0c0c0400u) | __builtin_amdgcn_perm(b[7], b[6], 0x04000c0cu));
-}
-
 // ---------------------------------------------------------------- device: wavefront reductions
 // Butterflies over lane distances 32, 16, ..., 1: at distance d every lane combines its value with lane l ^ d's.
 // The partners come from VALU lane moves, not the LDS crossbar: v_permlane32_swap / v_permlane16_swap (the two
@@ -132,6 +104,37 @@ __device__ __forceinline__ float max3_abs(float m, float a, float b) {
   asm("v_max3_f32 %0, %1, |%2|, |%3|" : "=v"(r) : "v"(m), "v"(a), "v"(b));
   return r;
 }
+// 8 int8 codes rint(x[e] / s) packed little-endian into two words. The callers' scales are max(amax / 127, floor)
+// with amax = max|x|, so |x / s| <= 127 (1 + 2^-23) < 128: every code lies in [-127, 127] without a clamp. The
+// product t = x * inv (inv = 1/s) is within 2^-16 of the quotient x / s and the IEEE quotient within 2^-17 of it, so
+// rint(t) equals rint(fp32(x / s)) unless t lies within 2^-15 of a half-integer: one wave-wide vote per 8 values (on
+// the largest |t - rint(t)|, flagged past 0.5 - 2^-14) sends only those lanes through the IEEE division, which makes
+// the codes bit-identical to rint_div element by element. A code n becomes the low byte of the float bits of
+// n + 1.5 * 2^23 (exact), and byte permutes pack four per word.
+__device__ __forceinline__ uint2 quant8_i8(const float* x, float s, float inv) {
+  constexpr float NEAR_TIE = 0.5f - 0x1p-14f;
+  float n[8], d = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 8; e += 2) {
+    const float t0 = x[e] * inv, t1 = x[e + 1] * inv;
+    n[e] = rintf(t0);
+    n[e + 1] = rintf(t1);
+    d = max3_abs(d, t0 - n[e], t1 - n[e + 1]);
+  }
+  if (__builtin_amdgcn_ballot_w64(d > NEAR_TIE) != 0) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float t = x[e] * inv;
+      if (fabsf(t - n[e]) > NEAR_TIE) n[e] = rintf(x[e] / s);
+    }
+  }
+  uint32_t b[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) b[e] = __float_as_uint(n[e] + 12582912.0f);
+  return make_uint2(__builtin_amdgcn_perm(b[1], b[0], 0x0c0c0400u) | __builtin_amdgcn_perm(b[3], b[2], 0x04000c0cu),
+                    __builtin_amdgcn_perm(b[5], b[4], 0x0c0c0400u) | __builtin_amdgcn_perm(b[7], b[6], 0x04000c0cu));
+}
+
 // running max of |x| over 8 bf16 held as raw words: the magnitude bits (sign cleared) order like the values, so
 // two 16-bit integer maxima per word track both halves (m2 holds two bf16 magnitudes); amax_of_pair gives the float
 __device__ __forceinline__ uint32_t absmax8_bf16(uint32_t m2, const uint4 r) {
