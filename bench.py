@@ -279,6 +279,45 @@ def gemm_side_measurements(m, device, reps=5):
     return fp8, vendor
 
 
+def h3_side_measurements(device, recipe, tokens=(22332, 44992)):
+    """One DiT block at MiniMax-H3's own shapes (hidden 5376, 56 x 128 heads, FFN 14336; the shapes of the
+    reference's published numbers) for each token count: 1 untimed block, then 1 block timed per phase with
+    events on torch's current stream. Runs after the metric's timed region, on fresh synthetic inputs."""
+    import torch
+    from rapid_h3.block import PHASES, fused_block
+    global HIDDEN, HEADS, FFN
+    saved = (HIDDEN, HEADS, FFN)
+    HIDDEN, HEADS, FFN, _ = MODELS["h3"]
+    res = {}
+    try:
+        for m in tokens:
+            x, w, mod, segments, tab = setup(m, device, recipe)
+            fused_block(x, w, mod, segments, tab)
+            torch.cuda.synchronize()
+            ev = []
+
+            def mark(name):
+                e = torch.cuda.Event(enable_timing=True)
+                e.record()
+                ev.append((name, e))
+            b = torch.cuda.Event(enable_timing=True)
+            b.record()
+            ev.append(("begin", b))
+            fused_block(x, w, mod, segments, tab, mark=mark)
+            torch.cuda.synchronize()
+            ph = {name: round(e0.elapsed_time(e1), 3) for (_, e0), (name, e1) in zip(ev[:-1], ev[1:])}
+            gemms, attn_ops = block_ops(m)
+            gms = sum(ph[k] for k in gemms)
+            res[str(m)] = {"ms_per_block": round(sum(ph.values()), 3), "phases_ms": ph,
+                           "gemm_tops": round(sum(gemms.values()) / (gms * 1e-3) / 1e12, 1),
+                           "attn_tops": round(attn_ops / (ph["attn_main"] * 1e-3) / 1e12, 1)}
+            del x, w, mod, tab
+            torch.cuda.empty_cache()
+    finally:
+        HIDDEN, HEADS, FFN = saved
+    return res
+
+
 def traffic_from_profile():
     """HBM bytes per launch of the attention main kernel from the committed rocprofv3 --pmc summary
     (FETCH_SIZE + WRITE_SIZE, calibrated against a copy kernel), or None if there is none."""
@@ -384,7 +423,8 @@ def main():
                     help="c2: hidden 3072, 24 heads, FFN 8192 (the metric's); h3: 5376, 56, 14336")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-side", action="store_true",
-                    help="skip the C3 FP8 GEMMs and the hipBLASLt int8 GEMM comparison after the timed block")
+                    help="skip the C3 FP8 GEMMs, the hipBLASLt int8 GEMM comparison and the MiniMax-H3-shape blocks after "
+                         "the timed block")
     ap.add_argument("--recipe", default="int8_rowwise", choices=("int8_rowwise", "int8_rot"),
                     help="int8_rowwise (the configuration the metric names) or the reference's int8_rot")
     ap.add_argument("--attn-config", type=int, default=None,
@@ -505,6 +545,7 @@ def main():
         fp8, vendor = gemm_side_measurements(m, dev)
         out["fp8_gemm_c3"] = fp8
         out["int8_gemm_vs_hipblaslt"] = vendor
+        out["h3_shapes"] = h3_side_measurements(dev, a.recipe)
     if not a.no_cpu:
         # one traced run of the same block supplies the intermediate tensors the CPU sample starts from
         x_in = x.clone()
