@@ -602,6 +602,15 @@ __global__ void __launch_bounds__(U8_NT, 1) attn_u8_kernel(const U8Args a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) o[db][r] = fmaf(ts, __int_as_float(acc[r]), fmaf(o[db][r], al, nm));
     }
+    // issue order: 8 of the 32 LDS reads (per block: 4 accumulator starts, 4 V^T fragments) first, then each
+    // P.V MFMA followed by two more reads, so the reads run ahead of the MFMAs that consume them
+    __builtin_amdgcn_sched_group_barrier(0x100, 8, 1);  // 0x100: LDS reads
+#pragma unroll
+    for (int i = 0; i < 12; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);  // 0x008: MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 4, 1);
   };
 
   auto softmax_pv_f8 = [&](const int j) __attribute__((always_inline)) {
