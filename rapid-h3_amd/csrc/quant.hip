@@ -209,7 +209,7 @@ __global__ void __launch_bounds__(256) quant_rows_kernel(const QuantArgs a) {
 
 // KIND_NORMMOD with the modulation rows and the norm weight staged in LDS: every token of a segment reads
 // the same table row, so a workgroup copies the row of its first token once (as fp32, plus the weight) and
-// each wavefront then quantizes RPW rows from LDS; a row with another table index reads its values from
+// each wavefront then quantizes NM_RPW rows from LDS; a row with another table index reads its values from
 // global memory. Same arithmetic and order as quant_rows_kernel<NCH, KIND_NORMMOD>.
 constexpr int NM_RPW = 8;
 template <int NCH, typename TabT>
@@ -220,8 +220,8 @@ __global__ void __launch_bounds__(256) quant_normmod_lds_kernel(const QuantArgs 
   float* w_s = sh_s + a.K;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t r0 = static_cast<int64_t>(blockIdx.x) * 4 * NM_RPW;
-  const int32_t idx0 = a.idx[r0];
-  const int64_t t0 = static_cast<int64_t>(idx0) * a.ld_tab;
+  const int32_t staged = __builtin_amdgcn_readfirstlane(a.idx[r0]);
+  const int64_t t0 = static_cast<int64_t>(staged) * a.ld_tab;
   for (int64_t c = threadIdx.x * 4; c < a.K; c += 256 * 4) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -237,26 +237,31 @@ __global__ void __launch_bounds__(256) quant_normmod_lds_kernel(const QuantArgs 
     d[0] = make_float4(wv[0], wv[1], wv[2], wv[3]);
     d[1] = make_float4(wv[4], wv[5], wv[6], wv[7]);
   }
-  auto load_raw = [&](int64_t m, uint4* raw) __attribute__((always_inline)) {
+  // Row loads and code stores go through a buffer resource per row (base = the row, size = its K elements, 0 for a
+  // row past M or a load not wanted): lanes past the row end read zeros and their stores are dropped by the
+  // hardware's range check, so neither needs a branch, and the lane offsets stay fixed (no per-row vector address
+  // arithmetic). Every row issues its successor's load, so the loop carries the row registers without copies.
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
+  auto load_raw = [&](int64_t m, uint4* raw, bool want) __attribute__((always_inline)) {
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(a.x + m * a.ldx), 0, want && m < a.M ? static_cast<int>(a.K * 2) : 0, BUF_RSRC_WORD3);
 #pragma unroll
     for (int j = 0; j < NCH; ++j) {
-      const int64_t c = 512 * j + 8 * lane;
-      raw[j] = c < a.K ? ld_stream16(a.x + m * a.ldx + c) : make_uint4(0, 0, 0, 0);
+      const u32x4_t t = __builtin_amdgcn_raw_buffer_load_b128(r, lane * 16 + j * 1024, 0, BUF_NT);
+      raw[j] = make_uint4(t[0], t[1], t[2], t[3]);
     }
   };
   uint4 raw[NCH];
-  load_raw(r0 + wave < a.M ? r0 + wave : a.M - 1, raw);
+  load_raw(r0 + wv, raw, true);
   __syncthreads();
   for (int i = 0; i < NM_RPW; ++i) {
-    const int64_t m = r0 + static_cast<int64_t>(i) * 4 + wave;
+    const int64_t m = r0 + static_cast<int64_t>(i) * 4 + wv;
     if (m >= a.M) break;
     float v[NCH][8];
 #pragma unroll
     for (int j = 0; j < NCH; ++j) unpack8(raw[j], v[j]);
-    if (i + 1 < NM_RPW) {  // the wavefront's next row is in flight while this one is reduced and written
-      const int64_t mn = m + 4;
-      load_raw(mn < a.M ? mn : a.M - 1, raw);
-    }
+    // the next row is in flight while this one is reduced and written (the last row's load reads nothing)
+    load_raw(m + 4, raw, i + 1 < NM_RPW);
     float ss = 0.0f;
 #pragma unroll
     for (int j = 0; j < NCH; ++j)
@@ -264,7 +269,7 @@ __global__ void __launch_bounds__(256) quant_normmod_lds_kernel(const QuantArgs 
       for (int e = 0; e < 8; ++e) ss = fmaf(v[j][e], v[j][e], ss);  // x*x exact (bf16 x): same as ss + x*x
     ss = wave_sum_tree(ss);
     const float rstd = 1.0f / sqrtf(ss / static_cast<float>(a.K) + a.eps);
-    const int32_t im = a.idx[m];
+    const int32_t im = __builtin_amdgcn_readfirstlane(a.idx[m]);   // one table row per token: wave-uniform
     const int64_t t = static_cast<int64_t>(im) * a.ld_tab;
 #pragma unroll
     for (int j = 0; j < NCH; ++j) {
@@ -276,7 +281,7 @@ __global__ void __launch_bounds__(256) quant_normmod_lds_kernel(const QuantArgs 
           const float4 w0 = pw[0], w1 = pw[1];
           wv[0] = w0.x; wv[1] = w0.y; wv[2] = w0.z; wv[3] = w0.w; wv[4] = w1.x; wv[5] = w1.y; wv[6] = w1.z; wv[7] = w1.w;
         }
-        if (im == idx0) {
+        if (im == staged) {
           const float4* ps = reinterpret_cast<const float4*>(sc_s + c);
           const float4* ph = reinterpret_cast<const float4*>(sh_s + c);
           const float4 s0 = ps[0], s1 = ps[1], h0 = ph[0], h1 = ph[1];
@@ -306,11 +311,13 @@ __global__ void __launch_bounds__(256) quant_normmod_lds_kernel(const QuantArgs 
     const float s = fmaxf(amax / 127.0f, 1e-12f);
     const float inv = 1.0f / s;
     if (lane == 0) a.s[m] = s;
+    const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(static_cast<int8_t*>(a.q) + m * a.ldq, 0,
+                                                                       static_cast<int>(a.K), BUF_RSRC_WORD3);
 #pragma unroll
     for (int j = 0; j < NCH; ++j) {
-      const int64_t c = 512 * j + 8 * lane;
-      if (c >= a.K) continue;
-      st_stream8(static_cast<int8_t*>(a.q) + m * a.ldq + c, quant8_i8(v[j], s, inv));
+      const uint2 c8 = quant8_i8(v[j], s, inv);
+      const u32x2_t t = {c8.x, c8.y};
+      __builtin_amdgcn_raw_buffer_store_b64(t, rq, lane * 8 + j * 512, 0, BUF_NT);
     }
   }
 }

@@ -61,6 +61,12 @@ __device__ __forceinline__ void st_stream8(void* p, uint2 v) {
   __builtin_nontemporal_store(t, reinterpret_cast<u32x2_t*>(p));
 }
 
+// Buffer-resource accesses: word 3 of a raw (stride 0) gfx9 buffer descriptor (32-bit data format), and the
+// nontemporal cache policy bit. A load whose byte offset (lane offset + immediate) lies at or past the
+// descriptor's size returns 0 and such a store is dropped, so a row's tail needs no branch.
+constexpr int BUF_RSRC_WORD3 = 0x00020000;
+constexpr int BUF_NT = 2;
+
 // 8 bf16 in a uint4 -> 8 floats
 __device__ __forceinline__ void unpack8(const uint4 r, float* v) {
   const uint32_t w[4] = {r.x, r.y, r.z, r.w};
@@ -122,10 +128,14 @@ __device__ __forceinline__ uint2 quant8_i8(const float* x, float s, float inv) {
     d = max3_abs(d, t0 - n[e], t1 - n[e + 1]);
   }
   if (__builtin_amdgcn_ballot_w64(d > NEAR_TIE) != 0) {
+    // s passes through an empty asm here so that the division's divisor-only steps stay on this rare path
+    // instead of being hoisted into the common one
+    float so = s;
+    asm volatile("" : "+v"(so));
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const float t = x[e] * inv;
-      if (fabsf(t - n[e]) > NEAR_TIE) n[e] = rintf(x[e] / s);
+      if (fabsf(t - n[e]) > NEAR_TIE) n[e] = rintf(x[e] / so);
     }
   }
   uint32_t b[8];

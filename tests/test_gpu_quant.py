@@ -74,6 +74,58 @@ def test_norm_mod_golden(dev, golden):
     del torch
 
 
+@pytest.mark.parametrize("m,k", [(1, 8), (7, 520), (33, 1032), (5, 3080), (70, 3072), (3, 5000), (2, 6144), (9, 6152)])
+def test_norm_mod_shapes(dev, m, k):
+    """Ragged K (a partial last 512-column chunk), M not a multiple of the rows a workgroup takes, and a padded
+    output whose padding bytes must stay untouched."""
+    import torch
+    from rapid_h3 import _native as nat
+    rng = np.random.default_rng(m * 977 + k)
+    x = _bf(rng.standard_normal((m, k)) * np.exp(rng.standard_normal((1, k))))
+    w = _bf(1.0 + 0.1 * rng.standard_normal(k))
+    idx = rng.integers(0, 3, m).astype(np.int32)
+    sh = (0.2 * rng.standard_normal((3, k))).astype(np.float32)
+    sc = (0.3 * rng.standard_normal((3, k))).astype(np.float32)
+    xt, it = to_dev(x, dev), to_dev(idx, dev)
+    for tab_bf in (False, True):
+        shv, scv = (_bf(sh), _bf(sc)) if tab_bf else (sh, sc)
+        st, ct = to_dev(shv, dev), to_dev(scv, dev)
+        for wt in (w, None):
+            eq, es = oq.norm_mod_quant_rows_i8(x, wt, 1e-6, idx, shv, scv)
+            ldq = k + 24
+            q = torch.full((m, ldq), 77, dtype=torch.int8, device=dev)
+            s = torch.empty(m, 1, dtype=torch.float32, device=dev)
+            wd = None if wt is None else to_dev(wt, dev)
+            nat.call("rh3_quant_norm_mod_i8", nat.ptr(xt), k, m, k, nat.ptr(wd), 1e-6, nat.ptr(it), nat.ptr(st),
+                     nat.ptr(ct), nat.RH3_DTYPE_BF16 if tab_bf else nat.RH3_DTYPE_F32, k, nat.ptr(q), ldq, nat.ptr(s),
+                     nat.stream(xt.device))
+            qn = to_np(q)
+            assert np.array_equal(qn[:, :k], eq), (m, k, tab_bf, wt is None)
+            assert np.array_equal(to_np(s), es), (m, k, tab_bf, wt is None)
+            assert (qn[:, k:] == 77).all(), (m, k, tab_bf, wt is None)
+    del torch
+
+
+@pytest.mark.parametrize("k", [64, 3072])
+def test_norm_mod_many_groups(dev, k):
+    """Segments of 4099 tokens on alternating table rows (row groups straddle segment ends, so a workgroup's staged
+    row is not every token's), scattered tokens of a fourth row, and more workgroups than the GPU holds at once."""
+    from rapid_h3 import quant
+    m = 90001 if k == 64 else 40003
+    rng = np.random.default_rng(k)
+    x = _bf(rng.standard_normal((m, k)))
+    idx = ((np.arange(m) // 4099) % 3).astype(np.int32)
+    idx[rng.integers(0, m, 200)] = 3
+    sh = (0.2 * rng.standard_normal((4, k))).astype(np.float32)
+    sc = (0.3 * rng.standard_normal((4, k))).astype(np.float32)
+    w = _bf(1.0 + 0.1 * rng.standard_normal(k))
+    q, s = quant.norm_mod_quant_rows_i8(to_dev(x, dev), to_dev(w, dev), 1e-6, to_dev(idx, dev), to_dev(sh, dev),
+                                        to_dev(sc, dev))
+    eq, es = oq.norm_mod_quant_rows_i8(x, w, 1e-6, idx, sh, sc)
+    assert np.array_equal(to_np(q), eq)
+    assert np.array_equal(to_np(s), es)
+
+
 def test_heads_golden(dev, golden):
     from rapid_h3 import quant
     g = golden("heads_swiglu")
