@@ -211,18 +211,21 @@ __global__ void __launch_bounds__(256) quant_rows_kernel(const QuantArgs a) {
 // the same table row, so a workgroup copies the row of its first token once (as fp32, plus the weight) and
 // each wavefront then quantizes NM_RPW rows from LDS; a row with another table index reads its values from
 // global memory. Same arithmetic and order as quant_rows_kernel<NCH, KIND_NORMMOD>.
-constexpr int NM_RPW = 8;
+constexpr int NM_RPW = 4, NM_WAVES = 4;
+static_assert(NM_RPW * NM_WAVES <= 64, "one lane per row of a workgroup holds the row's table index");
 template <int NCH, typename TabT>
-__global__ void __launch_bounds__(256) quant_normmod_lds_kernel(const QuantArgs a) {
+__global__ void __launch_bounds__(64 * NM_WAVES) quant_normmod_lds_kernel(const QuantArgs a) {
   extern __shared__ float4 nm_lds[];   // [K] 1 + scale, [K] shift, [K] weight (fp32)
   float* sc_s = reinterpret_cast<float*>(nm_lds);
   float* sh_s = sc_s + a.K;
   float* w_s = sh_s + a.K;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * 4 * NM_RPW;
-  const int32_t staged = __builtin_amdgcn_readfirstlane(a.idx[r0]);
+  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * NM_WAVES * NM_RPW;
+  // the table indices of the workgroup's rows, one per lane (read once, so no row waits on a load of its own)
+  const int32_t idx_rows = lane < NM_WAVES * NM_RPW && r0 + lane < a.M ? a.idx[r0 + lane] : 0;
+  const int32_t staged = __builtin_amdgcn_readfirstlane(idx_rows);
   const int64_t t0 = static_cast<int64_t>(staged) * a.ld_tab;
-  for (int64_t c = threadIdx.x * 4; c < a.K; c += 256 * 4) {
+  for (int64_t c = threadIdx.x * 4; c < a.K; c += 64 * NM_WAVES * 4) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       sc_s[c + e] = 1.0f + tab_load<TabT>(a.scale, t0 + c + e);  // the (1 + scale) of every token of the row
@@ -230,7 +233,7 @@ __global__ void __launch_bounds__(256) quant_normmod_lds_kernel(const QuantArgs 
     }
   }
   // without a weight the staged row is 1.0 (x * 1 is x exactly), so the row loop multiplies unconditionally
-  for (int64_t c = threadIdx.x * 8; c < a.K; c += 256 * 8) {
+  for (int64_t c = threadIdx.x * 8; c < a.K; c += 64 * NM_WAVES * 8) {
     float wv[8] = {1, 1, 1, 1, 1, 1, 1, 1};
     if (a.w) unpack8(*reinterpret_cast<const uint4*>(a.w + c), wv);
     float4* d = reinterpret_cast<float4*>(w_s + c);
@@ -255,13 +258,13 @@ __global__ void __launch_bounds__(256) quant_normmod_lds_kernel(const QuantArgs 
   load_raw(r0 + wv, raw, true);
   __syncthreads();
   for (int i = 0; i < NM_RPW; ++i) {
-    const int64_t m = r0 + static_cast<int64_t>(i) * 4 + wv;
+    const int64_t m = r0 + static_cast<int64_t>(i) * NM_WAVES + wv;
     if (m >= a.M) break;
     float v[NCH][8];
 #pragma unroll
     for (int j = 0; j < NCH; ++j) unpack8(raw[j], v[j]);
     // the next row is in flight while this one is reduced and written (the last row's load reads nothing)
-    load_raw(m + 4, raw, i + 1 < NM_RPW);
+    load_raw(m + NM_WAVES, raw, i + 1 < NM_RPW);
     float ss = 0.0f;
 #pragma unroll
     for (int j = 0; j < NCH; ++j)
@@ -269,7 +272,7 @@ __global__ void __launch_bounds__(256) quant_normmod_lds_kernel(const QuantArgs 
       for (int e = 0; e < 8; ++e) ss = fmaf(v[j][e], v[j][e], ss);  // x*x exact (bf16 x): same as ss + x*x
     ss = wave_sum_tree(ss);
     const float rstd = 1.0f / sqrtf(ss / static_cast<float>(a.K) + a.eps);
-    const int32_t im = __builtin_amdgcn_readfirstlane(a.idx[m]);   // one table row per token: wave-uniform
+    const int32_t im = __builtin_amdgcn_readlane(idx_rows, i * NM_WAVES + wv);
     const int64_t t = static_cast<int64_t>(im) * a.ld_tab;
 #pragma unroll
     for (int j = 0; j < NCH; ++j) {
@@ -468,7 +471,7 @@ int launch(const QuantArgs& a, hipStream_t st, const char* name) {
   }
   // up to 6144 columns the staged table and weight rows fit in 72 KB of LDS
   if (KIND == KIND_NORMMOD && !FP8 && a.K <= 6144 && a.K % 8 == 0) {
-    const dim3 grid(static_cast<unsigned>((a.M + 4 * NM_RPW - 1) / (4 * NM_RPW))), block(256);
+    const dim3 grid(static_cast<unsigned>((a.M + NM_WAVES * NM_RPW - 1) / (NM_WAVES * NM_RPW))), block(64 * NM_WAVES);
     const size_t lds = static_cast<size_t>(a.K) * (4 + 4 + 4);
     const int64_t nch = (a.K + 511) / 512;
     if (nch <= 2) hipLaunchKernelGGL((quant_normmod_lds_kernel<2, TabT>), grid, block, lds, st, a);

@@ -110,13 +110,31 @@ __device__ __forceinline__ float max3_abs(float m, float a, float b) {
   asm("v_max3_f32 %0, %1, |%2|, |%3|" : "=v"(r) : "v"(m), "v"(a), "v"(b));
   return r;
 }
+
+// Four integer-valued floats n in [-128, 127] -> their int8 codes packed in a word, low byte first. The float
+// n + 1.5 * 2^23 holds n's two's-complement byte in its low 8 bits (exact for |n| < 2^22); the SDWA form of that add
+// writes the low byte of its result straight into byte k of the word (dst_sel BYTE_k: the first pads the rest with
+// zeros, the others keep what is there), so the packing costs no permutes.
+__device__ __forceinline__ uint32_t pack4_codes(const float* n) {
+  const float magic = 12582912.0f;
+  uint32_t w;
+  asm("v_add_f32_sdwa %0, %1, %2 dst_sel:BYTE_0 dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:DWORD"
+      : "=v"(w) : "v"(n[0]), "s"(magic));
+  asm("v_add_f32_sdwa %0, %1, %2 dst_sel:BYTE_1 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD"
+      : "+v"(w) : "v"(n[1]), "s"(magic));
+  asm("v_add_f32_sdwa %0, %1, %2 dst_sel:BYTE_2 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD"
+      : "+v"(w) : "v"(n[2]), "s"(magic));
+  asm("v_add_f32_sdwa %0, %1, %2 dst_sel:BYTE_3 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD"
+      : "+v"(w) : "v"(n[3]), "s"(magic));
+  return w;
+}
+
 // 8 int8 codes rint(x[e] / s) packed little-endian into two words. The callers' scales are max(amax / 127, floor)
 // with amax = max|x|, so |x / s| <= 127 (1 + 2^-23) < 128: every code lies in [-127, 127] without a clamp. The
 // product t = x * inv (inv = 1/s) is within 2^-16 of the quotient x / s and the IEEE quotient within 2^-17 of it, so
 // rint(t) equals rint(fp32(x / s)) unless t lies within 2^-15 of a half-integer: one wave-wide vote per 8 values (on
 // the largest |t - rint(t)|, flagged past 0.5 - 2^-14) sends only those lanes through the IEEE division, which makes
-// the codes bit-identical to rint_div element by element. A code n becomes the low byte of the float bits of
-// n + 1.5 * 2^23 (exact), and byte permutes pack four per word.
+// the codes bit-identical to rint_div element by element; pack4_codes packs them.
 __device__ __forceinline__ uint2 quant8_i8(const float* x, float s, float inv) {
   constexpr float NEAR_TIE = 0.5f - 0x1p-14f;
   float n[8], d = 0.0f;
@@ -138,11 +156,7 @@ __device__ __forceinline__ uint2 quant8_i8(const float* x, float s, float inv) {
       if (fabsf(t - n[e]) > NEAR_TIE) n[e] = rintf(x[e] / so);
     }
   }
-  uint32_t b[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) b[e] = __float_as_uint(n[e] + 12582912.0f);
-  return make_uint2(__builtin_amdgcn_perm(b[1], b[0], 0x0c0c0400u) | __builtin_amdgcn_perm(b[3], b[2], 0x04000c0cu),
-                    __builtin_amdgcn_perm(b[5], b[4], 0x0c0c0400u) | __builtin_amdgcn_perm(b[7], b[6], 0x04000c0cu));
+  return make_uint2(pack4_codes(n), pack4_codes(n + 4));
 }
 
 // running max of |x| over 8 bf16 held as raw words: the magnitude bits (sign cleared) order like the values, so
