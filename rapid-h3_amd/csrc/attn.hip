@@ -167,8 +167,9 @@ struct FwdArgs {
   float scale_log2;
   int nqb;      // query blocks per head; (head, query block) id = h * nqb + qb (query blocks fastest)
   int nmain;    // workgroups 0 .. nmain-1 run ids 0 .. nmain-1 whole
-  int npair;    // workgroups nmain + i and nmain + npair + i run the two key halves of id nmain + i
+  int npair;    // items nmain + i and nmain + npair + i run the two key halves of id nmain + i
   float* tail;  // [2][npair][FWD_BQ][TAIL_ROW] fp32 partials of the split ids
+  int* ctr;     // work counter, zero at launch: a starting workgroup takes item ctr++
 };
 
 // a wave-uniform float (lane 0's value), held in an SGPR
@@ -472,16 +473,25 @@ __device__ __forceinline__ void fwd_body(const FwdArgs& a, const int bid, int8_t
   }
 }
 
-// One launch: the unsplit workgroups first, then the split halves, which take CUs as the last unsplit
-// workgroups finish. The LDS rings and scale table are declared once, shared by both bodies.
+// One launch over nmain + 2 npair items, the unsplit ids first, then the split halves (which take CUs as the last
+// unsplit items finish). A workgroup runs the item it takes from the work counter when it starts, not the one its
+// position names: the grid is dealt to the XCDs in fixed shares, and the XCDs run at different clocks (workgroup
+// times differ by up to 7 % between them), so fixed items would leave the fast XCDs idle while the slowest
+// finishes. The grid holds more workgroups than items; a fast XCD starts its queued workgroups sooner and takes
+// more items, and the workgroups that find the items gone return at once. The LDS rings and scale table are
+// declared once, shared by both bodies.
 __global__ void __launch_bounds__(FWD_NT, 1) attn_fwd_kernel(const FwdArgs a) {
   __shared__ __attribute__((aligned(16))) int8_t ring[NRING * (KSLOT + VSLOT)];
   __shared__ float2 kscale[4096];  // per-128-key-block (K scale, K scale x key-norm bound) of this head
-  const int bid = static_cast<int>(blockIdx.x);
-  if (bid < a.nmain)
-    fwd_body<false>(a, bid, ring, ring + NRING * KSLOT, kscale);
+  __shared__ int item_s;
+  if (threadIdx.x == 0) item_s = atomicAdd(a.ctr, 1);
+  __syncthreads();
+  const int item = __builtin_amdgcn_readfirstlane(item_s);
+  if (item >= a.nmain + 2 * a.npair) return;
+  if (item < a.nmain)
+    fwd_body<false>(a, item, ring, ring + NRING * KSLOT, kscale);
   else
-    fwd_body<true>(a, bid - a.nmain, ring, ring + NRING * KSLOT, kscale);
+    fwd_body<true>(a, item - a.nmain, ring, ring + NRING * KSLOT, kscale);
 }
 
 // Merge of the two key halves of a split workgroup: m = max(m0, m1), O = (O0 2^(m0-m) + O1 2^(m1-m)) / l with
@@ -560,7 +570,7 @@ int prepass(const uint16_t* q, int64_t q_ss, int64_t q_sh, const uint16_t* k, in
 int forward(const Work& w, int64_t Sq, int64_t Sk, int64_t H, float scale, uint16_t* out, int64_t o_ss,
             int64_t o_sh, hipStream_t st) {
   const int64_t nwg = attn_ws::fwd_blocks(Sq, H);
-  RH3_REQUIRE(nwg < (int64_t{1} << 31) / FWD_NT, "attention forward: %lld workgroups exceed the grid limit",
+  RH3_REQUIRE(nwg < (int64_t{1} << 30) / FWD_NT, "attention forward: %lld workgroups exceed the grid limit",
               (long long)nwg);
   const int nqb = static_cast<int>((Sq + FWD_BQ - 1) / FWD_BQ);
   // One workgroup per CU: the grid runs in rounds of `cus` workgroups. When the last round is at most half
@@ -578,8 +588,13 @@ int forward(const Work& w, int64_t Sq, int64_t Sk, int64_t H, float scale, uint1
                         ? static_cast<int>(last) : 0;
   const int nmain = static_cast<int>(nwg - npair);
   const FwdArgs f{w.q8, w.qs, w.k8, w.ks, w.kn, w.vt, out, o_ss, o_sh, Sq, Sk, pad(Sq), pad(Sk),
-                  scale * 1.4426950408889634f, nqb, nmain, npair, w.tail};
-  hipLaunchKernelGGL(attn_fwd_kernel, dim3(static_cast<uint32_t>(nmain + 2 * npair)), dim3(FWD_NT), 0, st, f);
+                  scale * 1.4426950408889634f, nqb, nmain, npair, w.tail, w.ctr};
+  // a quarter more workgroups than items: room for the fastest XCD to take a quarter more than its share
+  const int64_t items = nmain + 2 * static_cast<int64_t>(npair);
+  const int64_t grid = items + (items + 3) / 4;
+  // the counter is cleared by a fill kernel, not hipMemsetAsync, so the call stays safe inside a captured HIP graph
+  hipLaunchKernelGGL(zero_kernel, dim3(1), dim3(64), 0, st, reinterpret_cast<float*>(w.ctr), int64_t{1});
+  hipLaunchKernelGGL(attn_fwd_kernel, dim3(static_cast<uint32_t>(grid)), dim3(FWD_NT), 0, st, f);
   if (npair > 0)
     hipLaunchKernelGGL(attn_combine_kernel, dim3(npair, FWD_BQ / 16), dim3(256), 0, st, w.tail, npair, nmain, nqb, Sq,
                        out, o_ss, o_sh);

@@ -29,6 +29,7 @@ struct Work {
   int8_t* q8; float* qs; int8_t* k8; float* ks; float* kmean; double* part; uint16_t* vt;
   float* kn;    // [H][Skpad/128]: per 128-key block, an upper bound of the largest L2 norm of a key's int8 codes
   float* tail;  // [2][npair][FWD_BQ][TAIL_ROW] partials of the split last round; null when not reserved
+  int* ctr;     // the main kernel's work counter (cleared before each launch)
   int64_t bytes;
 };
 
@@ -51,6 +52,7 @@ inline Work layout(void* base, int64_t Sq, int64_t Sk, int64_t H, bool split = t
   const int64_t nwg = fwd_blocks(Sq, H);
   w.tail = split && nwg > TAIL_MAX ? reinterpret_cast<float*>(take(int64_t{2} * TAIL_MAX * FWD_BQ * TAIL_ROW * 4))
                                    : nullptr;
+  w.ctr = reinterpret_cast<int*>(take(256));
   w.bytes = off;
   return w;
 }
@@ -60,6 +62,7 @@ struct WorkU8 {
   int8_t* q8; float* qs; int8_t* k8; float* ks; int8_t* side; int8_t* vt;
   float* kmean; float* vmean; float* vscale;
   double* kpart; double* vsum; float* vmax; float* vmin;
+  int* ctr;  // the main kernel's work counter (cleared before each launch)
   int64_t bytes;
 };
 
@@ -82,6 +85,7 @@ inline WorkU8 layout_u8(void* base, int64_t Sq, int64_t Sk, int64_t H) {
   w.vsum = reinterpret_cast<double*>(take(H * nchunk * D * 8));
   w.vmax = reinterpret_cast<float*>(take(H * nchunk * D * 4));
   w.vmin = reinterpret_cast<float*>(take(H * nchunk * D * 4));
+  w.ctr = reinterpret_cast<int*>(take(256));
   w.bytes = off;
   return w;
 }

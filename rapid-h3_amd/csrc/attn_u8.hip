@@ -358,6 +358,8 @@ struct U8Args {
   float scale_log2;
   int nbias;
   float bias_log2;
+  int nqb;   // query blocks per head; item = h * nqb + qb (query blocks fastest)
+  int* ctr;  // work counter, zero at launch: a starting workgroup takes item ctr++
 };
 
 constexpr int U8_WAVES = 8, U8_NT = U8_WAVES * 64, U8_BQ = U8_WAVES * 32;
@@ -390,7 +392,14 @@ __global__ void __launch_bounds__(U8_NT, 1) attn_u8_kernel(const U8Args a) {
   constexpr bool BK = MODE == 1;
   constexpr int KB = TILE * D, VB = D * TILE, SLOT = KB + VB + SIDE;
   __shared__ __attribute__((aligned(16))) int8_t ring[4 * SLOT];
-  const int h = blockIdx.y, qb = blockIdx.x;
+  // the workgroup runs the item it takes from the work counter when it starts (a fast XCD takes more; see the
+  // launch), the (head, query block) pair h * nqb + qb
+  __shared__ int item_s;
+  if (threadIdx.x == 0) item_s = atomicAdd(a.ctr, 1);
+  __syncthreads();
+  const int item = __builtin_amdgcn_readfirstlane(item_s);
+  if (item >= static_cast<int>(gridDim.y) * a.nqb) return;
+  const int h = item / a.nqb, qb = item - h * a.nqb;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, g = lane >> 5;
@@ -806,12 +815,24 @@ int prepass_u8(const uint16_t* q, int64_t q_ss, int64_t q_sh, const uint16_t* k,
   return launch_status("attention_u8 prepass");
 }
 
+// Grid of the main kernel, whose workgroups take their (head, query block) items from a work counter: the grid is
+// dealt to the XCDs in fixed shares and the XCDs run at different clocks, so the grid holds a quarter more
+// workgroups than items (room for the fastest XCD to take a quarter more than its share); the extra ones return
+// at once. gridDim.y carries H. The counter is cleared first by a fill kernel (no hipMemsetAsync: graph-safe).
+dim3 claim_grid(U8Args& f, const WorkU8& w, int64_t Sq, int64_t H, hipStream_t st) {
+  f.nqb = static_cast<int>((Sq + U8_BQ - 1) / U8_BQ);
+  f.ctr = w.ctr;
+  const int64_t per_head = f.nqb + (f.nqb + 3) / 4;
+  hipLaunchKernelGGL(zero_kernel, dim3(1), dim3(64), 0, st, reinterpret_cast<float*>(w.ctr), int64_t{1});
+  return dim3(static_cast<uint32_t>(per_head), static_cast<uint32_t>(H));
+}
+
 // configs 50-56: the FP8 P.V main kernel; tile = the reference's BN (64 or 128 keys per running-max update)
 int forward_f8(const WorkU8& w, int64_t Sq, int64_t Sk, int64_t H, float scale, int tile, uint16_t* out, int64_t o_ss,
                int64_t o_sh, hipStream_t st) {
   U8Args f{w.q8, w.qs, w.k8, w.side, w.vt, w.vscale, w.vmean, out, o_ss, o_sh, Sq, Sk, padk(Sq), padk(Sk),
            scale * 1.4426950408889634f, 0, 0.0f};
-  const dim3 grid((Sq + U8_BQ - 1) / U8_BQ, H);
+  const dim3 grid = claim_grid(f, w, Sq, H, st);  // sets f.nqb and f.ctr: before f is passed
   if (tile == 64) hipLaunchKernelGGL((attn_u8_kernel<2, 64>), grid, dim3(U8_NT), 0, st, f);
   else hipLaunchKernelGGL((attn_u8_kernel<2, 128>), grid, dim3(U8_NT), 0, st, f);
   return launch_status("attention_f8 forward");
@@ -821,7 +842,8 @@ int forward_u8(const WorkU8& w, int64_t Sq, int64_t Sk, int64_t H, float scale, 
                int64_t o_ss, int64_t o_sh, hipStream_t st) {
   U8Args f{w.q8, w.qs, w.k8, w.side, w.vt, w.vscale, w.vmean, out, o_ss, o_sh, Sq, Sk, padk(Sq), padk(Sk),
            scale * 1.4426950408889634f, nbias, static_cast<float>(bias * 1.4426950408889634)};
-  hipLaunchKernelGGL(attn_u8_kernel<0>, dim3((Sq + U8_BQ - 1) / U8_BQ, H), dim3(U8_NT), 0, st, f);
+  const dim3 grid = claim_grid(f, w, Sq, H, st);  // sets f.nqb and f.ctr: before f is passed
+  hipLaunchKernelGGL(attn_u8_kernel<0>, grid, dim3(U8_NT), 0, st, f);
   return launch_status("attention_u8 forward");
 }
 
@@ -856,7 +878,8 @@ int forward_bk(const WorkU8& w, int64_t Sq, int64_t Sk, int64_t H, float scale, 
                int64_t o_sh, hipStream_t st) {
   U8Args f{w.q8, w.qs, w.k8, w.side, w.vt, w.vscale, w.vmean, out, o_ss, o_sh, Sq, Sk, padk(Sq), padk(Sk),
            scale * 1.4426950408889634f, 0, 0.0f};
-  hipLaunchKernelGGL(attn_u8_kernel<1>, dim3((Sq + U8_BQ - 1) / U8_BQ, H), dim3(U8_NT), 0, st, f);
+  const dim3 grid = claim_grid(f, w, Sq, H, st);  // sets f.nqb and f.ctr: before f is passed
+  hipLaunchKernelGGL(attn_u8_kernel<1>, grid, dim3(U8_NT), 0, st, f);
   return launch_status("attention_bk forward");
 }
 
