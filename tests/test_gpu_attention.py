@@ -175,6 +175,42 @@ def test_attention_split_switch(dev, monkeypatch):
     assert rel_l2(whole[:, hh], ref) < TOL
 
 
+def test_attention_work_counter_reused(dev):
+    """The main kernels take their (head, query block) items from a counter in the workspace, cleared by every
+    launch: two forward calls on one workspace (per-block recipe and production numerics), on a grid larger than
+    the CU count, give identical outputs, and the second one checks against the oracle (a counter left at the
+    previous launch's end would hand out no item and leave the output unwritten)."""
+    import torch
+    from rapid_h3 import attention
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    s = 1500
+    h = cus // 2 + 3                                         # 4 query blocks per head: more items than CUs
+    rng = np.random.default_rng(5)
+    q = _bf(rng.standard_normal((s, h, 128)))
+    k = _bf(rng.standard_normal((s, h, 128)) + 2.0 * rng.standard_normal((1, h, 128)))
+    v = _bf(rng.standard_normal((s, h, 128)))
+    qd, kd, vd = to_dev(q, dev), to_dev(k, dev), to_dev(v, dev)
+    pp = attention.prepass(qd, kd, vd)
+    outs = []
+    for _ in range(2):
+        o = torch.full((s, h, 128), float("nan"), dtype=torch.bfloat16, device=dev)
+        attention.forward(pp, s, out=o)
+        outs.append(to_np(o))
+    assert np.array_equal(outs[0], outs[1])
+    hh = h - 1
+    q8, qs, k8, ks, _ = oa.prepass(q[:, hh:hh + 1], k[:, hh:hh + 1])
+    ref = oa.attention_from_codes(q8, qs, k8, ks, v[:, hh:hh + 1], 128 ** -0.5)[:s, 0]
+    assert rel_l2(bf16_to_f32(outs[1])[:, hh], ref) < TOL
+    pu = attention.prepass_u8(qd, kd, vd)
+    outs = []
+    for _ in range(2):
+        o = torch.full((s, h, 128), float("nan"), dtype=torch.bfloat16, device=dev)
+        attention.forward_u8(pu, s, out=o)
+        outs.append(to_np(o))
+    assert np.array_equal(outs[0], outs[1])
+    assert np.isfinite(bf16_to_f32(outs[1])).all()
+
+
 def test_attention_full_size_sampled(dev):
     """C4: S = 145,152, H = 24, D = 128 with a per-head K offset ~ N(0, 2). Codes, scales and kmean of 3
     sampled heads bit-exact; output on 48 sampled query rows x those heads within tolerance, and
