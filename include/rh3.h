@@ -133,27 +133,32 @@ int rh3_quant_weight_rot_i8(const void* w, int w_dtype, int64_t ldw, int64_t N, 
  * Row-wise W8A8 GEMMs on int8 MFMA: acc[m,n] = sum_k xq[m,k] * wq[n,k] (int32, exact),
  * y = (fp32(acc) * xs[m]) * ws[n]. xq [M, K] int8 (row stride ldx), wq [N, K] int8 (row stride ldw),
  * xs [M], ws [N] fp32. K % 64 == 0, N % 8 == 0, strides % 16 == 0, 16-byte aligned rows.
+ * ctr: NULL, or 8 int32 of device memory (4-byte aligned) that the call owns while it runs on `stream`: the
+ * large shapes run one workgroup per CU over a tile sequence, and with ctr the workgroups of a faster XCD take
+ * over tiles of a slower one (per-XCD tile counters, cleared by a fill kernel on `stream` at each call, so the
+ * call stays capturable). Calls that may run concurrently (different streams) need different ctr. Same
+ * results with and without it; NULL keeps fixed per-XCD tile shares.
  * ------------------------------------------------------------------------------------------- */
 
 /* out = bf16_RNE(y [+ bias[n]]); bias [N] bf16 or NULL; out [M, N] row stride ldo.
  * replaces cutlass_fp8.int8_gemm -> int8_rowwise_gemm (cutlass_fp8.py:37-39, fp8_rowwise.cu:546-584) */
 int rh3_gemm_i8(const int8_t* xq, int64_t ldx, const float* xs, const int8_t* wq, int64_t ldw,
                 const float* ws, const uint16_t* bias, uint16_t* out, int64_t ldo,
-                int64_t M, int64_t N, int64_t K, hipStream_t stream);
+                int64_t M, int64_t N, int64_t K, int32_t* ctr, hipStream_t stream);
 
 /* SwiGLU epilogue for fc1 rows in swiglu_perm order ([g 4j..4j+3 | u 4j..4j+3] per 8 columns):
  * g, u = bf16(y); h[m, n/2..] = bf16((g * sigmoid(g)) * u); out [M, N/2] row stride ldo.
  * replaces cutlass_fp8.int8_gemm_swiglu (cutlass_fp8.py:65-67, fp8_rowwise.cu:611-629) */
 int rh3_gemm_i8_swiglu(const int8_t* xq, int64_t ldx, const float* xs, const int8_t* wq_perm, int64_t ldw,
                        const float* ws_perm, uint16_t* out, int64_t ldo,
-                       int64_t M, int64_t N, int64_t K, hipStream_t stream);
+                       int64_t M, int64_t N, int64_t K, int32_t* ctr, hipStream_t stream);
 
 /* Gated residual, in place: resid[m,n] = bf16_RNE(fma(bf16(y), gate[n], resid[m,n])); gate [N] bf16;
  * resid [M, N] row stride ldr.
  * replaces cutlass_fp8.int8_gemm_gated_residual (cutlass_fp8.py:49-52, fp8_rowwise.cu:587-608) */
 int rh3_gemm_i8_gated(const int8_t* xq, int64_t ldx, const float* xs, const int8_t* wq, int64_t ldw,
                       const float* ws, const uint16_t* gate, uint16_t* resid, int64_t ldr,
-                      int64_t M, int64_t N, int64_t K, hipStream_t stream);
+                      int64_t M, int64_t N, int64_t K, int32_t* ctr, hipStream_t stream);
 
 /* Gated residual with a gate row per output row (per-token modulation), in place:
  * resid[m,n] = bf16_RNE(fma(bf16(y), gate[gidx[m], n], resid[m,n])); gate [R, ldg] bf16 (16-byte aligned,
@@ -162,13 +167,14 @@ int rh3_gemm_i8_gated(const int8_t* xq, int64_t ldx, const float* xs, const int8
  * segments) for segments whose row is a tensor (__init__.py:242-245) */
 int rh3_gemm_i8_gated_rows(const int8_t* xq, int64_t ldx, const float* xs, const int8_t* wq, int64_t ldw,
                            const float* ws, const uint16_t* gate, int64_t ldg, const int32_t* gidx,
-                           uint16_t* resid, int64_t ldr, int64_t M, int64_t N, int64_t K, hipStream_t stream);
+                           uint16_t* resid, int64_t ldr, int64_t M, int64_t N, int64_t K, int32_t* ctr,
+                           hipStream_t stream);
 
 /* Verification: the raw int32 accumulators acc [M, N] (row stride ldc) of the same kernel.
  * No reference counterpart as an entry point: it exposes the s32 accumulator of
  * fp8_rowwise.cu:282-331 so tests can check it bit for bit. */
 int rh3_gemm_i8_acc(const int8_t* xq, int64_t ldx, const int8_t* wq, int64_t ldw, int32_t* acc, int64_t ldc,
-                    int64_t M, int64_t N, int64_t K, hipStream_t stream);
+                    int64_t M, int64_t N, int64_t K, int32_t* ctr, hipStream_t stream);
 
 /* The qkv projection with the attention pre-pass partly fused into its epilogue.
  * replaces cutlass_fp8.int8_gemm_qkv_prep -> run_qkv_prep / VisitorQkvPrep (cutlass_fp8.py:42-46,
@@ -189,7 +195,7 @@ int rh3_gemm_i8_qkv(const int8_t* xq, int64_t ldx, const float* xs, const int8_t
  * replaces cutlass_fp8.fp8_gemm -> fp8_rowwise_gemm (cutlass_fp8.py:32-34, fp8_rowwise.cu:512-544) */
 int rh3_gemm_fp8(const uint8_t* xq, int64_t ldx, const float* xs, const uint8_t* wq, int64_t ldw,
                  const float* ws, const uint16_t* bias, uint16_t* out, int64_t ldo,
-                 int64_t M, int64_t N, int64_t K, hipStream_t stream);
+                 int64_t M, int64_t N, int64_t K, int32_t* ctr, hipStream_t stream);
 
 /* ---------------------------------------------------------------------------------------------
  * INT8 flash attention, head_dim 128, non-causal. q [Sq, H, 128], k and v [Sk, H, 128] bf16 with any

@@ -83,6 +83,7 @@ struct GemmArgs {
   QkvPrep qp;
   const int32_t* gidx;  // EPI_GATED_ROWS: gate table row of each output row (the gate is [R, ldg] bf16)
   int64_t ldg;
+  int* ctr;  // persistent kernel: per-XCD tile counters (8 ints, zero at launch) or null (fixed tile shares)
 };
 
 // 16-byte chunk c (0..3) of LDS row r: rows r, r+1 share a 128-byte line; the XOR keeps 16
@@ -606,6 +607,31 @@ __global__ void __launch_bounds__(GEMM_NW * 64, GEMM_NW / 4) gemm_kernel(const G
   }
 }
 
+// The next tile of a persistent workgroup on XCD xcd, taken from the per-XCD counters: its own XCD's range first,
+// then the other XCDs' (so an XCD that runs faster takes over the tiles of a slower one at the end). Range x holds
+// tiles [lo_x, hi_x); its first (grid - x + 7) / 8 tiles went out as the workgroups' first tiles, the rest are
+// handed out in order by counter x. -1: no tile left.
+__device__ __forceinline__ int claim_tile(int* ctr, int xcd, int nb, int grid) {
+  // opaque to the compiler, so the range bounds below are computed here, at the claim, and not hoisted out of the
+  // caller's tile loop into registers held for the whole kernel
+  asm volatile("" : "+s"(nb), "+s"(grid));
+#pragma unroll 1
+  for (int d = 0; d < 8; ++d) {
+    const int x = (xcd + d) & 7;
+    const int lo = x * (nb / 8) + min(x, nb % 8);
+    const int hi = lo + nb / 8 + (x < nb % 8 ? 1 : 0);
+    const int first = lo + (grid - x + 7) / 8;
+    if (first >= hi) continue;
+    const int c = atomicAdd(ctr + x, 1);
+    if (first + c < hi) return first + c;
+  }
+  return -1;
+}
+
+__global__ void zero_ctr_kernel(int* p) {
+  if (threadIdx.x < 8) p[threadIdx.x] = 0;
+}
+
 // Persistent form of gemm_kernel (every epilogue but EPI_QKV; K a multiple of 4 k-steps, at least 8): one workgroup
 // per CU walks a strided share of its XCD's tile range, in the same grouped order. The k-loop runs on
 // across tile boundaries: the loads of the next tile's first three k-steps are issued by the current
@@ -614,7 +640,7 @@ __global__ void __launch_bounds__(GEMM_NW * 64, GEMM_NW / 4) gemm_kernel(const G
 // a 2 KiB per-wave LDS area and its global stores drain while the next tile's MFMAs run. The row scales,
 // column scales and bias / gate of a tile are loaded into registers at the tile start and parked in LDS
 // after its first four k-steps. Same arithmetic as gemm_kernel, element for element.
-template <bool FP8, int EPI>
+template <bool FP8, int EPI, bool CLAIM>
 __global__ void __launch_bounds__(512, 2) gemm_persistent_kernel(const GemmArgs a) {
   static_assert(EPI != EPI_QKV, "the qkv epilogue stages the whole tile in the ring");
   constexpr int NW = 8;
@@ -627,10 +653,13 @@ __global__ void __launch_bounds__(512, 2) gemm_persistent_kernel(const GemmArgs 
       st3[2 * TILE_BYTES];
   __shared__ __attribute__((aligned(16))) int8_t ep_lds[NW * 2048];  // per-wave 32 x 32 bf16 staging block
   __shared__ __attribute__((aligned(16))) float rec[3 * BM];         // xs[256], ws[256], bias / gate[256]
+  __shared__ int next_tile;
 
   // XCD-aware share: workgroup b runs on XCD b % 8; XCD x owns the logical tiles [lo, hi) and its nslot
   // workgroups take them round robin, so the ~32 tiles in flight on an XCD are consecutive in the grouped
-  // order (shared activation and weight panels in that XCD's L2)
+  // order (shared activation and weight panels in that XCD's L2). With counters (a.ctr), a workgroup's first tile
+  // is the same, and each later one is taken from the counters one tile ahead (claim_tile): the XCDs run at
+  // different clocks, and fixed shares leave the fast ones idle while the slowest finishes (3-5 % of a launch)
   const int nb = a.tiles_m * a.tiles_n;
   const int b = blockIdx.x, xcd = b % 8, slot = b / 8;
   const int nslot = (static_cast<int>(gridDim.x) - xcd + 7) / 8;
@@ -772,14 +801,16 @@ __global__ void __launch_bounds__(512, 2) gemm_persistent_kernel(const GemmArgs 
         }
       }
     }
-    const int ltn = lt + nslot;
-    const bool more = ltn < hi;
-    int64_t m0n = m0, n0n = n0;
-    if (more) tile_origin(ltn, m0n, n0n);
+    // the next tile: claimed by thread 0 now, read by every thread past the barrier of the first k-step
+    if (CLAIM && tid == 0) next_tile = claim_tile(a.ctr, xcd, nb, static_cast<int>(gridDim.x));
 
     // k-steps 0..3, then the record goes to LDS: every wave has finished the previous tile's epilogue (it
     // passed this tile's barriers since), and the barriers of the k-steps left publish it to this tile's
     step(3, st0, st1, st3);
+    const int ltn = CLAIM ? __builtin_amdgcn_readfirstlane(next_tile) : lt + nslot;
+    const bool more = CLAIM ? ltn >= 0 : ltn < hi;
+    int64_t m0n = m0, n0n = n0;
+    if (more) tile_origin(ltn, m0n, n0n);
     step(4, st1, st2, st0);
     step(5, st2, st3, st1);
     step(6, st3, st0, st2);
@@ -941,7 +972,14 @@ int run(GemmArgs a, hipStream_t st, const char* name) {
     const bool off32 = 255 * a.ldx + 64 < (1ll << 32) && 255 * a.ldw + 64 < (1ll << 32);
     if (nk % 4 == 0 && nk >= 8 && cus > 0 && off32) {
       const int64_t grid = nb < cus ? nb : cus;  // one workgroup per CU (the LDS use admits no second)
-      hipLaunchKernelGGL((gemm_persistent_kernel<FP8, EPI>), dim3(static_cast<unsigned>(grid)), dim3(512), 0, st, a);
+      // the counters are cleared by a fill kernel (no hipMemsetAsync: the call stays graph-safe)
+      const dim3 g(static_cast<unsigned>(grid));
+      if (a.ctr != nullptr) {
+        hipLaunchKernelGGL(zero_ctr_kernel, dim3(1), dim3(64), 0, st, a.ctr);
+        hipLaunchKernelGGL((gemm_persistent_kernel<FP8, EPI, true>), g, dim3(512), 0, st, a);
+      } else {
+        hipLaunchKernelGGL((gemm_persistent_kernel<FP8, EPI, false>), g, dim3(512), 0, st, a);
+      }
       return launch_status(name);
     }
   }
@@ -974,28 +1012,32 @@ using namespace rh3;
 
 extern "C" int rh3_gemm_i8(const int8_t* xq, int64_t ldx, const float* xs, const int8_t* wq, int64_t ldw,
                            const float* ws, const uint16_t* bias, uint16_t* out, int64_t ldo, int64_t M, int64_t N,
-                           int64_t K, hipStream_t stream) {
+                           int64_t K, int32_t* ctr, hipStream_t stream) {
   clear_error();
   if (int e = check("gemm_i8", xq, ldx, wq, ldw, out, ldo, M, N, K, N)) return e;
   RH3_REQUIRE(M == 0 || N == 0 || (xs && ws && aligned16(ws)), "gemm_i8: scales required (ws 16-byte aligned)");
   GemmArgs a{xq, ldx, wq, ldw, xs, ws, bias, nullptr, out, ldo, M, N, K, 0, 0};
+  RH3_REQUIRE((reinterpret_cast<uintptr_t>(ctr) & 3) == 0, "%s: ctr must be 4-byte aligned", "gemm_i8");
+  a.ctr = reinterpret_cast<int*>(ctr);
   return run<false, EPI_PLAIN>(a, stream, "gemm_i8");
 }
 
 extern "C" int rh3_gemm_i8_swiglu(const int8_t* xq, int64_t ldx, const float* xs, const int8_t* wq_perm, int64_t ldw,
                                   const float* ws_perm, uint16_t* out, int64_t ldo, int64_t M, int64_t N, int64_t K,
-                                  hipStream_t stream) {
+                                  int32_t* ctr, hipStream_t stream) {
   clear_error();
   if (int e = check("gemm_i8_swiglu", xq, ldx, wq_perm, ldw, out, ldo, M, N, K, N / 2)) return e;
   RH3_REQUIRE(M == 0 || N == 0 || (xs && ws_perm && aligned16(ws_perm)), "gemm_i8_swiglu: scales required");
   GemmArgs a{xq, ldx, wq_perm, ldw, xs, ws_perm, nullptr, nullptr, out, ldo, M, N, K, 0, 0};
+  RH3_REQUIRE((reinterpret_cast<uintptr_t>(ctr) & 3) == 0, "%s: ctr must be 4-byte aligned", "gemm_i8_swiglu");
+  a.ctr = reinterpret_cast<int*>(ctr);
   return run<false, EPI_SWIGLU>(a, stream, "gemm_i8_swiglu");
 }
 
 extern "C" int rh3_gemm_i8_gated_rows(const int8_t* xq, int64_t ldx, const float* xs, const int8_t* wq, int64_t ldw,
                                       const float* ws, const uint16_t* gate, int64_t ldg, const int32_t* gidx,
                                       uint16_t* resid, int64_t ldr, int64_t M, int64_t N, int64_t K,
-                                      hipStream_t stream) {
+                                      int32_t* ctr, hipStream_t stream) {
   clear_error();
   if (int e = check("gemm_i8_gated_rows", xq, ldx, wq, ldw, resid, ldr, M, N, K, N)) return e;
   RH3_REQUIRE(M == 0 || N == 0 || (xs && ws && gate && gidx && aligned16(ws) && aligned16(gate)),
@@ -1005,24 +1047,30 @@ extern "C" int rh3_gemm_i8_gated_rows(const int8_t* xq, int64_t ldx, const float
   GemmArgs a{xq, ldx, wq, ldw, xs, ws, nullptr, gate, resid, ldr, M, N, K, 0, 0};
   a.gidx = gidx;
   a.ldg = ldg;
+  RH3_REQUIRE((reinterpret_cast<uintptr_t>(ctr) & 3) == 0, "%s: ctr must be 4-byte aligned", "gemm_i8_gated_rows");
+  a.ctr = reinterpret_cast<int*>(ctr);
   return run<false, EPI_GATED_ROWS>(a, stream, "gemm_i8_gated_rows");
 }
 
 extern "C" int rh3_gemm_i8_gated(const int8_t* xq, int64_t ldx, const float* xs, const int8_t* wq, int64_t ldw,
                                  const float* ws, const uint16_t* gate, uint16_t* resid, int64_t ldr, int64_t M,
-                                 int64_t N, int64_t K, hipStream_t stream) {
+                                 int64_t N, int64_t K, int32_t* ctr, hipStream_t stream) {
   clear_error();
   if (int e = check("gemm_i8_gated", xq, ldx, wq, ldw, resid, ldr, M, N, K, N)) return e;
   RH3_REQUIRE(M == 0 || N == 0 || (xs && ws && gate && aligned16(ws)), "gemm_i8_gated: scales and gate required");
   GemmArgs a{xq, ldx, wq, ldw, xs, ws, nullptr, gate, resid, ldr, M, N, K, 0, 0};
+  RH3_REQUIRE((reinterpret_cast<uintptr_t>(ctr) & 3) == 0, "%s: ctr must be 4-byte aligned", "gemm_i8_gated");
+  a.ctr = reinterpret_cast<int*>(ctr);
   return run<false, EPI_GATED>(a, stream, "gemm_i8_gated");
 }
 
 extern "C" int rh3_gemm_i8_acc(const int8_t* xq, int64_t ldx, const int8_t* wq, int64_t ldw, int32_t* acc,
-                               int64_t ldc, int64_t M, int64_t N, int64_t K, hipStream_t stream) {
+                               int64_t ldc, int64_t M, int64_t N, int64_t K, int32_t* ctr, hipStream_t stream) {
   clear_error();
   if (int e = check("gemm_i8_acc", xq, ldx, wq, ldw, acc, ldc, M, N, K, N)) return e;
   GemmArgs a{xq, ldx, wq, ldw, nullptr, nullptr, nullptr, nullptr, acc, ldc, M, N, K, 0, 0};
+  RH3_REQUIRE((reinterpret_cast<uintptr_t>(ctr) & 3) == 0, "%s: ctr must be 4-byte aligned", "gemm_i8_acc");
+  a.ctr = reinterpret_cast<int*>(ctr);
   return run<false, EPI_ACC>(a, stream, "gemm_i8_acc");
 }
 
@@ -1072,11 +1120,13 @@ extern "C" int rh3_gemm_i8_qkv(const int8_t* xq, int64_t ldx, const float* xs, c
 
 extern "C" int rh3_gemm_fp8(const uint8_t* xq, int64_t ldx, const float* xs, const uint8_t* wq, int64_t ldw,
                             const float* ws, const uint16_t* bias, uint16_t* out, int64_t ldo, int64_t M, int64_t N,
-                            int64_t K, hipStream_t stream) {
+                            int64_t K, int32_t* ctr, hipStream_t stream) {
   clear_error();
   if (int e = check("gemm_fp8", xq, ldx, wq, ldw, out, ldo, M, N, K, N)) return e;
   RH3_REQUIRE(M == 0 || N == 0 || (xs && ws && aligned16(ws)), "gemm_fp8: scales required (ws 16-byte aligned)");
   GemmArgs a{reinterpret_cast<const int8_t*>(xq), ldx, reinterpret_cast<const int8_t*>(wq), ldw, xs, ws, bias,
              nullptr, out, ldo, M, N, K, 0, 0};
+  RH3_REQUIRE((reinterpret_cast<uintptr_t>(ctr) & 3) == 0, "%s: ctr must be 4-byte aligned", "gemm_fp8");
+  a.ctr = reinterpret_cast<int*>(ctr);
   return run<true, EPI_PLAIN>(a, stream, "gemm_fp8");
 }

@@ -10,6 +10,8 @@ import os
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get("RH3_LIB", os.path.join(_HERE, "librh3.so"))
 
+ABI_VERSION = 2  # rh3_abi_version() of the library these signatures describe
+
 _P = ctypes.c_void_p
 _I = ctypes.c_int64
 _F = ctypes.c_float
@@ -33,13 +35,13 @@ SIGNATURES = {
     "rh3_quant_any": ([_P, _C, _I, _I, _I, _C, _P, _I, _P, _P, _P], _C),
     "rh3_quant_weight_rot_i8": ([_P, _C, _I, _I, _I, _P, _I, _P, _P], _C),
     "rh3_fake_nvfp4": ([_P, _C, _I, _I, _I, _P, _I, _P, _P], _C),
-    "rh3_gemm_i8": ([_P, _I, _P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _P], _C),
-    "rh3_gemm_i8_swiglu": ([_P, _I, _P, _P, _I, _P, _P, _I, _I, _I, _I, _P], _C),
-    "rh3_gemm_i8_gated": ([_P, _I, _P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _P], _C),
-    "rh3_gemm_i8_gated_rows": ([_P, _I, _P, _P, _I, _P, _P, _I, _P, _P, _I, _I, _I, _I, _P], _C),
-    "rh3_gemm_i8_acc": ([_P, _I, _P, _I, _P, _I, _I, _I, _I, _P], _C),
+    "rh3_gemm_i8": ([_P, _I, _P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _P, _P], _C),
+    "rh3_gemm_i8_swiglu": ([_P, _I, _P, _P, _I, _P, _P, _I, _I, _I, _I, _P, _P], _C),
+    "rh3_gemm_i8_gated": ([_P, _I, _P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _P, _P], _C),
+    "rh3_gemm_i8_gated_rows": ([_P, _I, _P, _P, _I, _P, _P, _I, _P, _P, _I, _I, _I, _I, _P, _P], _C),
+    "rh3_gemm_i8_acc": ([_P, _I, _P, _I, _P, _I, _I, _I, _I, _P, _P], _C),
     "rh3_gemm_i8_qkv": ([_P, _I, _P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _P, _C, _P, _P, _F, _C, _C, _P, _I, _P], _C),
-    "rh3_gemm_fp8": ([_P, _I, _P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _P], _C),
+    "rh3_gemm_fp8": ([_P, _I, _P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _P, _P], _C),
     "rh3_attention_workspace_bytes": ([_I, _I, _I], ctypes.c_int64),
     "rh3_int8_attention": ([_P, _I, _I, _P, _I, _I, _P, _I, _I, _I, _I, _I, _F, _C, _P, _I, _I, _P, _I, _P], _C),
     "rh3_int8_attention_noalloc": ([_P, _I, _I, _P, _I, _I, _P, _I, _I, _I, _I, _I, _F, _C, _P, _I, _I, _P], _C),
@@ -90,6 +92,9 @@ def lib():
             f = getattr(lib_, name)
             f.argtypes = argt
             f.restype = rest
+        if lib_.rh3_abi_version() != ABI_VERSION:
+            raise RuntimeError(f"{LIB_PATH} has ABI version {lib_.rh3_abi_version()}, this binding expects "
+                               f"{ABI_VERSION}: rebuild it with `python rapid-h3_amd/build.py`")
         _lib = lib_
     return _lib
 
@@ -113,3 +118,20 @@ def ptr(t):
 def stream(device):
     import torch
     return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+_GEMM_CTR = {}
+
+
+def gemm_ctr(device):
+    """The GEMM tile counters (8 int32) of torch's current stream on `device`: one buffer per (device, stream), kept
+    for the life of the process, so calls on one stream share it in order and calls on different streams never do
+    (the ownership rule of the `ctr` argument of the rh3_gemm_* entry points)."""
+    import torch
+    st = torch.cuda.current_stream(device)
+    key = (st.device.index, st.cuda_stream)
+    t = _GEMM_CTR.get(key)
+    if t is None:
+        t = torch.zeros(64, dtype=torch.int32, device=st.device)
+        _GEMM_CTR[key] = t
+    return ctypes.c_void_p(t.data_ptr())

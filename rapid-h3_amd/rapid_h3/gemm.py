@@ -39,7 +39,8 @@ def int8_gemm(xq, xs, wq, ws, bias=None, config=2):
         bias = bias.to(torch.bfloat16).contiguous()
     out = torch.empty((m, n), device=xq.device, dtype=torch.bfloat16)
     nat.call("rh3_gemm_i8", nat.ptr(xq), xq.stride(0), nat.ptr(xs), nat.ptr(wq), wq.stride(0), nat.ptr(ws),
-             nat.ptr(bias), nat.ptr(out), out.stride(0), m, n, k, nat.stream(xq.device))
+             nat.ptr(bias), nat.ptr(out), out.stride(0), m, n, k, nat.gemm_ctr(xq.device),
+             nat.stream(xq.device))
     return out
 
 
@@ -50,7 +51,8 @@ def int8_gemm_acc(xq, wq):
     n = wq.shape[0]
     acc = torch.empty((m, n), device=xq.device, dtype=torch.int32)
     nat.call("rh3_gemm_i8_acc", nat.ptr(xq), xq.stride(0), nat.ptr(wq), wq.stride(0), nat.ptr(acc), acc.stride(0),
-             m, n, k, nat.stream(xq.device))
+             m, n, k, nat.gemm_ctr(xq.device),
+             nat.stream(xq.device))
     return acc
 
 
@@ -65,7 +67,8 @@ def fp8_gemm(xq, xs, wq, ws, bias=None, config=2, fast_accum=True):
         bias = bias.to(torch.bfloat16).contiguous()
     out = torch.empty((m, n), device=xq.device, dtype=torch.bfloat16)
     nat.call("rh3_gemm_fp8", nat.ptr(xq), xq.stride(0), nat.ptr(xs), nat.ptr(wq), wq.stride(0), nat.ptr(ws),
-             nat.ptr(bias), nat.ptr(out), out.stride(0), m, n, k, nat.stream(xq.device))
+             nat.ptr(bias), nat.ptr(out), out.stride(0), m, n, k, nat.gemm_ctr(xq.device),
+             nat.stream(xq.device))
     return out
 
 
@@ -81,7 +84,8 @@ def int8_gemm_gated_residual(xq, xs, wq, ws, gate, resid, config=6):
     if gate.numel() != n:
         raise RuntimeError("int8_gemm_gated_residual: gate must have N elements")
     nat.call("rh3_gemm_i8_gated", nat.ptr(xq), xq.stride(0), nat.ptr(xs), nat.ptr(wq), wq.stride(0), nat.ptr(ws),
-             nat.ptr(gate), nat.ptr(resid), resid.stride(0), m, n, k, nat.stream(xq.device))
+             nat.ptr(gate), nat.ptr(resid), resid.stride(0), m, n, k, nat.gemm_ctr(xq.device),
+             nat.stream(xq.device))
     return resid
 
 
@@ -101,7 +105,7 @@ def int8_gemm_gated_residual_rows(xq, xs, wq, ws, gate, rows, resid):
         raise RuntimeError("int8_gemm_gated_residual_rows: one gate row index per token required")
     nat.call("rh3_gemm_i8_gated_rows", nat.ptr(xq), xq.stride(0), nat.ptr(xs), nat.ptr(wq), wq.stride(0),
              nat.ptr(ws), nat.ptr(gate), gate.stride(0), nat.ptr(rows), nat.ptr(resid), resid.stride(0), m, n, k,
-             nat.stream(xq.device))
+             nat.gemm_ctr(xq.device), nat.stream(xq.device))
     return resid
 
 
@@ -125,7 +129,8 @@ def int8_gemm_swiglu(xq, xs, wq_perm, ws_perm, config=6):
     xs, ws = _vec(xs, m, "swiglu xs"), _vec(ws_perm, n, "swiglu ws")
     out = torch.empty((m, n // 2), device=xq.device, dtype=torch.bfloat16)
     nat.call("rh3_gemm_i8_swiglu", nat.ptr(xq), xq.stride(0), nat.ptr(xs), nat.ptr(wq_perm), wq_perm.stride(0),
-             nat.ptr(ws), nat.ptr(out), out.stride(0), m, n, k, nat.stream(xq.device))
+             nat.ptr(ws), nat.ptr(out), out.stride(0), m, n, k, nat.gemm_ctr(xq.device),
+             nat.stream(xq.device))
     return out
 
 

@@ -25,16 +25,16 @@ def test_header_symbols_exported_and_bound():
         assert hasattr(lib, n), n
         assert n in _native.SIGNATURES, f"{n} declared in rh3.h but not bound in _native"
     assert set(_native.SIGNATURES) == set(names)
-    assert lib.rh3_abi_version() == 1
+    assert lib.rh3_abi_version() == _native.ABI_VERSION == 2
 
 
 def test_argument_validation_without_gpu():
     from rapid_h3 import _native as nat
     lib = nat.lib()
     fake = ctypes.c_void_p(0x1000)          # never dereferenced: validation fails first
-    st = lib.rh3_gemm_i8(fake, 96, fake, fake, 96, fake, None, fake, 16, 4, 16, 96, None)
+    st = lib.rh3_gemm_i8(fake, 96, fake, fake, 96, fake, None, fake, 16, 4, 16, 96, None, None)
     assert st == 1 and "multiple of 64" in nat.last_error()
-    st = lib.rh3_gemm_i8(fake, 64, fake, fake, 64, fake, None, fake, 16, 4, 12, 64, None)
+    st = lib.rh3_gemm_i8(fake, 64, fake, fake, 64, fake, None, fake, 16, 4, 12, 64, None, None)
     assert st == 1 and "multiple of 8" in nat.last_error()
     st = lib.rh3_quant_rows_i8(fake, 12, 4, 12, fake, 16, fake, None)
     assert st == 1 and "multiple of 8" in nat.last_error()
@@ -61,14 +61,14 @@ def test_argument_validation_without_gpu():
                                       fake, 1e-5, 1, 1, 1, fake, 1 << 30, fake, None)
     assert st == 1 and "self-attention" in nat.last_error()
     with pytest.raises(RuntimeError, match="multiple of 64"):
-        nat.call("rh3_gemm_i8", fake, 96, fake, fake, 96, fake, None, fake, 16, 4, 16, 96, None)
+        nat.call("rh3_gemm_i8", fake, 96, fake, fake, 96, fake, None, fake, 16, 4, 16, 96, None, None)
 
 
 def test_empty_inputs_are_no_ops():
     from rapid_h3 import _native as nat
     lib = nat.lib()
     assert lib.rh3_quant_rows_i8(None, 0, 0, 64, None, 64, None, None) == 0
-    assert lib.rh3_gemm_i8(None, 64, None, None, 64, None, None, None, 8, 0, 8, 64, None) == 0
+    assert lib.rh3_gemm_i8(None, 64, None, None, 64, None, None, None, 8, 0, 8, 64, None, None) == 0
 
 
 def test_workspace_size_matches_layout():

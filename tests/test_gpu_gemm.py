@@ -115,6 +115,27 @@ def test_gemm_persistent_epilogues(dev, m, n, k):
     assert og.rel_l2(got, bf16_to_f32(og.fp8_gemm(fq, xs, fwq, ws))) < 1e-2
 
 
+@pytest.mark.parametrize("m,n,k", [(4500, 4112, 512), (9000, 8200, 256), (700, 784, 1024)])
+def test_gemm_tile_counters(dev, m, n, k):
+    """The persistent kernel with per-XCD tile counters (ctr, the Python layer's default) and with the fixed tile
+    shares (ctr NULL) against the oracle's int32 accumulators, bit-exact; two calls in a row on one counter buffer
+    (each call clears it). 306 and 1155 tiles (more than one per CU, so workgroups claim and steal) and 12 tiles
+    (fewer than the CUs: every workgroup's first tile is its last)."""
+    import ctypes
+    import torch
+    from rapid_h3 import _native as nat
+    rng = np.random.default_rng(m + n + k)
+    xq = np.clip(np.rint(rng.standard_normal((m, k)) * 30), -127, 127).astype(np.int8)
+    wq = np.clip(np.rint(rng.standard_normal((n, k)) * 30), -127, 127).astype(np.int8)
+    want = og.int8_acc(xq, wq)
+    xt, wt = to_dev(xq, dev), to_dev(wq, dev)
+    ctr = torch.full((8,), 12345, dtype=torch.int32, device=dev)  # stale contents: the call must clear them
+    for c in (None, ctypes.c_void_p(ctr.data_ptr()), ctypes.c_void_p(ctr.data_ptr())):
+        acc = torch.full((m, n), -1, dtype=torch.int32, device=dev)
+        nat.call("rh3_gemm_i8_acc", nat.ptr(xt), k, nat.ptr(wt), k, nat.ptr(acc), n, m, n, k, c, nat.stream(dev))
+        assert np.array_equal(to_np(acc), want)
+
+
 @pytest.mark.parametrize("m,n,k", [(4500, 4112, 512), (300, 264, 128)])
 def test_gemm_gated_rows(dev, m, n, k):
     """The gated residual with a gate row per token (per-token modulation) bit-exact against the oracle, on the
