@@ -50,11 +50,22 @@ class BlockWeights:
     recipe: str = "int8_rowwise"      # or "int8_rot": the weights above must be quantized the same way
 
 
+_ROW_INDEX = {}
+
+
 def row_index(segments, s, device):
-    """Per-token modulation-row index (int32 [S]) from [(start, stop, row)] (__init__.py:189-200)."""
+    """Per-token modulation-row index (int32 [S]) from [(start, stop, row)] (__init__.py:189-200). Like the
+    reference, the last index built is kept for the same segments object (identity, S and device), so the blocks of
+    one model call build it once; a caller that edits a segments list in place passes a new list instead."""
+    key = (id(segments), s, str(device))
+    hit = _ROW_INDEX.get(key)
+    if hit is not None and hit[0] is segments:
+        return hit[1]
     idx = torch.empty(s, dtype=torch.int32, device=device)
     for a, b, row in segments:
         idx[a:b] = row.to(device=device, dtype=torch.int32) if torch.is_tensor(row) else int(row)
+    _ROW_INDEX.clear()
+    _ROW_INDEX[key] = (segments, idx)
     return idx
 
 
