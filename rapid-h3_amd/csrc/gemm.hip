@@ -724,6 +724,10 @@ __global__ void __launch_bounds__(512, 2) gemm_persistent_kernel(const GemmArgs 
   // vmcnt(8): the loads of the next k-step have landed, the two k-steps after it stay in flight (loads
   // or stores issued in between only make the wait stronger)
   auto sync_next = [&]() __attribute__((always_inline)) {
+    // int8: every MFMA of the half step is issued before the barrier (left alone, the scheduler moved the last
+    // ones past it, so a wave waiting there had no MFMA queued; about 0.5-1 % on the C2 shapes); fp8 is faster
+    // with the scheduler's order
+    if constexpr (MM::KSUB == 2) __builtin_amdgcn_sched_barrier(0);
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_waitcnt(0x0078);
     __builtin_amdgcn_s_barrier();
