@@ -90,8 +90,7 @@ __global__ void __launch_bounds__(256) quant_kernel(const uint16_t* __restrict__
     if (knorm) {
       int r = __builtin_amdgcn_sdot4(static_cast<int>(c8.x), static_cast<int>(c8.x), 0, false);
       r = __builtin_amdgcn_sdot4(static_cast<int>(c8.y), static_cast<int>(c8.y), r, false);
-#pragma unroll
-      for (int o = 1; o < 16; o <<= 1) r += __shfl_xor(r, o, 64);
+      r = row_sum16_i(r);
       n2 = max(n2, r);
     }
   }

@@ -3,6 +3,8 @@
 // prologue and the normalized 128-point Walsh-Hadamard transform.
 #pragma once
 
+#include <type_traits>
+
 #include "rh3_common.hpp"
 
 namespace rh3 {
@@ -19,6 +21,49 @@ __device__ __forceinline__ void load8(const uint16_t* p, float* v) {
   unpack8(*reinterpret_cast<const uint4*>(p), v);
 }
 
+// The value of lane l ^ M (M = 1, 2, 4, 8) of the 16-lane row group, by DPP lane moves instead of the LDS crossbar:
+// row_ror:8 (l ^ 8 in a 16-lane row), row_half_mirror then quad_perm [3,2,1,0] (l ^ 7, then ^ 3: l ^ 4),
+// quad_perm [2,3,0,1] (l ^ 2) and [1,0,3,2] (l ^ 1)
+template <int M>
+__device__ __forceinline__ float xor16(float v) {
+  static_assert(M == 1 || M == 2 || M == 4 || M == 8, "lane distance");
+  if constexpr (M == 8) return dpp_mov<0x128>(v);
+  else if constexpr (M == 4) return dpp_mov<0x1B>(dpp_mov<0x141>(v));
+  else if constexpr (M == 2) return dpp_mov<0x4E>(v);
+  else return dpp_mov<0xB1>(v);
+}
+// sum over the 16 lanes of a row group, in the butterfly order of lane distances 8, 4, 2, 1 (each lane adds its
+// partner's value to its own, as x + shfl_xor(x, m) does: the same bits)
+__device__ __forceinline__ float row_sum16(float v) {
+  v = v + xor16<8>(v);
+  v = v + xor16<4>(v);
+  v = v + xor16<2>(v);
+  v = v + xor16<1>(v);
+  return v;
+}
+// integer sum over the 16 lanes of a row group (exact in any order), on the same lane moves
+__device__ __forceinline__ int row_sum16_i(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x128, 0xf, 0xf, true);
+  v += __builtin_amdgcn_update_dpp(0, __builtin_amdgcn_update_dpp(0, v, 0x141, 0xf, 0xf, true), 0x1B, 0xf, 0xf, true);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xf, 0xf, true);
+  v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xf, 0xf, true);
+  return v;
+}
+// the RoPE partner of every lane's 8 channels: lane l16 + step for the first rot/2 channels, l16 - step for the next
+// rot/2, the lane itself past rot (step = rot/16 lanes); rot = 128 is one DPP move (l ^ 8), other widths go through
+// the LDS crossbar
+__device__ __forceinline__ void rope_partner8(const float* y, float* py, int lane, int rot) {
+  if (rot == 128) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) py[e] = xor16<8>(y[e]);
+    return;
+  }
+  const int l16 = lane & 15, hr = rot >> 1, step = hr >> 3, c0 = 8 * l16;
+  const int src = c0 < hr ? l16 + step : (c0 < rot ? l16 - step : l16);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) py[e] = __shfl(y[e], (lane & ~15) + src, 64);
+}
+
 // Per-head RMSNorm + split-half RoPE of one 128-channel row held by 16 lanes (8 channels each,
 // lane l16 owns channels 8*l16..8*l16+7). Fixed order: per-lane x*x sum over e, then xor 8,4,2,1.
 __device__ __forceinline__ void rms_rope8(float* x, int lane, const RR& rr, int64_t s) {
@@ -27,24 +72,17 @@ __device__ __forceinline__ void rms_rope8(float* x, int lane, const RR& rr, int6
   float ss = 0.0f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) ss = fmaf(x[e], x[e], ss);
-  ss = ss + __shfl_xor(ss, 8, 64);
-  ss = ss + __shfl_xor(ss, 4, 64);
-  ss = ss + __shfl_xor(ss, 2, 64);
-  ss = ss + __shfl_xor(ss, 1, 64);
+  ss = row_sum16(ss);
   const float r = 1.0f / sqrtf(ss / 128.0f + rr.eps);
   float w[8];
   load8(rr.w + 8 * l16, w);
   float y[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) y[e] = round_bf((r * x[e]) * w[e]);
-  const int hr = rr.rot >> 1, step = hr >> 3;  // partner lane distance in 8-channel units
+  const int hr = rr.rot >> 1;
   const int c0 = 8 * l16;
-  int src = l16;
-  if (c0 < hr) src = l16 + step;
-  else if (c0 < rr.rot) src = l16 - step;
   float py[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) py[e] = __shfl(y[e], (lane & ~15) + src, 64);
+  rope_partner8(y, py, lane, rr.rot);
   if (c0 < rr.rot) {
     const bool first = c0 < hr;
     const int i0 = first ? c0 : c0 - hr;  // rotary pair index of channel e is i0 + e
@@ -96,22 +134,15 @@ __device__ __forceinline__ void rms_rope8_pre(float* x, int lane, const RR& rr, 
   float ss = 0.0f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) ss = fmaf(x[e], x[e], ss);
-  ss = ss + __shfl_xor(ss, 8, 64);
-  ss = ss + __shfl_xor(ss, 4, 64);
-  ss = ss + __shfl_xor(ss, 2, 64);
-  ss = ss + __shfl_xor(ss, 1, 64);
+  ss = row_sum16(ss);
   const float r = 1.0f / sqrtf(ss / 128.0f + rr.eps);
   float y[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) y[e] = round_bf((r * x[e]) * w[e]);
-  const int hr = rr.rot >> 1, step = hr >> 3;
+  const int hr = rr.rot >> 1;
   const int c0 = 8 * l16;
-  int src = l16;
-  if (c0 < hr) src = l16 + step;
-  else if (c0 < rr.rot) src = l16 - step;
   float py[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) py[e] = __shfl(y[e], (lane & ~15) + src, 64);
+  rope_partner8(y, py, lane, rr.rot);
   if (c0 < rr.rot) {
     const bool first = c0 < hr;
 #pragma unroll
@@ -140,21 +171,16 @@ __device__ __forceinline__ void rms_rope8_raw(float* x, int lane, const RR& rr, 
   float ss = 0.0f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) ss = fmaf(x[e], x[e], ss);
-  ss = ss + __shfl_xor(ss, 8, 64);
-  ss = ss + __shfl_xor(ss, 4, 64);
-  ss = ss + __shfl_xor(ss, 2, 64);
-  ss = ss + __shfl_xor(ss, 1, 64);
+  ss = row_sum16(ss);
   const float r = 1.0f / sqrtf(ss / 128.0f + rr.eps);
   float y[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) y[e] = round_bf((r * x[e]) * w[e]);
-  const int hr = rr.rot >> 1, step = hr >> 3;
+  const int hr = rr.rot >> 1;
   const int c0 = 8 * l16;
   const bool first = c0 < hr, rotl = c0 < rr.rot;
-  const int src = first ? l16 + step : (rotl ? l16 - step : l16);
   float py[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) py[e] = __shfl(y[e], (lane & ~15) + src, 64);
+  rope_partner8(y, py, lane, rr.rot);
   // v_perm_b32(hi, lo, sel): selector bytes 0-3 take lo's bytes, 4-7 hi's, 0x0c gives 0x00
   const uint32_t sela = first || !rotl ? 0x01000c0cu : 0x07060c0cu;  // A: lo16(word 0) or hi16(word 1)
   const uint32_t selb = first || !rotl ? 0x03020c0cu : 0x05040c0cu;  // B: hi16(word 0) or lo16(word 1)
@@ -182,15 +208,19 @@ __device__ __forceinline__ void wht128_row(float* v, int l16) {
         v[e] = lo + hi;
         v[e + st] = lo - hi;
       }
-#pragma unroll
-  for (int m = 1; m < 16; m <<= 1) {
-    const bool hi = l16 & m;
+  auto stage = [&](auto mc) __attribute__((always_inline)) {
+    constexpr int M = decltype(mc)::value;
+    const bool hi = l16 & M;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const float y = __shfl_xor(v[e], m, 64);
+      const float y = xor16<M>(v[e]);
       v[e] = hi ? y - v[e] : v[e] + y;
     }
-  }
+  };
+  stage(std::integral_constant<int, 1>{});
+  stage(std::integral_constant<int, 2>{});
+  stage(std::integral_constant<int, 4>{});
+  stage(std::integral_constant<int, 8>{});
 #pragma unroll
   for (int e = 0; e < 8; ++e) v[e] = v[e] * 0.08838834764831845f;
 }
@@ -200,8 +230,10 @@ __device__ __forceinline__ float row_amax16(const float* v) {
   float amax = 0.0f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[e]));
-#pragma unroll
-  for (int m = 8; m > 0; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 64));
+  amax = fmaxf(amax, xor16<8>(amax));
+  amax = fmaxf(amax, xor16<4>(amax));
+  amax = fmaxf(amax, xor16<2>(amax));
+  amax = fmaxf(amax, xor16<1>(amax));
   return amax;
 }
 
