@@ -115,12 +115,13 @@ def test_gemm_persistent_epilogues(dev, m, n, k):
     assert og.rel_l2(got, bf16_to_f32(og.fp8_gemm(fq, xs, fwq, ws))) < 1e-2
 
 
-@pytest.mark.parametrize("m,n,k", [(4500, 4112, 512), (9000, 8200, 256), (700, 784, 1024)])
+@pytest.mark.parametrize("m,n,k", [(4500, 4112, 512), (9000, 8200, 256), (700, 784, 1024), (300, 264, 512)])
 def test_gemm_tile_counters(dev, m, n, k):
     """The persistent kernel with per-XCD tile counters (ctr, the Python layer's default) and with the fixed tile
     shares (ctr NULL) against the oracle's int32 accumulators, bit-exact; two calls in a row on one counter buffer
-    (each call clears it). 306 and 1155 tiles (more than one per CU, so workgroups claim and steal) and 12 tiles
-    (fewer than the CUs: every workgroup's first tile is its last)."""
+    (each call clears it). 306 and 1155 tiles (more than one per CU, so workgroups claim and steal), 12 tiles
+    (fewer than the CUs: every workgroup's first tile is its last) and 4 tiles (fewer than the 8 XCDs: some XCD
+    ranges are empty and every claim returns none)."""
     import ctypes
     import torch
     from rapid_h3 import _native as nat
