@@ -264,3 +264,29 @@ def test_fp8_full_size_c3(dev, n, k):
     assert og.rel_l2(got, ref) < 1e-2
     exact = bf16_to_f32(xr).astype(np.float64) @ bf16_to_f32(to_np(w)).astype(np.float64).T
     assert og.rel_l2(got, exact) < 0.08
+
+
+def test_gemm_counter_buffers_per_stream(dev):
+    """The Python layer's tile-counter buffers: one per (device, stream), reused on its stream, never shared between
+    streams (calls on different streams may run at once); a GEMM on a second stream matches the first bit for bit."""
+    import torch
+    from rapid_h3 import _native as nat
+    from rapid_h3 import gemm
+    a = nat.gemm_ctr(dev).value
+    assert nat.gemm_ctr(dev).value == a
+    s = torch.cuda.Stream(device=dev)
+    with torch.cuda.stream(s):
+        b = nat.gemm_ctr(dev).value
+        assert nat.gemm_ctr(dev).value == b
+    assert a != b
+    rng = np.random.default_rng(3)
+    xq = to_dev(np.clip(np.rint(rng.standard_normal((2000, 512)) * 30), -127, 127).astype(np.int8), dev)
+    wq = to_dev(np.clip(np.rint(rng.standard_normal((2048, 512)) * 30), -127, 127).astype(np.int8), dev)
+    xs = to_dev((rng.random((2000, 1)) * 1e-3 + 1e-4).astype(np.float32), dev)
+    ws = to_dev((rng.random((1, 2048)) * 1e-3 + 1e-4).astype(np.float32), dev)
+    y0 = gemm.int8_gemm(xq, xs, wq, ws)
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        y1 = gemm.int8_gemm(xq, xs, wq, ws)
+    torch.cuda.synchronize()
+    assert torch.equal(y0.view(torch.int16), y1.view(torch.int16))
