@@ -197,6 +197,13 @@ int rh3_gemm_fp8(const uint8_t* xq, int64_t ldx, const float* xs, const uint8_t*
                  const float* ws, const uint16_t* bias, uint16_t* out, int64_t ldo,
                  int64_t M, int64_t N, int64_t K, int32_t* ctr, hipStream_t stream);
 
+/* The raw fp32 accumulators acc [M, N] (row stride ldc) of the FP8 GEMM, before any scale: the product
+ * torch._scaled_mm forms before it applies its scales, for outputs other than bf16.
+ * replaces the fp16 / fp32 out_dtype of torch._scaled_mm in kernels.linear's fp8_tensor mode
+ * (kernels.py:124-127); the caller applies (acc * scale_a) * scale_b and rounds to its dtype. */
+int rh3_gemm_fp8_acc(const uint8_t* xq, int64_t ldx, const uint8_t* wq, int64_t ldw, float* acc, int64_t ldc,
+                     int64_t M, int64_t N, int64_t K, int32_t* ctr, hipStream_t stream);
+
 /* ---------------------------------------------------------------------------------------------
  * INT8 flash attention, head_dim 128, non-causal. q [Sq, H, 128], k and v [Sk, H, 128] bf16 with any
  * token / head strides (elements; the 128 channels contiguous). Q and K are quantized per
@@ -219,10 +226,13 @@ int rh3_int8_attention(const uint16_t* q, int64_t q_ss, int64_t q_sh,
 
 /* rh3_int8_attention without a workspace argument, for callers that cannot allocate device memory (code
  * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart in the
- * reference. The pre-pass operands live in a 64 MiB device array of the library, one per GPU, held until the
- * process ends; sizes whose operands need more (rh3_attention_workspace_bytes less the split partials, roughly
- * 512 bytes per token and head) fail with RH3_EINVAL. The call allocates nothing and calls no allocating
- * routine. All calls on one GPU share the array: calls that overlap there (two streams, two host threads) race. */
+ * reference. The pre-pass operands live in a 16 MiB device array of the library, one per GPU, held until the
+ * process ends (every process that loads the library holds it on each GPU where the module loads, called or not);
+ * sizes whose operands need more (rh3_attention_workspace_bytes less the split partials, roughly 512 bytes per
+ * token and head, so about 32k token-heads) fail with RH3_EINVAL. The call allocates no device memory and calls no
+ * allocating routine, except that the first call on a device resolves the array's address (hipGetSymbolAddress),
+ * which may load the code object: make one call per device before capturing it in a graph. All calls on one GPU
+ * share the array: calls that overlap there (two streams, two host threads) race. */
 int rh3_int8_attention_noalloc(const uint16_t* q, int64_t q_ss, int64_t q_sh,
                                const uint16_t* k, int64_t k_ss, int64_t k_sh,
                                const uint16_t* v, int64_t v_ss, int64_t v_sh,
@@ -240,6 +250,16 @@ int rh3_int8_attention_rr(const uint16_t* q, int64_t q_ss, int64_t q_sh,
                           const uint16_t* qw, const uint16_t* kw, float eps, float scale, int smooth_k,
                           uint16_t* out, int64_t o_ss, int64_t o_sh,
                           void* workspace, int64_t workspace_bytes, hipStream_t stream);
+
+/* Per-head RMSNorm (qw / kw [128] bf16, eps) and split-half RoPE (tab as above, rot 96 or 128) of q and k
+ * [S, H, 128] bf16 in place (token / head strides in elements, multiples of 8): the prologue the *_rr entry points
+ * and the pre-passes apply, on its own and bit-identical to it, for a caller that hands the roped q / k to another
+ * attention.
+ * replaces comfy_kitchen's ck.rms_rope_split_half_(q, k, rope_freqs, qw, kw, epsilon, rot_dim) (comfy-kitchen
+ * 0.2.39, not vendored), called by _fused_block and _rr_check (__init__.py:297, :340) */
+int rh3_rms_rope_qk(uint16_t* q, int64_t q_ss, int64_t q_sh, uint16_t* k, int64_t k_ss, int64_t k_sh,
+                    int64_t S, int64_t H, const uint16_t* tab, int rot, const uint16_t* qw, const uint16_t* kw,
+                    float eps, hipStream_t stream);
 
 /* Pre-pass operands for verification (int8_prepass, attn_int8.cu:2851-2879): writes into the
  * workspace and returns pointers to q8 [H, Sqpad, 128] int8, qs [H, Sqpad/128] fp32, k8, ks,

@@ -600,6 +600,34 @@ int forward(const Work& w, int64_t Sq, int64_t Sk, int64_t H, float scale, uint1
   return launch_status("attention forward");
 }
 
+// ------------------------------------------------------------------ standalone RMSNorm + RoPE (in place)
+// The per-head prologue of the pre-pass on its own, for callers that hand the roped q / k to another attention:
+// 16 lanes per (token, head) row, heads fastest (rows of one token are contiguous in the qkv output), grid.y 0 = q,
+// 1 = k. rms_rope8 is the function the pre-pass applies, so the results are the pre-pass's own operands bit for bit.
+// Lanes past the last row compute on a clamped row (the RoPE partner exchange needs every lane) and store nothing.
+__global__ void __launch_bounds__(256) rms_rope_kernel(uint16_t* q, int64_t q_ss, int64_t q_sh, uint16_t* k,
+                                                       int64_t k_ss, int64_t k_sh, int64_t S, int64_t H, RR rq,
+                                                       RR rk) {
+  const int lane = threadIdx.x & 63;
+  const bool isk = blockIdx.y != 0;
+  const int64_t rows = S * H;
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * 16 + (threadIdx.x >> 4);
+  const int64_t rc = r < rows ? r : rows - 1;
+  const int64_t s = rc / H, h = rc - s * H;
+  uint16_t* p = (isk ? k + s * k_ss + h * k_sh : q + s * q_ss + h * q_sh) + 8 * (lane & 15);
+  float x[8];
+  load8(p, x);
+  rms_rope8(x, lane, isk ? rk : rq, s);
+  if (r < rows) {
+    uint4 o;
+    o.x = pack_bf2(x[0], x[1]);
+    o.y = pack_bf2(x[2], x[3]);
+    o.z = pack_bf2(x[4], x[5]);
+    o.w = pack_bf2(x[6], x[7]);
+    *reinterpret_cast<uint4*>(p) = o;
+  }
+}
+
 int check_rr(const char* name, const uint16_t* tab, int rot, const uint16_t* qw, const uint16_t* kw) {
   RH3_REQUIRE(tab && qw && kw, "%s: tab, qw and kw are required", name);
   RH3_REQUIRE(rot == 96 || rot == 128, "%s: rot_dim %d (96 or 128 supported)", name, rot);
@@ -612,9 +640,10 @@ int check_rr(const char* name, const uint16_t* tab, int rot, const uint16_t* qw,
 
 // ------------------------------------------------------------------ allocation-free variant
 // The workspace of rh3_int8_attention_noalloc: a file-scope device array, one copy per GPU for the life of the
-// process. Host code never passes `scratch` itself (in host code the name is only a stand-in): each device's
+// process. It is part of the code object, so every process that loads the library holds these 16 MiB on each GPU
+// where the module is loaded, whether or not it calls this entry point. Host code never passes `scratch` itself (in host code the name is only a stand-in): each device's
 // address comes from hipGetSymbolAddress once, with that device current, and is kept in g_scratch.
-constexpr int64_t NOALLOC_SCRATCH_BYTES = int64_t{64} << 20;
+constexpr int64_t NOALLOC_SCRATCH_BYTES = int64_t{16} << 20;
 static __device__ __align__(256) char scratch[NOALLOC_SCRATCH_BYTES];
 
 namespace rh3 {
@@ -648,7 +677,7 @@ int scratch_of(hipStream_t stream, void** out) {
 
 using namespace rh3;
 
-// rh3_int8_attention without a workspace argument: the pre-pass operands live in this GPU's 64 MiB scratch array,
+// rh3_int8_attention without a workspace argument: the pre-pass operands live in this GPU's 16 MiB scratch array,
 // and the main kernel runs every workgroup whole (no split last round, whose partials would need more room). The
 // pre-pass writes every element the main kernel reads, so nothing is cleared first. Calls that overlap on one GPU
 // (two streams, or two host threads) share the array and race.
@@ -790,4 +819,23 @@ extern "C" int rh3_int8_attention_rr(const uint16_t* q, int64_t q_ss, int64_t q_
   const RR rq{tab, qw, eps, rot}, rk{tab, kw, eps, rot};
   if (int e = prepass(q, q_ss, q_sh, k, k_ss, k_sh, v, v_ss, v_sh, S, S, H, rq, rk, smooth_k, w, stream)) return e;
   return forward(w, S, S, H, scale, out, o_ss, o_sh, stream);
+}
+
+// RMSNorm + RoPE of q and k in place ([S, H, 128] bf16, any token / head strides in elements, multiples of 8),
+// the prologue every rh3_*_rr / prepass entry point applies before quantizing.
+extern "C" int rh3_rms_rope_qk(uint16_t* q, int64_t q_ss, int64_t q_sh, uint16_t* k, int64_t k_ss, int64_t k_sh,
+                               int64_t S, int64_t H, const uint16_t* tab, int rot, const uint16_t* qw,
+                               const uint16_t* kw, float eps, hipStream_t stream) {
+  clear_error();
+  RH3_REQUIRE(S >= 0 && H > 0, "rms_rope_qk: bad sizes S=%lld H=%lld", (long long)S, (long long)H);
+  if (S == 0) return RH3_OK;
+  if (int e = check_rr("rms_rope_qk", tab, rot, qw, kw)) return e;
+  RH3_REQUIRE(q && k && aligned16(q) && aligned16(k), "rms_rope_qk: q and k must be 16-byte aligned");
+  RH3_REQUIRE(q_ss % 8 == 0 && q_sh % 8 == 0 && k_ss % 8 == 0 && k_sh % 8 == 0,
+              "rms_rope_qk: strides must be multiples of 8 elements");
+  const int64_t blocks = (S * H + 15) / 16;
+  RH3_REQUIRE(blocks < (int64_t{1} << 31), "rms_rope_qk: S*H=%lld rows exceed the grid", (long long)(S * H));
+  hipLaunchKernelGGL(rms_rope_kernel, dim3(static_cast<unsigned>(blocks), 2), dim3(256), 0, stream, q, q_ss, q_sh,
+                     k, k_ss, k_sh, S, H, RR{tab, qw, eps, rot}, RR{tab, kw, eps, rot});
+  return launch_status("rms_rope_qk");
 }

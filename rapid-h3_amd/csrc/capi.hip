@@ -42,4 +42,4 @@ int device_cus() {
 
 extern "C" const char* rh3_last_error(void) { return rh3::g_error.c_str(); }
 
-extern "C" int rh3_abi_version(void) { return 2; }
+extern "C" int rh3_abi_version(void) { return 3; }

@@ -6,7 +6,7 @@
 //   EPI_SWIGLU  g, u = bf16(y) over the swiglu_perm interleave; h = bf16((g * sigmoid(g)) * u) at n / 2
 //   EPI_GATED   resid = bf16(fma(bf16(y), gate[n], resid))     (in place)
 //   EPI_GATED_ROWS  the same with gate[gidx[m]][n], a gate table row per output row (per-token modulation)
-//   EPI_ACC     raw int32 accumulators (verification)
+//   EPI_ACC     raw accumulators: int32 (int8 operands) or fp32 (e4m3 operands)
 //   EPI_QKV     the qkv projection with the attention pre-pass partly fused (the reference's config 3xx,
 //               fp8_rowwise.cu:108-272): the 256x256 tile (two heads of q, k or v, 256 tokens = one statistics
 //               chunk) is staged whole in LDS; q: per-head RMSNorm + RoPE and the Q quantization of the
@@ -99,6 +99,10 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
   const float sig = __builtin_amdgcn_rcpf(1.0f + __expf(-g));
   return (g * sig) * u;
 }
+
+// EPI_ACC stores the accumulator registers as they are: int32 values (int8) or fp32 bit patterns (e4m3)
+__device__ __forceinline__ int acc_bits(int v) { return v; }
+__device__ __forceinline__ int acc_bits(float v) { return __builtin_bit_cast(int, v); }
 
 template <bool FP8>
 struct Mma;
@@ -276,7 +280,6 @@ __global__ void __launch_bounds__(GEMM_NW * 64, GEMM_NW / 4) gemm_kernel(const G
   // epilogue: acc[i][j] register r holds m = m0 + wm*128 + j*32 + l32,
   //           n = n0 + wn*64 + i*32 + 8*(r/4) + 4*g + (r%4)
   if constexpr (EPI == EPI_ACC) {
-    static_assert(!FP8, "raw accumulators are an int8 feature");
 #pragma unroll
     for (int j = 0; j < TJ; ++j) {
       const int64_t m = m0 + wm * WM + j * 32 + l32;
@@ -287,10 +290,10 @@ __global__ void __launch_bounds__(GEMM_NW * 64, GEMM_NW / 4) gemm_kernel(const G
           const int64_t n = n0 + wn * WN + i * 32 + 8 * rq + 4 * g;
           if (m < a.M && n < a.N) {
             int4 v;
-            v.x = acc[i][j][4 * rq + 0];
-            v.y = acc[i][j][4 * rq + 1];
-            v.z = acc[i][j][4 * rq + 2];
-            v.w = acc[i][j][4 * rq + 3];
+            v.x = acc_bits(acc[i][j][4 * rq + 0]);
+            v.y = acc_bits(acc[i][j][4 * rq + 1]);
+            v.z = acc_bits(acc[i][j][4 * rq + 2]);
+            v.w = acc_bits(acc[i][j][4 * rq + 3]);
             *reinterpret_cast<int4*>(static_cast<int32_t*>(a.out) + m * a.ldo + n) = v;
           }
         }
@@ -840,7 +843,6 @@ __global__ void __launch_bounds__(512, 2) gemm_persistent_kernel(const GemmArgs 
     // epilogue: acc[i][j] register r holds m = m0 + wm*128 + j*32 + l32,
     //           n = n0 + wn*64 + i*32 + 8*(r/4) + 4*g + (r%4)
     if constexpr (EPI == EPI_ACC) {
-      static_assert(!FP8, "raw accumulators are an int8 feature");
 #pragma unroll
       for (int j = 0; j < TJ; ++j) {
         const int64_t m = m0 + wm * WM + j * 32 + l32;
@@ -851,10 +853,10 @@ __global__ void __launch_bounds__(512, 2) gemm_persistent_kernel(const GemmArgs 
             const int64_t n = n0 + wn * WN + i * 32 + 8 * rq + 4 * g;
             if (m < a.M && n < a.N) {
               int4 v;
-              v.x = acc[i][j][4 * rq + 0];
-              v.y = acc[i][j][4 * rq + 1];
-              v.z = acc[i][j][4 * rq + 2];
-              v.w = acc[i][j][4 * rq + 3];
+              v.x = acc_bits(acc[i][j][4 * rq + 0]);
+              v.y = acc_bits(acc[i][j][4 * rq + 1]);
+              v.z = acc_bits(acc[i][j][4 * rq + 2]);
+              v.w = acc_bits(acc[i][j][4 * rq + 3]);
               *reinterpret_cast<int4*>(static_cast<int32_t*>(a.out) + m * a.ldo + n) = v;
             }
           }
@@ -1133,4 +1135,15 @@ extern "C" int rh3_gemm_fp8(const uint8_t* xq, int64_t ldx, const float* xs, con
   RH3_REQUIRE((reinterpret_cast<uintptr_t>(ctr) & 3) == 0, "%s: ctr must be 4-byte aligned", "gemm_fp8");
   a.ctr = reinterpret_cast<int*>(ctr);
   return run<true, EPI_PLAIN>(a, stream, "gemm_fp8");
+}
+
+extern "C" int rh3_gemm_fp8_acc(const uint8_t* xq, int64_t ldx, const uint8_t* wq, int64_t ldw, float* acc,
+                                int64_t ldc, int64_t M, int64_t N, int64_t K, int32_t* ctr, hipStream_t stream) {
+  clear_error();
+  if (int e = check("gemm_fp8_acc", xq, ldx, wq, ldw, acc, ldc, M, N, K, N)) return e;
+  GemmArgs a{reinterpret_cast<const int8_t*>(xq), ldx, reinterpret_cast<const int8_t*>(wq), ldw, nullptr, nullptr,
+             nullptr, nullptr, acc, ldc, M, N, K, 0, 0};
+  RH3_REQUIRE((reinterpret_cast<uintptr_t>(ctr) & 3) == 0, "%s: ctr must be 4-byte aligned", "gemm_fp8_acc");
+  a.ctr = reinterpret_cast<int*>(ctr);
+  return run<true, EPI_ACC>(a, stream, "gemm_fp8_acc");
 }

@@ -10,7 +10,7 @@ import os
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get("RH3_LIB", os.path.join(_HERE, "librh3.so"))
 
-ABI_VERSION = 2  # rh3_abi_version() of the library these signatures describe
+ABI_VERSION = 3  # rh3_abi_version() of the library these signatures describe
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int64
@@ -42,11 +42,13 @@ SIGNATURES = {
     "rh3_gemm_i8_acc": ([_P, _I, _P, _I, _P, _I, _I, _I, _I, _P, _P], _C),
     "rh3_gemm_i8_qkv": ([_P, _I, _P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _P, _C, _P, _P, _F, _C, _C, _P, _I, _P], _C),
     "rh3_gemm_fp8": ([_P, _I, _P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _P, _P], _C),
+    "rh3_gemm_fp8_acc": ([_P, _I, _P, _I, _P, _I, _I, _I, _I, _P, _P], _C),
     "rh3_attention_workspace_bytes": ([_I, _I, _I], ctypes.c_int64),
     "rh3_int8_attention": ([_P, _I, _I, _P, _I, _I, _P, _I, _I, _I, _I, _I, _F, _C, _P, _I, _I, _P, _I, _P], _C),
     "rh3_int8_attention_noalloc": ([_P, _I, _I, _P, _I, _I, _P, _I, _I, _I, _I, _I, _F, _C, _P, _I, _I, _P], _C),
     "rh3_int8_attention_rr": ([_P, _I, _I, _P, _I, _I, _P, _I, _I, _I, _I, _P, _C, _P, _P, _F, _F, _C, _P, _I, _I,
                                _P, _I, _P], _C),
+    "rh3_rms_rope_qk": ([_P, _I, _I, _P, _I, _I, _I, _I, _P, _C, _P, _P, _F, _P], _C),
     "rh3_attention_forward": ([_I, _I, _I, _F, _P, _I, _I, _P, _I, _P], _C),
     "rh3_attention_prepass": ([_P, _I, _I, _P, _I, _I, _P, _I, _I, _I, _I, _I, _P, _C, _P, _P, _F, _C, _P, _I,
                                ctypes.POINTER(ctypes.c_void_p), _P], _C),
@@ -124,14 +126,19 @@ _GEMM_CTR = {}
 
 
 def gemm_ctr(device):
-    """The GEMM tile counters (8 int32) of torch's current stream on `device`: one buffer per (device, stream), kept
-    for the life of the process, so calls on one stream share it in order and calls on different streams never do
-    (the ownership rule of the `ctr` argument of the rh3_gemm_* entry points)."""
+    """The GEMM tile counters (8 int32) for a call on torch's current stream of `device`, as a tensor the caller
+    holds until the call is enqueued. Eagerly: one buffer per (device, stream), kept for the life of the process, so
+    calls on one stream share it in order and calls on different streams never do (the ownership rule of the `ctr`
+    argument of the rh3_gemm_* entry points). Under stream capture: a new buffer per call from the caching allocator,
+    which then belongs to the graph's private pool. Graphs captured on the same capture stream would otherwise bake
+    in one shared buffer and race when replayed on two streams at once."""
     import torch
     st = torch.cuda.current_stream(device)
+    if torch.cuda.is_current_stream_capturing():
+        return torch.empty(64, dtype=torch.int32, device=st.device)
     key = (st.device.index, st.cuda_stream)
     t = _GEMM_CTR.get(key)
     if t is None:
         t = torch.zeros(64, dtype=torch.int32, device=st.device)
         _GEMM_CTR[key] = t
-    return ctypes.c_void_p(t.data_ptr())
+    return t

@@ -184,6 +184,22 @@ def _check_rr(q, tab, qw, kw):
     return tab.contiguous(), qw.contiguous(), kw.contiguous(), rot
 
 
+def rms_rope_(q, k, tab, qw, kw, eps):
+    """Per-head RMSNorm (qw / kw [128] bf16, eps) and split-half RoPE (tab [1, S, 1, rot/2, 2, 2] bf16) of q and k
+    ([S, H, 128] bf16, strided ok) in place, bit-identical to the prologue the *_rr pre-passes fuse (rh3_rms_rope_qk).
+    The stand-in for comfy_kitchen's ck.rms_rope_split_half_(q, k, rope_freqs, qw, kw, epsilon, rot_dim) that
+    _fused_block calls before handing q, k to another attention (__init__.py:297)."""
+    for t, n in ((q, "q"), (k, "k")):
+        if t.ndim != 3 or t.shape[2] != D or t.dtype != torch.bfloat16 or t.stride(2) != 1 or not t.is_cuda:
+            raise RuntimeError(f"rms_rope_: {n} must be a bf16 [S, H, 128] GPU tensor with contiguous last dim")
+    if q.shape != k.shape:
+        raise RuntimeError("rms_rope_: q and k shapes must match")
+    tab, qw, kw, rot = _check_rr(q, tab, qw, kw)
+    nat.call("rh3_rms_rope_qk", nat.ptr(q), q.stride(0), q.stride(1), nat.ptr(k), k.stride(0), k.stride(1),
+             q.shape[0], q.shape[1], nat.ptr(tab), rot, nat.ptr(qw), nat.ptr(kw), float(eps), nat.stream(q.device))
+    return q, k
+
+
 def attention_rr(q, k, v, tab, qw, kw, eps, scale=None, config=94, smooth_k=True, smooth_v=True, rotate=True,
                  out=None):
     """attention() on the raw qkv-projection q, k ([S, H, 128] bf16, strided ok) with the per-head

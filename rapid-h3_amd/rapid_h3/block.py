@@ -95,7 +95,7 @@ _QUANTIZERS = {
 
 
 def fused_block(x, w: BlockWeights, mod, segments, rope_tab, idx=None, mark=None, trace=None, attn_config=None,
-                text_bias=None, fuse_qkv=False):
+                text_bias=None, fuse_qkv=False, attn_fn=None, attn_check=None):
     """One DiT block forward on x [S, hidden] bf16 (modified in place). mod = (shift_msa, scale_msa,
     gate_msa, shift_mlp, scale_mlp, gate_mlp), each [R, hidden]; rope_tab [1, S, 1, rot/2, 2, 2] bf16.
     mark: optional callable, called with each name of PHASES after that phase is enqueued (a timer
@@ -107,7 +107,12 @@ def fused_block(x, w: BlockWeights, mod, segments, rope_tab, idx=None, mark=None
     attention's Q operands and K / V statistics itself (gemm.int8_gemm_qkv, the reference's config 3xx
     path), so the pre-pass skips its Q pass and statistics passes; the result is the same bit for bit. Off by
     default: at the benchmark shape the longer GEMM epilogue costs 0.4-0.6 ms more than the pre-pass passes it
-    removes."""
+    removes.
+    attn_fn(q, k, v) -> o [1, H, S, 128] bf16: the unfused attention route of the reference (__init__.py:295-305): q and
+    k ([S, H, 128] views of the qkv output) get the per-head RMSNorm + RoPE in place (attention.rms_rope_), then attn_fn
+    computes the attention (an installed override, or the stock attention); attn_config and text_bias do not apply.
+    attn_check(q, k, v, o): called after the fused attention with the raw q, k, v views and o (the reference's
+    config-2xx check, __init__.py:303-304)."""
     shift_msa, scale_msa, gate_msa, shift_mlp, scale_mlp, gate_mlp = mod
     tick = mark or (lambda name: None)
     keep = trace.__setitem__ if trace is not None else (lambda k, v: None)
@@ -115,55 +120,18 @@ def fused_block(x, w: BlockWeights, mod, segments, rope_tab, idx=None, mark=None
         raise ValueError(f"fused_block: recipe {w.recipe!r} (int8_rowwise or int8_rot)")
     norm_mod_q, heads_q, rows_q = _QUANTIZERS[w.recipe]
     s = x.shape[0]
-    h = w.heads
     if idx is None:
         idx = row_index(segments, s, x.device)
     xq, xs = norm_mod_q(x, w.norm1_w, w.eps, idx, shift_msa, scale_msa)
     keep("xq1", xq), keep("xs1", xs)
     tick("quant_norm1")
-    numerics = 0 if attn_config is None else 1
-    if attn_config is None:
-        if text_bias is not None:
-            raise RuntimeError("text bias: needs the production attention (attn_config 90 or 94)")
+    if attn_fn is not None:
+        if attn_config is not None or text_bias is not None or fuse_qkv:
+            raise RuntimeError("fused_block: attn_fn runs the unfused attention route (no attn_config, text_bias or "
+                               "fuse_qkv)")
+        o = _unfused_attention(xq, xs, w, rope_tab, s, tick, keep, attn_fn)
     else:
-        _attn._production(attn_config, "fused_block")
-        if 60 <= int(attn_config) % 100 < 70:
-            raise RuntimeError("configs 60-69 have no fused rms/rope path")    # attn_int8.cu:2606
-        if text_bias is not None and text_bias[0] and int(attn_config) % 100 not in (90, 94):
-            raise RuntimeError("text bias: config 94 or 90 only")
-    f8_tile = _attn._fp8_tile(attn_config)     # configs 50-56: the FP8 P.V kernel
-    fused = fuse_qkv and h % 2 == 0 and not f8_tile
-    if fused:
-        wsb = (_attn.workspace if numerics == 0 else _attn.workspace_u8)(s, s, h, x.device)
-        qkv = _gemm.int8_gemm_qkv(xq, xs, w.qkv.q, w.qkv.scale, h, wsb, numerics, tab=rope_tab, qw=w.q_norm_w,
-                                  kw=w.k_norm_w, eps=w.qk_eps)
-    else:
-        qkv = _gemm.int8_gemm(xq, xs, w.qkv.q, w.qkv.scale)
-    keep("qkv", qkv)
-    tick("gemm_qkv")
-    q, k, v = (t.view(s, h, D) for t in qkv.split(h * D, dim=-1))
-    o = torch.empty(1, h, s, D, dtype=x.dtype, device=x.device)
-    # attention_rr = pre-pass (RMSNorm + RoPE + stats + INT8) then the main kernel, as two calls
-    if fused:
-        pp = _attn.prepass_qkv(k, v, wsb, numerics, rope_tab, w.k_norm_w, w.qk_eps)
-    elif numerics == 0:
-        pp = _attn.prepass(q, k, v, rope_tab, w.q_norm_w, w.k_norm_w, w.qk_eps)
-    elif f8_tile:
-        pp = _attn.prepass_f8(q, k, v, rope_tab, w.q_norm_w, w.k_norm_w, w.qk_eps)
-    else:
-        pp = _attn.prepass_u8(q, k, v, rope_tab, w.q_norm_w, w.k_norm_w, w.qk_eps)
-    keep("q8", pp["q8"]), keep("qs", pp["qs"])
-    tick("attn_prepass")
-    if numerics == 0:
-        _attn.forward(pp, s, out=o[0].transpose(0, 1))
-    elif f8_tile:
-        _attn.forward_f8(pp, s, out=o[0].transpose(0, 1), tile=f8_tile)
-    else:
-        nbias, bias = text_bias if text_bias is not None else (0, 0.0)
-        _attn.forward_u8(pp, s, out=o[0].transpose(0, 1), nbias=nbias, bias=bias)
-    keep("o", o)
-    tick("attn_main")
-    del qkv, pp
+        o = _fused_attention(xq, xs, w, rope_tab, s, tick, keep, attn_config, text_bias, fuse_qkv, attn_check)
     oq, os_ = heads_q(o[0])
     keep("oq", oq), keep("os", os_)
     tick("quant_heads")
@@ -185,6 +153,76 @@ def fused_block(x, w: BlockWeights, mod, segments, rope_tab, idx=None, mark=None
     x = gemm_gated(hq, hs, w.fc2, x, gate_mlp, segments)
     tick("gemm_down_gated")
     return x
+
+
+def _unfused_attention(xq, xs, w, rope_tab, s, tick, keep, attn_fn):
+    """QKV GEMM, RMSNorm + RoPE of q, k in place, then attn_fn (the reference's route when the installed attention
+    override carries no fused-path tag, __init__.py:295-305)."""
+    h = w.heads
+    qkv = _gemm.int8_gemm(xq, xs, w.qkv.q, w.qkv.scale)
+    keep("qkv", qkv)
+    tick("gemm_qkv")
+    q, k, v = (t.view(s, h, D) for t in qkv.split(h * D, dim=-1))
+    _attn.rms_rope_(q, k, rope_tab, w.q_norm_w, w.k_norm_w, w.qk_eps)
+    tick("attn_prepass")
+    o = attn_fn(q, k, v)
+    if tuple(o.shape) != (1, h, s, D) or o.dtype != torch.bfloat16 or o.stride(-1) != 1:
+        raise RuntimeError(f"fused_block: attn_fn must return bf16 [1, {h}, {s}, {D}], got {o.dtype} "
+                           f"{tuple(o.shape)}")
+    keep("o", o)
+    tick("attn_main")
+    return o
+
+
+def _fused_attention(xq, xs, w, rope_tab, s, tick, keep, attn_config, text_bias, fuse_qkv, attn_check):
+    """QKV GEMM and this build's INT8 attention with the RMSNorm + RoPE in its pre-pass (attention_rr's two calls)."""
+    h = w.heads
+    x_dev = xq.device
+    numerics = 0 if attn_config is None else 1
+    if attn_config is None:
+        if text_bias is not None:
+            raise RuntimeError("text bias: needs the production attention (attn_config 90 or 94)")
+    else:
+        _attn._production(attn_config, "fused_block")
+        if 60 <= int(attn_config) % 100 < 70:
+            raise RuntimeError("configs 60-69 have no fused rms/rope path")    # attn_int8.cu:2606
+        if text_bias is not None and text_bias[0] and int(attn_config) % 100 not in (90, 94):
+            raise RuntimeError("text bias: config 94 or 90 only")
+    f8_tile = _attn._fp8_tile(attn_config)     # configs 50-56: the FP8 P.V kernel
+    fused = fuse_qkv and h % 2 == 0 and not f8_tile
+    if fused:
+        wsb = (_attn.workspace if numerics == 0 else _attn.workspace_u8)(s, s, h, x_dev)
+        qkv = _gemm.int8_gemm_qkv(xq, xs, w.qkv.q, w.qkv.scale, h, wsb, numerics, tab=rope_tab, qw=w.q_norm_w,
+                                  kw=w.k_norm_w, eps=w.qk_eps)
+    else:
+        qkv = _gemm.int8_gemm(xq, xs, w.qkv.q, w.qkv.scale)
+    keep("qkv", qkv)
+    tick("gemm_qkv")
+    q, k, v = (t.view(s, h, D) for t in qkv.split(h * D, dim=-1))
+    o = torch.empty(1, h, s, D, dtype=torch.bfloat16, device=x_dev)
+    # attention_rr = pre-pass (RMSNorm + RoPE + stats + INT8) then the main kernel, as two calls
+    if fused:
+        pp = _attn.prepass_qkv(k, v, wsb, numerics, rope_tab, w.k_norm_w, w.qk_eps)
+    elif numerics == 0:
+        pp = _attn.prepass(q, k, v, rope_tab, w.q_norm_w, w.k_norm_w, w.qk_eps)
+    elif f8_tile:
+        pp = _attn.prepass_f8(q, k, v, rope_tab, w.q_norm_w, w.k_norm_w, w.qk_eps)
+    else:
+        pp = _attn.prepass_u8(q, k, v, rope_tab, w.q_norm_w, w.k_norm_w, w.qk_eps)
+    keep("q8", pp["q8"]), keep("qs", pp["qs"])
+    tick("attn_prepass")
+    if numerics == 0:
+        _attn.forward(pp, s, out=o[0].transpose(0, 1))
+    elif f8_tile:
+        _attn.forward_f8(pp, s, out=o[0].transpose(0, 1), tile=f8_tile)
+    else:
+        nbias, bias = text_bias if text_bias is not None else (0, 0.0)
+        _attn.forward_u8(pp, s, out=o[0].transpose(0, 1), nbias=nbias, bias=bias)
+    keep("o", o)
+    tick("attn_main")
+    if attn_check is not None:
+        attn_check(q, k, v, o)
+    return o
 
 
 def fused_mlp(x, fc1, fc2, recipe="int8_rot", trace=None):

@@ -38,8 +38,9 @@ def int8_gemm(xq, xs, wq, ws, bias=None, config=2):
     if bias is not None:
         bias = bias.to(torch.bfloat16).contiguous()
     out = torch.empty((m, n), device=xq.device, dtype=torch.bfloat16)
+    ctr = nat.gemm_ctr(xq.device)     # held until the launch is enqueued
     nat.call("rh3_gemm_i8", nat.ptr(xq), xq.stride(0), nat.ptr(xs), nat.ptr(wq), wq.stride(0), nat.ptr(ws),
-             nat.ptr(bias), nat.ptr(out), out.stride(0), m, n, k, nat.gemm_ctr(xq.device),
+             nat.ptr(bias), nat.ptr(out), out.stride(0), m, n, k, nat.ptr(ctr),
              nat.stream(xq.device))
     return out
 
@@ -50,8 +51,9 @@ def int8_gemm_acc(xq, wq):
     m, k = xq.shape
     n = wq.shape[0]
     acc = torch.empty((m, n), device=xq.device, dtype=torch.int32)
+    ctr = nat.gemm_ctr(xq.device)     # held until the launch is enqueued
     nat.call("rh3_gemm_i8_acc", nat.ptr(xq), xq.stride(0), nat.ptr(wq), wq.stride(0), nat.ptr(acc), acc.stride(0),
-             m, n, k, nat.gemm_ctr(xq.device),
+             m, n, k, nat.ptr(ctr),
              nat.stream(xq.device))
     return acc
 
@@ -66,10 +68,24 @@ def fp8_gemm(xq, xs, wq, ws, bias=None, config=2, fast_accum=True):
     if bias is not None:
         bias = bias.to(torch.bfloat16).contiguous()
     out = torch.empty((m, n), device=xq.device, dtype=torch.bfloat16)
+    ctr = nat.gemm_ctr(xq.device)     # held until the launch is enqueued
     nat.call("rh3_gemm_fp8", nat.ptr(xq), xq.stride(0), nat.ptr(xs), nat.ptr(wq), wq.stride(0), nat.ptr(ws),
-             nat.ptr(bias), nat.ptr(out), out.stride(0), m, n, k, nat.gemm_ctr(xq.device),
+             nat.ptr(bias), nat.ptr(out), out.stride(0), m, n, k, nat.ptr(ctr),
              nat.stream(xq.device))
     return out
+
+
+def fp8_gemm_acc(xq, wq):
+    """Raw fp32 accumulators xq @ wq^T [M, N] of the FP8 GEMM, no scales applied (the product torch._scaled_mm
+    scales for a non-bf16 out_dtype)."""
+    _check(xq, wq, FP8, "fp8_gemm_acc")
+    m, k = xq.shape
+    n = wq.shape[0]
+    acc = torch.empty((m, n), device=xq.device, dtype=torch.float32)
+    ctr = nat.gemm_ctr(xq.device)     # held until the launch is enqueued
+    nat.call("rh3_gemm_fp8_acc", nat.ptr(xq), xq.stride(0), nat.ptr(wq), wq.stride(0), nat.ptr(acc), acc.stride(0),
+             m, n, k, nat.ptr(ctr), nat.stream(xq.device))
+    return acc
 
 
 def int8_gemm_gated_residual(xq, xs, wq, ws, gate, resid, config=6):
@@ -83,10 +99,32 @@ def int8_gemm_gated_residual(xq, xs, wq, ws, gate, resid, config=6):
     gate = gate.reshape(-1).to(torch.bfloat16).contiguous()
     if gate.numel() != n:
         raise RuntimeError("int8_gemm_gated_residual: gate must have N elements")
+    ctr = nat.gemm_ctr(xq.device)     # held until the launch is enqueued
     nat.call("rh3_gemm_i8_gated", nat.ptr(xq), xq.stride(0), nat.ptr(xs), nat.ptr(wq), wq.stride(0), nat.ptr(ws),
-             nat.ptr(gate), nat.ptr(resid), resid.stride(0), m, n, k, nat.gemm_ctr(xq.device),
+             nat.ptr(gate), nat.ptr(resid), resid.stride(0), m, n, k, nat.ptr(ctr),
              nat.stream(xq.device))
     return resid
+
+
+_ROWS_OK = {}
+
+
+def _check_rows(rows, r):
+    """Raise IndexError unless every gate row index is in [0, r), as torch's gather does. The kernel reads the table
+    unchecked, so the check runs here, once per index tensor (identity, storage, version) and table height: the blocks
+    of one model call share their segments' index tensors and pay for each once."""
+    key = (id(rows), rows.data_ptr(), rows._version, r)
+    hit = _ROWS_OK.get(key)
+    if hit is not None and hit is rows:
+        return
+    if rows.numel():
+        lo, hi = int(rows.min()), int(rows.max())
+        if lo < 0 or hi >= r:
+            raise IndexError(f"int8_gemm_gated_residual_rows: gate row index out of range [{lo}, {hi}] for a table "
+                             f"of {r} rows")
+    if len(_ROWS_OK) >= 64:
+        _ROWS_OK.clear()
+    _ROWS_OK[key] = rows
 
 
 def int8_gemm_gated_residual_rows(xq, xs, wq, ws, gate, rows, resid):
@@ -100,12 +138,14 @@ def int8_gemm_gated_residual_rows(xq, xs, wq, ws, gate, rows, resid):
         raise RuntimeError("int8_gemm_gated_residual_rows: resid must be bf16 [M, N] with unit column stride")
     xs, ws = _vec(xs, m, "gated xs"), _vec(ws, n, "gated ws")
     gate = gate.to(torch.bfloat16).reshape(-1, n).contiguous()
-    rows = rows.reshape(-1).to(device=xq.device, dtype=torch.int32).contiguous()
     if rows.numel() != m:
         raise RuntimeError("int8_gemm_gated_residual_rows: one gate row index per token required")
+    _check_rows(rows, gate.shape[0])
+    rows = rows.reshape(-1).to(device=xq.device, dtype=torch.int32).contiguous()
+    ctr = nat.gemm_ctr(xq.device)     # held until the launch is enqueued
     nat.call("rh3_gemm_i8_gated_rows", nat.ptr(xq), xq.stride(0), nat.ptr(xs), nat.ptr(wq), wq.stride(0),
              nat.ptr(ws), nat.ptr(gate), gate.stride(0), nat.ptr(rows), nat.ptr(resid), resid.stride(0), m, n, k,
-             nat.gemm_ctr(xq.device), nat.stream(xq.device))
+             nat.ptr(ctr), nat.stream(xq.device))
     return resid
 
 
@@ -128,8 +168,9 @@ def int8_gemm_swiglu(xq, xs, wq_perm, ws_perm, config=6):
         raise RuntimeError("int8_gemm_swiglu: N must be a multiple of 8")
     xs, ws = _vec(xs, m, "swiglu xs"), _vec(ws_perm, n, "swiglu ws")
     out = torch.empty((m, n // 2), device=xq.device, dtype=torch.bfloat16)
+    ctr = nat.gemm_ctr(xq.device)     # held until the launch is enqueued
     nat.call("rh3_gemm_i8_swiglu", nat.ptr(xq), xq.stride(0), nat.ptr(xs), nat.ptr(wq_perm), wq_perm.stride(0),
-             nat.ptr(ws), nat.ptr(out), out.stride(0), m, n, k, nat.gemm_ctr(xq.device),
+             nat.ptr(ws), nat.ptr(out), out.stride(0), m, n, k, nat.ptr(ctr),
              nat.stream(xq.device))
     return out
 

@@ -12,8 +12,9 @@ Differences from the reference, all on purpose:
     torch fp32 matmul of unspecified order;
   * the nvfp4 verification modes run their fp32 round trip on a HIP kernel (rh3_fake_nvfp4) and the
     bf16 x bf16 product on torch.nn.functional.linear, as the reference does (kernels.py:53-56, :120-122);
-  * fp8_tensor: the tensor absmax and codes on rh3_quant_any, the product on the FP8 GEMM kernel with the two
-    scales in its epilogue and a bf16 result (cast to x.dtype), where the reference's _scaled_mm writes x.dtype.
+  * fp8_tensor: the tensor absmax and codes on rh3_quant_any, the product on the FP8 GEMM kernel: for bf16 x with the
+    two scales in its epilogue, for fp16 / fp32 x as raw fp32 accumulators scaled by (acc * s_x) * s_w and rounded
+    once to x.dtype, as the reference's _scaled_mm(out_dtype=x.dtype) does.
 """
 from dataclasses import dataclass
 
@@ -104,8 +105,11 @@ def linear(x, qw, mode):
     if mode == "fp8_tensor":
         xq, s = _quant.quant_any(x, "fp8_tensor")
         m, n = x.shape[0], qw.q.shape[0]
-        y = _gemm.fp8_gemm(xq, s.reshape(1).expand(m).contiguous(), qw.q, qw.scale.reshape(1).expand(n).contiguous())
-        return y.to(x.dtype)
+        if x.dtype == torch.bfloat16:   # the two scales in the GEMM epilogue, rounded once to bf16
+            return _gemm.fp8_gemm(xq, s.reshape(1).expand(m).contiguous(), qw.q,
+                                  qw.scale.reshape(1).expand(n).contiguous())
+        # fp16 / fp32 out: the raw fp32 product, then (acc * s_x) * s_w rounded once to x.dtype
+        return ((_gemm.fp8_gemm_acc(xq, qw.q) * s.reshape(1)) * qw.scale.reshape(1)).to(x.dtype)
     if x.dtype != torch.bfloat16:
         if mode == "fp8_rowwise_torch":
             mode = "fp8_rowwise"

@@ -12,8 +12,11 @@ What it keeps from the reference:
   * a weight cached in SwiGLU-epilogue row order is returned to natural order (:155-157);
   * measure_every = n > 0 records the relative L2 error against F.linear every n calls into
     stats[name] (:139-165).
-What it does not keep: ComfyUI's cast context for off-GPU / LoRA weights, and the F.linear path for CPU
-or fp32 inputs (:147-148), which here raise: no CPU path. fp16 activations take kernels.linear's path for them.
+  * activations that are not on a GPU or not bf16 / fp16 take torch's F.linear with the weight in x.dtype, as in
+    the reference (:147-148): the quantized kernels are for bf16 / fp16 GPU activations only. An adopted
+    int8_convrot weight has no bf16 copy; there it is dequantized (codes times scale, rotated back by the
+    orthogonal, symmetric blockdiag(H256)), as the reference's QuantizedTensor dequantizes inside F.linear.
+What it does not keep: ComfyUI's cast context for off-GPU / LoRA weights (:93-105, needs comfy).
 """
 import torch
 
@@ -55,10 +58,21 @@ class QuantLinear:
             self.cache_key = key
         return self.qweight
 
+    def dense_weight(self, device, dtype):
+        """The weight for the F.linear route: the module's weight, or the adopted int8_convrot weight dequantized."""
+        if self.weight is not None:
+            return self.weight.to(device=device, dtype=dtype)
+        from .triton_fp8 import ROT_GROUP, regular_hadamard
+        q, sc = self.qweight.q, self.qweight.scale
+        n, k = q.shape
+        w = q.float() * sc.reshape(n, 1).float()
+        w = (w.reshape(n, k // ROT_GROUP, ROT_GROUP) @ regular_hadamard(ROT_GROUP, w.device)).reshape(n, k)
+        return w.to(device=device, dtype=dtype)
+
     def __call__(self, x):
         if not x.is_cuda or x.dtype not in (torch.bfloat16, torch.float16):
-            raise TypeError(f"QuantLinear {self.name}: bf16 / fp16 GPU activations only (no CPU path), got {x.dtype} "
-                            f"on {x.device}")
+            b = None if self.bias is None else self.bias.to(device=x.device, dtype=x.dtype)
+            return torch.nn.functional.linear(x, self.dense_weight(x.device, x.dtype), b)
         qw = self.qweight_for()
         shape = x.shape
         y = kernels.linear(x.reshape(-1, shape[-1]), qw, self.mode)

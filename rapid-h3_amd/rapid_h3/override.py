@@ -13,9 +13,15 @@ Behaviour kept from the reference:
     block, config >= 200 with rapidh3_rrcheck (:1000, :1043-1045);
   * a call carrying transformer_options["rapidh3_text_bias"] with S >= 1024 raises (the bias needs the fused
     block path, :1025-1027).
+stock_attention stands in for ComfyUI's optimized_attention, the function an override receives as func and falls
+through to. rr_check is the reference's config-2xx check of the fused RMSNorm + RoPE path (_rr_check, :334-349).
 """
+import json
+import os
+
 import torch
 
+from . import attention as _attention
 from . import attn_int8
 
 
@@ -38,6 +44,52 @@ def exact_attention_rows(q, k, v, out, spans, scale=None):
                                                                scale=scale)
         out[:, :, a:b] = ref.to(out.dtype)
     return out
+
+
+def stock_attention(q, k, v, heads, mask=None, attn_precision=None, skip_reshape=False, skip_output_reshape=False,
+                    transformer_options=None, scale=None, **kwargs):
+    """The stock attention an override falls through to, in ComfyUI's optimized_attention calling convention: q, k, v
+    [B, H, S, D] with skip_reshape, else [B, S, H * D]; the output [B, H, Sq, D] with skip_output_reshape, else
+    [B, Sq, H * D], in q.dtype. Computed in fp32 (torch's scaled_dot_product_attention on fp32 copies, 1024 query rows
+    at a time) and rounded once; mask is added to the scores (bool: True keeps)."""
+    if not skip_reshape:
+        b, _, hd = q.shape
+        d = hd // heads
+        q, k, v = (t.reshape(b, -1, heads, d).transpose(1, 2) for t in (q, k, v))
+    b, h, sq, d = q.shape
+    out = torch.empty(b, h, sq, d, dtype=q.dtype, device=q.device)
+    kf, vf = k.float().contiguous(), v.float().contiguous()
+    for a in range(0, sq, 1024):
+        m = mask
+        if m is not None and m.dim() >= 2 and m.shape[-2] == sq:
+            m = m[..., a:a + 1024, :]
+        out[:, :, a:a + 1024] = torch.nn.functional.scaled_dot_product_attention(
+            q[:, :, a:a + 1024].float().contiguous(), kf, vf, attn_mask=m, scale=scale).to(q.dtype)
+    if skip_output_reshape:
+        return out
+    return out.transpose(1, 2).reshape(b, sq, h * d)
+
+
+def rr_check(q, k, v, o, tab, qw, kw, eps, cfg, transformer_options):
+    """The config-2xx check (the reference's _rr_check, __init__.py:334-349) on the real q, k, v of one fused block:
+    the fused RMSNorm + RoPE path's output o [1, H, S, 128] and its pre-pass operands against the unfused path
+    (attention.rms_rope_ on copies of q, k, then attn_int8.attention with the same config). One JSON line per call,
+    appended to $RAPIDH3_RRCHECK (default /data/output/rapidh3_rrcheck.jsonl, as in the reference). q, k, v:
+    the raw [S, H, 128] qkv-projection views."""
+    qc, kc = q.clone(), k.clone()
+    _attention.rms_rope_(qc, kc, tab, qw, kw, eps)
+    ref = attn_int8.attention(qc, kc, v, config=cfg)
+    pu = attn_int8.ext().int8_prepass(qc, kc, v, config=cfg)
+    pf = attn_int8.ext().int8_prepass(q, k, v, tab, qw, kw, eps, config=cfg)
+    got = o[0].transpose(0, 1)
+    rec = {"block": transformer_options.get("block_index"), "S": q.shape[0],
+           "out_equal": torch.equal(ref, got),
+           "operands_equal": all(a is None and b is None or torch.equal(a, b) for a, b in zip(pu, pf)),
+           "max_abs_diff": float((ref.float() - got.float()).abs().max())}
+    path = os.environ.get("RAPIDH3_RRCHECK", "/data/output/rapidh3_rrcheck.jsonl")
+    with open(path, "a") as f:
+        f.write(json.dumps(rec) + "\n")
+    return rec
 
 
 def make_override(config, exact_rows="", prev=None):

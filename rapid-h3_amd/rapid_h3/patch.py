@@ -15,11 +15,19 @@ Kept from the reference:
 The fused block forward reads the block duck-typed, with the attribute names of ComfyUI's H3 block that the reference
 uses (:253-320): adaln_proj(t_emb) -> the six modulation tables, norm1 / norm2 (.weight, .eps), attn (.heads,
 .head_dim, .q_norm, .k_norm), and takes forward(x, t_emb, mod_segments, rope_freqs, transformer_options={},
-attention=None). Its attention is the INT8 attention with the override's config tag (rapidh3_rmsrope, set by
-override.make_override for configs >= 100) and the text bias of transformer_options["rapidh3_text_bias"]; without a
-tag it runs this build's per-block INT8 recipe (the reference hands the rms-roped q, k to ComfyUI's attention
-dispatcher there). Inputs the fused path does not take (not bf16, not 2-D, on the CPU, an attention argument, no
-rope table) go to the block's own forward, as in the reference (:255-258).
+attention=None). Its attention follows the reference (:277-306):
+  * an override tagged rapidh3_rmsrope (override.make_override, configs >= 100 without exact_rows) and S >= 1024: the
+    INT8 attention with that config and the RMSNorm + RoPE in its pre-pass, with the text bias of
+    transformer_options["rapidh3_text_bias"]; a rapidh3_rrcheck tag (configs >= 200) adds override.rr_check;
+  * otherwise, when an override is installed (or patch() was given the stock attention): q, k get the RMSNorm + RoPE
+    in place and the override is called in ComfyUI's convention, override(func, q, k, v, heads, mask=None,
+    skip_reshape=True, skip_output_reshape=True, transformer_options=...), func being the stock attention
+    (`attention`, default override.stock_attention), so the override's own config and exact_rows decide the
+    numerics; with no override, func itself runs;
+  * with neither an override nor a stock attention given, this build's per-block INT8 recipe (RMSNorm + RoPE fused
+    in its pre-pass), the attention the benchmark measures.
+Inputs the fused path does not take (not bf16, not 2-D, on the CPU, an attention argument, no rope table) go to the
+block's own forward, as in the reference (:255-258).
 """
 import json
 import os
@@ -28,6 +36,7 @@ import re
 import torch
 
 from . import block as _block
+from . import override as _override
 from .linear import QuantLinear
 
 NAME_RE = re.compile(r"^blocks\.(\d+)\.(attn|mlp)\.(qkv_proj|out_proj|fc1|fc2)$")
@@ -72,8 +81,9 @@ def _text_rows(opts):
     return seg[1]
 
 
-def fused_block_forward(blk, qkv, out, fc1, fc2, recipe="int8_rot"):
-    """The forward that replaces a DiT block (the reference's _fused_block, __init__.py:207-321)."""
+def fused_block_forward(blk, qkv, out, fc1, fc2, recipe="int8_rot", stock_attention=None):
+    """The forward that replaces a DiT block (the reference's _fused_block, __init__.py:207-321). stock_attention:
+    the attention ComfyUI's dispatcher would run (override.stock_attention's convention), or None."""
     orig = type(blk).forward
     state = {}
 
@@ -106,16 +116,39 @@ def fused_block_forward(blk, qkv, out, fc1, fc2, recipe="int8_rot"):
             return orig(blk, x, t_emb, mod_segments, rope_freqs, transformer_options=transformer_options,
                         attention=attention)
         mod = blk.adaln_proj(t_emb)
+        a = blk.attn
         ov = transformer_options.get("optimized_attention_override")
         cfg = getattr(ov, "rapidh3_rmsrope", None)
+        if cfg is not None and not (x.shape[0] >= 1024 and a.head_dim == 128 and rope_freqs.dtype == torch.bfloat16):
+            cfg = None                                  # the reference's fused-path condition (:284-285)
         tb = transformer_options.get("rapidh3_text_bias")
+        w = weights(x)
+        if cfg is None and (ov is not None or stock_attention is not None):
+            if tb is not None:
+                raise RuntimeError("RapidH3TextAttnBias: needs the fused INT8 attention path (RapidH3Int8Attention "
+                                   "190 or 194)")
+            func = stock_attention or _override.stock_attention
+
+            def attn_fn(q, k, v):
+                q4, k4, v4 = (t.unsqueeze(0).transpose(1, 2) for t in (q, k, v))     # [1, H, S, 128] views
+                kw = dict(mask=None, skip_reshape=True, skip_output_reshape=True,
+                          transformer_options=transformer_options)
+                return ov(func, q4, k4, v4, a.heads, **kw) if ov is not None else func(q4, k4, v4, a.heads, **kw)
+
+            return _block.fused_block(x, w, mod, mod_segments, rope_freqs, attn_fn=attn_fn)
         text_bias = None
         if tb is not None:
             if cfg is None:
                 raise RuntimeError("RapidH3TextAttnBias: needs the fused INT8 attention path (RapidH3Int8Attention "
                                    "190 or 194)")
             text_bias = (_text_rows(transformer_options), tb)
-        return _block.fused_block(x, weights(x), mod, mod_segments, rope_freqs, attn_config=cfg, text_bias=text_bias)
+        check = None
+        if cfg is not None and getattr(ov, "rapidh3_rrcheck", False):
+            def check(q, k, v, o):
+                _override.rr_check(q, k, v, o, rope_freqs, w.q_norm_w, w.k_norm_w, w.qk_eps, cfg,
+                                   transformer_options)
+        return _block.fused_block(x, w, mod, mod_segments, rope_freqs, attn_config=cfg, text_bias=text_bias,
+                                  attn_check=check)
 
     return forward
 
@@ -138,7 +171,7 @@ class LinearQuantPatch:
     **kwargs) runs executor with the replacement forwards installed and restores the previous ones afterwards."""
 
     def __init__(self, diffusion_model, mode, targets="qkv_proj,out_proj,fc1,fc2", keep_bf16_blocks="",
-                 measure_every=0, fuse_block=True, patch_id=None, stats_path=None):
+                 measure_every=0, fuse_block=True, patch_id=None, stats_path=None, attention=None):
         self.mode, self.stats, self.stats_path = mode, {}, stats_path
         self.wrappers, self.by_name = [], {}
         if mode == "bf16":
@@ -158,7 +191,7 @@ class LinearQuantPatch:
                     continue
                 parts = [self.by_name.get(f"{name}.{p}") for p in PARTS]
                 if all(parts) and fuse_block:
-                    self.wrappers.append((mod, fused_block_forward(mod, *parts)))
+                    self.wrappers.append((mod, fused_block_forward(mod, *parts, stock_attention=attention)))
                 elif parts[2] and parts[3]:
                     self.wrappers.append((mod.mlp, fused_mlp_forward(mod.mlp, parts[3])))
 
@@ -185,9 +218,11 @@ class LinearQuantPatch:
 
 
 def patch(diffusion_model, mode, targets="qkv_proj,out_proj,fc1,fc2", keep_bf16_blocks="", measure_every=0,
-          fuse_block=True, patch_id=None, stats_path=None):
-    """LinearQuantPatch for a model; stats_path defaults to $RAPIDH3_STATS as in the reference (:396)."""
+          fuse_block=True, patch_id=None, stats_path=None, attention=None):
+    """LinearQuantPatch for a model; stats_path defaults to $RAPIDH3_STATS as in the reference (:396). attention: the
+    stock attention of the fused blocks' unfused route (ComfyUI's optimized_attention in the reference; the
+    calling convention of override.stock_attention)."""
     if stats_path is None:
         stats_path = os.environ.get("RAPIDH3_STATS")
     return LinearQuantPatch(diffusion_model, mode, targets, keep_bf16_blocks, measure_every, fuse_block, patch_id,
-                            stats_path)
+                            stats_path, attention)

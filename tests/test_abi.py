@@ -25,7 +25,7 @@ def test_header_symbols_exported_and_bound():
         assert hasattr(lib, n), n
         assert n in _native.SIGNATURES, f"{n} declared in rh3.h but not bound in _native"
     assert set(_native.SIGNATURES) == set(names)
-    assert lib.rh3_abi_version() == _native.ABI_VERSION == 2
+    assert lib.rh3_abi_version() == _native.ABI_VERSION == 3
 
 
 def test_argument_validation_without_gpu():
@@ -60,6 +60,12 @@ def test_argument_validation_without_gpu():
     st = lib.rh3_attention_u8_prepass(fake, 128, 128, fake, 128, 128, fake, 128, 128, 10, 12, 1, fake, 96, fake,
                                       fake, 1e-5, 1, 1, 1, fake, 1 << 30, fake, None)
     assert st == 1 and "self-attention" in nat.last_error()
+    st = lib.rh3_rms_rope_qk(fake, 128, 128, fake, 128, 128, 10, 1, fake, 64, fake, fake, 1e-5, None)
+    assert st == 1 and "rot_dim" in nat.last_error()
+    st = lib.rh3_rms_rope_qk(fake, 100, 128, fake, 128, 128, 10, 1, fake, 128, fake, fake, 1e-5, None)
+    assert st == 1 and "multiples of 8" in nat.last_error()
+    st = lib.rh3_gemm_fp8_acc(fake, 96, fake, 96, fake, 16, 4, 16, 96, None, None)
+    assert st == 1 and "multiple of 64" in nat.last_error()
     with pytest.raises(RuntimeError, match="multiple of 64"):
         nat.call("rh3_gemm_i8", fake, 96, fake, fake, 96, fake, None, fake, 16, 4, 16, 96, None, None)
 
@@ -69,6 +75,7 @@ def test_empty_inputs_are_no_ops():
     lib = nat.lib()
     assert lib.rh3_quant_rows_i8(None, 0, 0, 64, None, 64, None, None) == 0
     assert lib.rh3_gemm_i8(None, 64, None, None, 64, None, None, None, 8, 0, 8, 64, None, None) == 0
+    assert lib.rh3_rms_rope_qk(None, 128, 128, None, 128, 128, 0, 1, None, 128, None, None, 1e-5, None) == 0
 
 
 def test_workspace_size_matches_layout():

@@ -272,12 +272,12 @@ def test_gemm_counter_buffers_per_stream(dev):
     import torch
     from rapid_h3 import _native as nat
     from rapid_h3 import gemm
-    a = nat.gemm_ctr(dev).value
-    assert nat.gemm_ctr(dev).value == a
+    a = nat.gemm_ctr(dev).data_ptr()
+    assert nat.gemm_ctr(dev).data_ptr() == a
     s = torch.cuda.Stream(device=dev)
     with torch.cuda.stream(s):
-        b = nat.gemm_ctr(dev).value
-        assert nat.gemm_ctr(dev).value == b
+        b = nat.gemm_ctr(dev).data_ptr()
+        assert nat.gemm_ctr(dev).data_ptr() == b
     assert a != b
     rng = np.random.default_rng(3)
     xq = to_dev(np.clip(np.rint(rng.standard_normal((2000, 512)) * 30), -127, 127).astype(np.int8), dev)
@@ -290,3 +290,26 @@ def test_gemm_counter_buffers_per_stream(dev):
         y1 = gemm.int8_gemm(xq, xs, wq, ws)
     torch.cuda.synchronize()
     assert torch.equal(y0.view(torch.int16), y1.view(torch.int16))
+
+
+def test_gated_rows_index_out_of_range(dev):
+    """A per-token gate row index outside the table raises on the host (torch's gather raises there too); the kernel
+    is never launched with it."""
+    import torch
+    from rapid_h3 import gemm
+    m, n, k = 64, 256, 256
+    xq = torch.ones(m, k, dtype=torch.int8, device=dev)
+    wq = torch.ones(n, k, dtype=torch.int8, device=dev)
+    xs = torch.ones(m, 1, device=dev)
+    ws = torch.ones(1, n, device=dev)
+    gate = torch.ones(3, n, dtype=torch.bfloat16, device=dev)
+    resid = torch.zeros(m, n, dtype=torch.bfloat16, device=dev)
+    for bad in (3, -1):
+        rows = torch.zeros(m, dtype=torch.long, device=dev)
+        rows[17] = bad
+        with pytest.raises(IndexError):
+            gemm.int8_gemm_gated_residual_rows(xq, xs, wq, ws, gate, rows, resid)
+    assert int(resid.abs().max()) == 0
+    rows = torch.full((m,), 2, dtype=torch.long, device=dev)
+    gemm.int8_gemm_gated_residual_rows(xq, xs, wq, ws, gate, rows, resid)
+    assert float(resid.float().min()) == float(k)

@@ -17,7 +17,9 @@ def _bf(a):
 
 
 def _capture(fn):
-    """fn() run twice on a side stream (lazy library state, the side stream's tile counters), then captured."""
+    """fn() run twice on a side stream (lazy library state), then captured on torch's default capture stream. The
+    GEMMs inside the capture take new tile-counter buffers from the graph's private pool, so no two graphs share
+    one."""
     import torch
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
@@ -80,6 +82,58 @@ def test_graph_gemms(dev):
     xq2 = torch.randint(-127, 128, (1000, k), device=dev, dtype=torch.int8)
     _replays(g, (y, h, resid), (y_e, h_e, r_e), reset=lambda: resid.copy_(r0),
              between=lambda: gemm.int8_gemm(xq2, xs[:1000], wq, ws))
+
+
+def test_graph_gemms_two_graphs_at_once(dev):
+    """Two graphs captured on the same (default) capture stream, replayed at once on two streams: each holds its own
+    tile counters, so neither skips a tile nor applies the in-place gated residual twice; each replay matches its
+    eager result bit for bit."""
+    import torch
+    from rapid_h3 import gemm
+    rng = np.random.default_rng(15)
+    m, n, k = 6000, 4096, 1024
+    sets = []
+    for _ in range(2):
+        xq = to_dev(np.clip(np.rint(rng.standard_normal((m, k)) * 30), -127, 127).astype(np.int8), dev)
+        wq = to_dev(np.clip(np.rint(rng.standard_normal((n, k)) * 30), -127, 127).astype(np.int8), dev)
+        xs = to_dev((rng.random((m, 1)) * 1e-3 + 1e-4).astype(np.float32), dev)
+        ws = to_dev((rng.random((1, n)) * 1e-3 + 1e-4).astype(np.float32), dev)
+        gate = to_dev(_bf(rng.standard_normal(n)), dev)
+        r0 = to_dev(_bf(rng.standard_normal((m, n))), dev)
+        sets.append((xq, wq, xs, ws, gate, r0, r0.clone()))
+
+    def make(i):
+        xq, wq, xs, ws, gate, r0, resid = sets[i]
+
+        def fn():
+            gemm.int8_gemm_gated_residual(xq, xs, wq, ws, gate, resid)
+            return (gemm.int8_gemm(xq, xs, wq, ws),)
+        return fn
+
+    fns = [make(0), make(1)]
+    want = []
+    for i in range(2):
+        sets[i][6].copy_(sets[i][5])
+        y = fns[i]()[0]
+        want.append((y, sets[i][6].clone()))
+    graphs = []
+    for i in range(2):
+        sets[i][6].copy_(sets[i][5])
+        graphs.append(_capture(fns[i]))
+    streams = [torch.cuda.Stream(device=dev) for _ in range(2)]
+    for rep in range(3):
+        for i in range(2):
+            graphs[i][1][0].zero_()
+            sets[i][6].copy_(sets[i][5])
+        torch.cuda.synchronize()
+        for i in range(2):
+            with torch.cuda.stream(streams[i]):
+                graphs[i][0].replay()
+        torch.cuda.synchronize()
+        for i in range(2):
+            y_w, r_w = want[i]
+            assert torch.equal(graphs[i][1][0].view(torch.int16), y_w.view(torch.int16)), f"graph {i} replay {rep}"
+            assert torch.equal(sets[i][6].view(torch.int16), r_w.view(torch.int16)), f"graph {i} resid {rep}"
 
 
 @pytest.mark.parametrize("config", [None, 94])

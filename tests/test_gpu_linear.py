@@ -1,6 +1,6 @@
 """rapid_h3.linear.QuantLinear, the _QuantLinear drop-in (__init__.py:83-167): output equal to
 kernels.linear + bias, the weight cache and its invalidation, adoption of int8_convrot weights, the
-measured-error diagnostics, and no CPU path."""
+measured-error diagnostics, and F.linear for CPU / fp32 activations."""
 import numpy as np
 import pytest
 
@@ -34,7 +34,9 @@ def test_quant_linear_matches_kernels_linear(dev, mode):
     assert lin.qweight is not q0
 
 
-def test_quant_linear_adopts_convrot_and_refuses_cpu(dev):
+def test_quant_linear_adopts_convrot_and_cpu_takes_f_linear(dev):
+    """An adopted int8_convrot weight runs the quantized path on bf16 GPU activations; CPU and fp32 activations take
+    F.linear with the weight dequantized (the reference's route for them, __init__.py:147-148)."""
     import torch
     from rapid_h3 import kernels
     from rapid_h3.linear import QuantLinear
@@ -44,8 +46,11 @@ def test_quant_linear_adopts_convrot_and_refuses_cpu(dev):
     lin = QuantLinear.from_quantized(qw.q, qw.scale.reshape(-1))
     x = torch.randn(33, 256, generator=g).to(torch.bfloat16).to(dev)
     assert np.array_equal(to_np(lin(x)), to_np(kernels.linear(x, qw, "int8_rot")))
-    with pytest.raises(TypeError):
-        lin(x.cpu())
+    y = lin(x.cpu())
+    assert y.device.type == "cpu" and torch.equal(y, torch.nn.functional.linear(x.cpu(), lin.dense_weight("cpu", x.dtype)))
+    y32 = lin(x.float())
+    ref = x.float() @ w.float().t()
+    assert y32.dtype == torch.float32 and float((y32 - ref).norm() / ref.norm()) < 0.01
     with pytest.raises(ValueError):
         QuantLinear(w, mode="bf16")
 
@@ -89,6 +94,37 @@ def test_quantize_any_dtype_against_torch(dev, dtype):
         assert yf.dtype == dt and float((yf.cpu().float() - exact).norm() / exact.norm()) < 0.05
         with pytest.raises(ValueError):
             kernels.linear(x.to(dev), qw, "int8_rot")            # the reference's torch path has no int8_rot
+
+
+@pytest.mark.parametrize("dtype", ["float32", "float16"])
+def test_fp8_tensor_linear_non_bf16_out(dev, dtype):
+    """fp8_tensor with fp32 / fp16 activations returns x.dtype rounded once from fp32, as the reference's
+    torch._scaled_mm(out_dtype=x.dtype) does (kernels.py:124-127): the raw fp32 accumulators of the FP8 GEMM
+    (rh3_gemm_fp8_acc) within 1e-4 rel-L2 of the exact product of the codes (oracle; measured 3e-5, the MFMA's own
+    fp32 accumulation), and the output within 1e-4 (fp32) or the fp16 rounding (1e-3) of torch._scaled_mm run on the
+    CPU with the same codes and scales. A bf16-rounded epilogue would miss every bound (its rounding alone is about
+    2e-3)."""
+    import torch
+    from oracle import gemm as og
+    from oracle.numerics import fp8_e4m3_to_f32
+    from rapid_h3 import gemm, kernels, quant
+    dt = getattr(torch, dtype)
+    g = torch.Generator(device="cpu").manual_seed(12)
+    w = (0.02 * torch.randn(264, 512, generator=g)).to(dt)
+    x = torch.randn(130, 512, generator=g)
+    x[:, :5] *= 20
+    x = x.to(dt)
+    qw = kernels.quantize_weight(w.to(dev), "fp8_tensor")
+    y = kernels.linear(x.to(dev), qw, "fp8_tensor")
+    assert y.dtype == dt and tuple(y.shape) == (130, 264)
+    xq, s = quant.quant_any(x.to(dev), "fp8_tensor")
+    acc = gemm.fp8_gemm_acc(xq, qw.q)
+    a64 = fp8_e4m3_to_f32(to_np(xq.view(torch.uint8))).astype(np.float64)
+    b64 = fp8_e4m3_to_f32(to_np(qw.q.view(torch.uint8))).astype(np.float64)
+    assert og.rel_l2(to_np(acc), a64 @ b64.T) < 1e-4
+    ref = torch._scaled_mm(xq.cpu(), qw.q.cpu().t(), s.cpu().reshape(()), qw.scale.cpu().reshape(()), out_dtype=dt)
+    err = float((y.cpu().double() - ref.double()).norm() / ref.double().norm())
+    assert err < (1e-4 if dt == torch.float32 else 1e-3), err
 
 
 def test_c1_linear_full_size(dev):

@@ -11,6 +11,7 @@ from torch import nn
 from conftest import to_np
 from oracle import gemm as og
 from oracle import quant as oq
+from oracle.numerics import bf16_to_f32, f32_to_bf16
 
 pytestmark = pytest.mark.gpu
 
@@ -127,3 +128,148 @@ def test_fused_mlp_against_oracle(dev):
     d = np.abs(T["hq"].astype(np.int32) - hq.astype(np.int32))
     assert d.max() <= 1 and (d > 0).mean() < 0.01
     assert np.array_equal(to_np(y), og.int8_gemm(T["hq"], T["hs"], q2, s2))
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# The attention route of a fused block (__init__.py:277-306, :334-349, :1023-1041): an override tagged for the fused
+# RMSNorm + RoPE path (configs >= 100) runs inside the block's pre-pass; an untagged override (configs < 100, or any
+# exact_rows) gets q, k after a separate RMSNorm + RoPE and decides the numerics itself.
+
+SL = 1100                                                          # >= 1024: the override's INT8 path
+
+
+class _Layout:
+    def __init__(self, segments):
+        self.segments, self.seq_len = segments, SL
+
+
+def _route_setup(dev, seed):
+    g = torch.Generator().manual_seed(seed)
+    model = _DiT(g).to(dev)
+    x0 = (torch.randn(SL, HID, generator=g) * torch.where(torch.rand(HID, generator=g) < 0.02, 20.0, 1.0)).to(
+        torch.bfloat16).to(dev)
+    import bench
+    return model, x0, bench.rope_table(SL, dev)
+
+
+def _spy(ov, log):
+    """An untagged wrapper of an override that records what the block hands it and what it returns."""
+    def spy(func, *args, **kwargs):
+        out = ov(func, *args, **kwargs)
+        log.append(([a.clone() for a in args[:3]], args[3], dict(kwargs), out.clone()))
+        return out
+    return spy
+
+
+def test_untagged_override_decides_the_numerics(dev):
+    """make_override(94) (untagged): the block's q, k reach the override after RMSNorm + RoPE (bit-exact against the
+    oracle's rms_rope of the qkv GEMM output), in ComfyUI's [1, H, S, 128] skip_reshape convention, and the block
+    continues from the override's own output, which matches the oracle's config-94 emulation. The whole patched
+    block is bit-identical to the tagged route make_override(194), whose RMSNorm + RoPE runs inside the pre-pass."""
+    from oracle import attn as oa
+    from rapid_h3 import override, patch
+    model, x0, tab = _route_setup(dev, 21)
+    segs = [(0, 300, 0), (300, SL, 1)]
+    p = patch.patch(model, "int8_rot")
+    blk = model.blocks[0]
+    log = []
+    opts = {"optimized_attention_override": _spy(override.make_override(94), log)}
+    got = p.wrapper(lambda x: blk(x, None, segs, tab, transformer_options=opts), x0.clone())
+    (q4, k4, v4), heads, kw, out = log[0]
+    assert heads == HEADS and kw["skip_reshape"] and kw["skip_output_reshape"] and kw["mask"] is None
+    assert tuple(q4.shape) == (1, HEADS, SL, 128) and kw["transformer_options"] is opts
+    # q, k, v are what the oracle's chain gives: the int8_rot qkv GEMM, then rms_rope on q and k
+    qkv_w = p.by_name["blocks.0.attn.qkv_proj"].qweight_for()
+    xq, xs = oq.norm_mod_rot_quant_rows_i8(to_np(x0), to_np(blk.norm1.weight), 1e-6, np.repeat([0, 1], [300, SL - 300]),
+                                          to_np(blk.mods[0]), to_np(blk.mods[1]))
+    qkv = og.int8_gemm(xq, xs, to_np(qkv_w.q), to_np(qkv_w.scale)).reshape(SL, 3, HEADS, 128)
+    tb = to_np(tab).reshape(SL, 48, 2, 2)
+    rq = f32_to_bf16(oa.rms_rope(qkv[:, 0], tb, to_np(blk.attn.q_norm.weight), 1e-6))
+    rk = f32_to_bf16(oa.rms_rope(qkv[:, 1], tb, to_np(blk.attn.k_norm.weight), 1e-6))
+    assert np.array_equal(to_np(q4[0].transpose(0, 1)), rq)
+    assert np.array_equal(to_np(k4[0].transpose(0, 1)), rk)
+    assert np.array_equal(to_np(v4[0].transpose(0, 1)), qkv[:, 2])
+    pp = oa.prepass_u8(rq, rk, qkv[:, 2])
+    rows = np.arange(0, SL, 7)
+    ref = oa.attention_u8_from_codes(pp, 128 ** -0.5, rows=rows)
+    o = bf16_to_f32(to_np(out[0].transpose(0, 1)[rows]))
+    assert og.rel_l2(o, ref) < 2e-3
+    # the tagged route (fused RMSNorm + RoPE, same config) gives the same block output bit for bit
+    opts2 = {"optimized_attention_override": override.make_override(194)}
+    assert override.make_override(194).rapidh3_rmsrope == 94
+    got2 = p.wrapper(lambda x: blk(x, None, segs, tab, transformer_options=opts2), x0.clone())
+    assert torch.equal(got, got2)
+
+
+def test_exact_rows_override_through_the_block(dev):
+    """make_override(194, exact_rows="text") is untagged (exact_rows needs the unfused route): the text segment's
+    query rows come out as exact attention of the roped q, k (fp32, rounded once), the others as config 94."""
+    from oracle import attn as oa
+    from rapid_h3 import override, patch
+    model, x0, tab = _route_setup(dev, 22)
+    segs = [(0, 64, 0), (64, SL, 1)]
+    lay = _Layout([(0, 64, "text"), (64, SL, "video")])
+    ov = override.make_override(194, exact_rows="text")
+    assert getattr(ov, "rapidh3_rmsrope", None) is None
+    p = patch.patch(model, "int8_rot")
+    blk = model.blocks[1]
+    log = []
+    opts = {"optimized_attention_override": _spy(ov, log), "minimax_h3_layout": lay}
+    p.wrapper(lambda x: blk(x, None, segs, tab, transformer_options=opts), x0.clone())
+    (q4, k4, v4), _, _, out = log[0]
+    qn, kn, vn = (to_np(t[0].transpose(0, 1)) for t in (q4, k4, v4))
+    ex = oa.attention_exact(qn, kn, vn, 128 ** -0.5, rows=np.arange(64))
+    o = bf16_to_f32(to_np(out[0].transpose(0, 1)[:64]))
+    assert og.rel_l2(o, ex) < 4e-3                                 # bf16 rounding of the output only
+    rows = np.arange(64, SL, 9)
+    ref = oa.attention_u8_from_codes(oa.prepass_u8(qn, kn, vn), 128 ** -0.5, rows=rows)
+    assert og.rel_l2(bf16_to_f32(to_np(out[0].transpose(0, 1)[rows])), ref) < 2e-3
+
+
+def test_rrcheck_override_records_equality(dev, tmp_path, monkeypatch):
+    """make_override(294): tagged for the fused path with the config-2xx check, which appends one JSON record per
+    block: the fused RMSNorm + RoPE pre-pass and output equal the unfused ones bit for bit."""
+    import json
+    from rapid_h3 import override, patch
+    model, x0, tab = _route_setup(dev, 23)
+    rec = tmp_path / "rr.jsonl"
+    monkeypatch.setenv("RAPIDH3_RRCHECK", str(rec))
+    ov = override.make_override(294)
+    assert ov.rapidh3_rmsrope == 94 and ov.rapidh3_rrcheck
+    p = patch.patch(model, "int8_rot")
+    segs = [(0, SL, 0)]
+
+    def run(x):
+        for i, b in enumerate(model.blocks):
+            x = b(x, None, segs, tab, transformer_options={"optimized_attention_override": ov, "block_index": i})
+        return x
+
+    p.wrapper(run, x0.clone())
+    lines = [json.loads(s) for s in rec.read_text().splitlines()]
+    assert [r["block"] for r in lines] == [0, 1]
+    assert all(r["out_equal"] and r["operands_equal"] and r["max_abs_diff"] == 0.0 and r["S"] == SL for r in lines)
+
+
+def test_stock_attention_for_the_unfused_route(dev):
+    """patch(attention=f) with no override: the block hands f the roped q, k, v; a short sequence under a tagged
+    override (S < 1024) takes the same route and the override falls through to f, as in the reference."""
+    from rapid_h3 import override, patch
+    model, x0, tab = _route_setup(dev, 24)
+    log = []
+
+    def stock(q, k, v, heads, **kw):
+        out = override.stock_attention(q, k, v, heads, **kw)
+        log.append(out)
+        return out
+
+    p = patch.patch(model, "int8_rot", attention=stock)
+    blk = model.blocks[0]
+    p.wrapper(lambda x: blk(x, None, [(0, SL, 0)], tab), x0.clone())
+    assert len(log) == 1 and tuple(log[0].shape) == (1, HEADS, SL, 128)
+    short = x0[:500].clone()
+    tab_s = tab[:, :500].contiguous()
+    p2 = patch.patch(model, "int8_rot", attention=stock)
+    p2.wrapper(lambda x: blk(x, None, [(0, 500, 0)], tab_s,
+                             transformer_options={"optimized_attention_override": override.make_override(194)}),
+               short)
+    assert len(log) == 2 and tuple(log[1].shape) == (1, HEADS, 500, 128)

@@ -100,3 +100,40 @@ def test_weight_cache_key_default_tracks_tensor():
     with torch.no_grad():
         q.module.weight.add_(1)                                     # in-place update bumps the version counter
     assert q.q._key() != k0
+
+
+def test_cpu_and_fp32_activations_take_f_linear():
+    """Activations off the GPU or not bf16 / fp16 take torch's F.linear with the weight in x.dtype, as the reference's
+    _QuantLinear does (__init__.py:147-148): an fp32 CPU forward through a patched stub returns F.linear exactly, and
+    the quantized weight is never made."""
+    import torch.nn.functional as F
+    m = _DiT(2)
+    with torch.no_grad():
+        m.blocks[1].attn.qkv_proj.bias = nn.Parameter(torch.randn(24))
+    p = P.patch(m, "int8_rot", targets="qkv_proj,out_proj")       # no fused paths
+    x = torch.randn(3, 5, 8)
+    for lin in (m.blocks[0].attn.qkv_proj, m.blocks[1].attn.qkv_proj, m.blocks[1].attn.out_proj):
+        got = p.wrapper(lambda t: lin(t), x)
+        assert torch.equal(got, F.linear(x, lin.weight, lin.bias))
+        got16 = p.wrapper(lambda t: lin(t), x.to(torch.float64))
+        assert got16.dtype == torch.float64
+    assert all(q.q.qweight is None for q in p.by_name.values())
+
+
+def test_adopted_convrot_weight_dequantizes_for_f_linear():
+    """An adopted int8_convrot weight (codes of W @ blockdiag(H256)^T and a per-row scale, from the oracle) on the
+    F.linear route: dequantized and rotated back, it reproduces W within the int8 quantization error."""
+    import numpy as np
+    from oracle import quant as oq
+    from oracle.numerics import bf16_to_f32, f32_to_bf16
+    from rapid_h3.linear import QuantLinear
+    rng = np.random.default_rng(8)
+    w = f32_to_bf16((0.02 * rng.standard_normal((48, 512))).astype(np.float32))
+    q, s = oq.quantize_weight(w, "int8_rot")
+    lin = QuantLinear.from_quantized(torch.from_numpy(q), torch.from_numpy(s).reshape(-1))
+    x = torch.from_numpy(rng.standard_normal((7, 512)).astype(np.float32))
+    y = lin(x)
+    ref = x.double() @ torch.from_numpy(bf16_to_f32(w)).double().t()
+    assert y.dtype == torch.float32 and float((y.double() - ref).norm() / ref.norm()) < 0.01
+    wd = lin.dense_weight("cpu", torch.float64)
+    assert float((wd - torch.from_numpy(bf16_to_f32(w)).double()).abs().max()) < 0.02 * 4 / 127
