@@ -13,8 +13,9 @@ with 1 % of channels x20, weights N(0, 0.02) random init, modulation and norm we
                     [--recipe int8_rot] [--attn-config 94] [--model h3]
 
 After the timed block (outside the timed region): the C3 FP8 GEMMs at the three C2 shapes and hipBLASLt's int8
-GEMM (torch._int_mm) beside this build's at the four block shapes (fp8_gemm_c3, int8_gemm_vs_hipblaslt), and the
-CPU baseline (cpu_baseline) on the same block's inputs.
+GEMM (torch._int_mm) beside this build's at the four block shapes (fp8_gemm_c3, int8_gemm_vs_hipblaslt), one block
+at MiniMax-H3's shapes (h3_shapes), one block in the reference's preset numerics (reference_preset: int8_rot
+quantizers, attention config 94), and the CPU baseline (cpu_baseline) on the same block's inputs.
 
 --model h3 runs the same block at MiniMax-H3's own shapes (hidden 5376, 56 x 128 heads, FFN 14336,
 S = 44,992 by default), the shapes of the reference's published GB10 numbers; the default (c2) is the
@@ -138,15 +139,18 @@ def _median_time(fn, runs=5, warmup=1):
     return ts[len(ts) // 2]
 
 
-def cpu_baseline(m, x, w, mod, segments, tab, trace):
-    """The CPU baseline: the build's CPU restatement of the reference's PyTorch path (oracle/, a
-    numpy port: kernels.quantize_rows / quantize_weight, the exact int32 product, the (acc * xs) * ws epilogues, the
-    per-block attention emulation), on the host cores of the GPU box, median of 5 runs after 1 warm-up.
+def cpu_baseline(m, x, w, mod, segments, tab, trace, ms=4096, rows=1024):
+    """The CPU baseline: the build's CPU restatement of the reference's PyTorch path (oracle/, a numpy port:
+    kernels.quantize_rows / quantize_weight, the exact int32 product, the (acc * xs) * ws epilogues, the per-block
+    attention emulation), on the host cores of the GPU box, each part the median of 5 runs after 1 warm-up, sampled
+    as BASELINE.md's CPU plan says:
       * C1 (X [4096, 3072] with 1 % outlier channels, W [3072, 3072] ~ N(0, 0.02), seed 0): measured in full;
-      * the block: every quantizer and GEMM of the timed DiT block on its first MS tokens, and the attention of
-        head 0 for the first R query rows against all keys (the pre-pass of that head in full), on the GPU leg's own
-        inputs (x, the block's int8 weights, its modulation, and the qkv / o / h of a traced run of the same block),
-        extrapolated to the block: token phases x M / MS, attention rows x S / R x H, the pre-pass x H."""
+      * C2: each of the block's four GEMMs with the quantizer that feeds it, on the first `ms` = 4,096 tokens of the
+        GPU leg's own inputs (x, the block's int8 weights, its modulation, and the o / h / x of a traced run of the
+        same block), scaled by M / ms;
+      * C4: the attention of head 0 for the first `rows` = 1,024 query rows against all keys, scaled by
+        (S / rows) x H, and that head's pre-pass over all keys, scaled by H.
+    Each part's time and factor are reported; the block's time is their sum."""
     import numpy as np
     import torch
     from oracle import attn as oa
@@ -174,7 +178,7 @@ def cpu_baseline(m, x, w, mod, segments, tab, trace):
     ops_c1 = 2 * 4096 * 3072 * 3072
 
     # the block sample on the GPU leg's inputs
-    ms, rows = 256, 128
+    ms = min(ms, m)
     T = {k: v for k, v in trace.items()}
     idx = np.zeros(ms, np.int32)
     for a, b, r in segments:
@@ -186,25 +190,32 @@ def cpu_baseline(m, x, w, mod, segments, tab, trace):
     xa = host(T["x_attn"][:ms])
     nw1, nw2 = host(w.norm1_w), host(w.norm2_w)
     wts = {n: (host(getattr(w, n).q), host(getattr(w, n).scale)) for n in ("qkv", "out", "fc1_perm", "fc2")}
-    oqs = {n: host(T[n][:ms]) for n in ("xq1", "xs1", "oq", "os", "xq2", "xs2", "hq", "hs")}
     o_h = host(T["o"][0][:, :ms])                                          # [H, ms, 128] head-major
     h_ = host(T["h"][:ms])
     s = x.shape[0]
+    rows = min(rows, s)
     qkv0 = T["qkv"].view(s, 3, HEADS, D)[:, :, 0]                           # head 0 of the raw projection
     q0, k0, v0 = host(qkv0[:rows, 0]).reshape(rows, 1, D), host(qkv0[:, 1]).reshape(s, 1, D), host(qkv0[:, 2])
     v0 = v0.reshape(s, 1, D)
     tabh = host(tab.reshape(s, 48, 2, 2))
     rr = (tabh, host(w.q_norm_w), host(w.k_norm_w), w.qk_eps)
+    gate_a, gate_m = f32_to_bf16(mods[2][0]), f32_to_bf16(mods[5][0])
 
-    def token_phases():
-        oq.norm_mod_quant_rows_i8(xs_, nw1, w.eps, idx, mods[0], mods[1])
-        og.int8_gemm(oqs["xq1"], oqs["xs1"], *wts["qkv"])
-        oq.heads_quant_rows_i8(o_h)
-        og.int8_gemm_gated_residual(oqs["oq"], oqs["os"], *wts["out"], f32_to_bf16(mods[2][0]), xa)
-        oq.norm_mod_quant_rows_i8(xa, nw2, w.eps, idx, mods[3], mods[4])
-        og.int8_gemm_swiglu(oqs["xq2"], oqs["xs2"], *wts["fc1_perm"])
-        oq.quantize_rows(h_, "int8_rowwise")
-        og.int8_gemm_gated_residual(oqs["hq"], oqs["hs"], *wts["fc2"], f32_to_bf16(mods[5][0]), xa)
+    def qkv_part():
+        xq, xs = oq.norm_mod_quant_rows_i8(xs_, nw1, w.eps, idx, mods[0], mods[1])
+        og.int8_gemm(xq, xs, *wts["qkv"])
+
+    def out_part():
+        oq_, os_ = oq.heads_quant_rows_i8(o_h)
+        og.int8_gemm_gated_residual(oq_, os_, *wts["out"], gate_a, xa)
+
+    def up_part():
+        xq, xs = oq.norm_mod_quant_rows_i8(xa, nw2, w.eps, idx, mods[3], mods[4])
+        og.int8_gemm_swiglu(xq, xs, *wts["fc1_perm"])
+
+    def down_part():
+        hq, hs = oq.quantize_rows(h_, "int8_rowwise")
+        og.int8_gemm_gated_residual(hq, hs, *wts["fc2"], gate_m, xa)
 
     pre = {}
 
@@ -215,21 +226,24 @@ def cpu_baseline(m, x, w, mod, segments, tab, trace):
         q8, qs, k8, ks, _ = pre["ops"]
         oa.attention_from_codes(q8, qs, k8, ks, v0, D ** -0.5, rows=np.arange(rows))
 
-    t_tok = _median_time(token_phases)
-    t_pre = _median_time(prepass)
-    t_att = _median_time(attn_rows)
     gemms, attn_ops = block_ops(m)
-    t_block = t_tok * (m / ms) + t_pre * HEADS + t_att * (s / rows) * HEADS
+    parts = {}
+    for name, fn, factor in (("quant_norm1+gemm_qkv", qkv_part, m / ms), ("quant_heads+gemm_out_gated", out_part, m / ms),
+                             ("quant_norm2+gemm_up_swiglu", up_part, m / ms),
+                             ("quant_h+gemm_down_gated", down_part, m / ms),
+                             ("attn_prepass", prepass, HEADS), ("attn_main", attn_rows, (s / rows) * HEADS)):
+        t = _median_time(fn)
+        parts[name] = {"s": round(t, 3), "factor": round(factor, 1), "s_per_block": round(t * factor, 1)}
+    t_block = sum(p_["s_per_block"] for p_ in parts.values())
     total = sum(gemms.values()) + attn_ops
     return {"value": round(total / t_block / 1e12, 4), "unit": "TOPS", "cores": int(threads), "kind": "port",
             "cpu_model": _cpu_model(), "os_cpu_count": os.cpu_count(), "runs": "median of 5 after 1 warm-up",
             "c1_measured": {"ms": round(t_c1 * 1e3, 1), "tops": round(ops_c1 / t_c1 / 1e12, 4),
                             "workload": "C1 W8A8 linear, 4096 x 3072 x 3072, in full"},
-            "sample": (f"oracle (numpy) on the GPU leg's inputs: the block's 4 quantizers + 4 GEMMs on its first {ms} "
-                       f"tokens ({t_tok:.2f} s, x{m / ms:.0f}), head 0's pre-pass over all {s} keys ({t_pre:.2f} s, "
-                       f"x{HEADS}) and its attention for {rows} query rows ({t_att:.2f} s, x{s / rows * HEADS:.0f}); "
-                       f"extrapolated to the block; C1 measured in full"),
-            "seconds_per_block": round(t_block, 1)}
+            "sample": (f"oracle (numpy) on the GPU leg's inputs: each block GEMM with its quantizer on the first {ms} "
+                       f"tokens (x{m / ms:.1f}), head 0's pre-pass over all {s} keys (x{HEADS}) and its attention for "
+                       f"{rows} query rows (x{s / rows * HEADS:.0f}); extrapolated to the block; C1 measured in full"),
+            "parts": parts, "seconds_per_block": round(t_block, 1)}
 
 
 def gemm_side_measurements(m, device, reps=5):
@@ -325,6 +339,51 @@ def h3_side_measurements(device, recipe, tokens=(22332, 44992)):
     finally:
         HIDDEN, HEADS, FFN = saved
     return res
+
+
+def preset_side_measurement(m, device, steps=2):
+    """The reference's preset numerics at the metric's shape (its RapidH3 presets 190 / 194): every quantizer with the
+    ConvRot H256 rotation (int8_rot weights and activations) and the production attention, config 94 (per-token
+    H128-rotated Q/K, per-channel int8 V, u8 P against each 128-key tile's max, int8 P.V). 1 untimed block, then
+    `steps` blocks timed per phase with events on torch's current stream; runs after the metric's timed region, on
+    fresh synthetic inputs."""
+    import torch
+    from rapid_h3.block import PHASES, fused_block
+    x, w, mod, segments, tab = setup(m, device, "int8_rot")
+    fused_block(x, w, mod, segments, tab, attn_config=94)
+    torch.cuda.synchronize()
+    phase_ms = {p: 0.0 for p in PHASES}
+    lead_in()
+    for _ in range(steps):
+        ev = []
+
+        def mark(name):
+            e = torch.cuda.Event(enable_timing=True)
+            e.record()
+            ev.append((name, e))
+        b = torch.cuda.Event(enable_timing=True)
+        b.record()
+        ev.append(("begin", b))
+        fused_block(x, w, mod, segments, tab, attn_config=94, mark=mark)
+        torch.cuda.synchronize()
+        for (_, e0), (name, e1) in zip(ev[:-1], ev[1:]):
+            phase_ms[name] += e0.elapsed_time(e1) / steps
+    gemms, attn_ops = block_ops(m)
+    qbytes = quant_bytes(m)
+    parts = {}
+    for p_, t in phase_ms.items():
+        parts[p_] = {"ms": round(t, 3)}
+        if p_ in qbytes:
+            parts[p_]["frac_hbm"] = round(qbytes[p_] / (t * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)
+        elif p_ in gemms:
+            parts[p_]["frac_int8_peak"] = round(gemms[p_] / (t * 1e-3) / 1e12 / PEAK_INT8_TOPS, 4)
+    tops = attn_ops / (phase_ms["attn_main"] * 1e-3) / 1e12
+    del x, w, mod, tab
+    torch.cuda.empty_cache()
+    return {"recipe": "int8_rot quantizers and weights + attention config 94 (attn_u8_kernel), the reference's "
+                      "preset numerics", "steps": steps, "ms_per_block": round(sum(phase_ms.values()), 3),
+            "attn_u8_tops": round(tops, 1), "attn_u8_frac_int8_peak": round(tops / PEAK_INT8_TOPS, 4),
+            "parts": parts}
 
 
 def traffic_from_profile():
@@ -556,6 +615,7 @@ def main():
         out["fp8_gemm_c3"] = fp8
         out["int8_gemm_vs_hipblaslt"] = vendor
         out["h3_shapes"] = h3_side_measurements(dev, a.recipe)
+        out["reference_preset"] = preset_side_measurement(m, dev)
     if not a.no_cpu:
         # one traced run of the same block supplies the intermediate tensors the CPU sample starts from
         x_in = x.clone()

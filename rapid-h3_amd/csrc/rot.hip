@@ -112,9 +112,9 @@ __device__ __forceinline__ void tab8(const void* p, int64_t i, float* t) {
   }
 }
 
-// prologue values of the 8 columns c..c+7 of row m
-template <int KIND, typename TabT, bool VEC>
-__device__ __forceinline__ void prologue8(const RotArgs& a, int64_t m, int64_t c, float rstd, int64_t trow, float* v) {
+// prologue values of the 8 columns c..c+7 of row m (the plain row, silu(g) * u, or the head-major gather)
+template <int KIND>
+__device__ __forceinline__ void prologue8(const RotArgs& a, int64_t m, int64_t c, float* v) {
   if (KIND == ROT_HEADS) {
     unpack8(*reinterpret_cast<const uint4*>(a.x + (c >> 7) * a.ld_head + m * a.ldx + (c & 127)), v);
   } else if (KIND == ROT_SWIGLU) {
@@ -126,69 +126,91 @@ __device__ __forceinline__ void prologue8(const RotArgs& a, int64_t m, int64_t c
     for (int e = 0; e < 8; ++e) v[e] = silu_mul_f(g[e], u[e]);
   } else {
     unpack8(*reinterpret_cast<const uint4*>(a.x + m * a.ldx + c), v);
-    if (KIND == ROT_NORMMOD) {
-      float wv[8], sc[8], sh[8];
-      if (a.w) unpack8(*reinterpret_cast<const uint4*>(a.w + c), wv);
-      tab8<TabT, VEC>(a.scale, trow + c, sc);
-      tab8<TabT, VEC>(a.shift, trow + c, sh);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        float y = v[e] * rstd;
-        if (a.w) y = y * wv[e];
-        v[e] = y * (1.0f + sc[e]) + sh[e];
-      }
-    }
   }
 }
 
-// y = the rotated values of chunk ch (zeros for a lane past the row: its whole quad is past it)
-template <int KIND, typename TabT, bool VEC>
-__device__ __forceinline__ void rot_act_chunk(const RotArgs& a, int64_t m, int64_t ch, bool valid, float rstd,
-                                              int64_t trow, float sb, float sc, float sd, float (&y)[64]) {
-  double d[64];
-  if (valid) {
-#pragma unroll
-    for (int t = 0; t < 8; ++t) {
-      float v[8];
-      prologue8<KIND, TabT, VEC>(a, m, ch * 64 + 8 * t, rstd, trow, v);
-#pragma unroll
-      for (int e = 0; e < 8; e += 2) {  // bf16 round to nearest even (v_cvt_pk_bf16_f32), back to fp32 exactly
-        const uint32_t pk = pk_bf16_hw(v[e], v[e + 1]);
-        d[8 * t + e] = static_cast<double>(__uint_as_float(pk << 16));
-        d[8 * t + e + 1] = static_cast<double>(__uint_as_float(pk & 0xffff0000u));
-      }
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < 64; ++i) d[i] = 0.0;
-  }
+// The fp32 H4 combine of four chunk values z of a lane quad, before the halving: lane q computes
+// t_q = ((A + sB B) + sC C) + sD D with (A, B, C, D) its quad's z in the order of the reference's formula for y_q
+// (lanes 0-2: z0, z1, z2, z3; lane 3: z1, z2, z3, z0) and the lane's signs. Each term is one v_fmac_f32 whose first
+// operand arrives through a DPP quad permutation (the product with +-1 is exact, so each step is the reference's add
+// or subtract rounded once). Four elements per block; s_nop 1 gives the DPP reads of z the two wait states a VALU
+// write needs before them.
+__device__ __forceinline__ void quad_combine4(const float* z, float sb, float sc, float sd, float* t) {
+  asm volatile(
+      "s_nop 1\n\t"
+      "v_mov_b32_dpp %0, %4 quad_perm:[0,0,0,1] row_mask:0xf bank_mask:0xf\n\t"
+      "v_mov_b32_dpp %1, %5 quad_perm:[0,0,0,1] row_mask:0xf bank_mask:0xf\n\t"
+      "v_mov_b32_dpp %2, %6 quad_perm:[0,0,0,1] row_mask:0xf bank_mask:0xf\n\t"
+      "v_mov_b32_dpp %3, %7 quad_perm:[0,0,0,1] row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %0, %4, %8 quad_perm:[1,1,1,2] row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %1, %5, %8 quad_perm:[1,1,1,2] row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %2, %6, %8 quad_perm:[1,1,1,2] row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %3, %7, %8 quad_perm:[1,1,1,2] row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %0, %4, %9 quad_perm:[2,2,2,3] row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %1, %5, %9 quad_perm:[2,2,2,3] row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %2, %6, %9 quad_perm:[2,2,2,3] row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %3, %7, %9 quad_perm:[2,2,2,3] row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %0, %4, %10 quad_perm:[3,3,3,0] row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %1, %5, %10 quad_perm:[3,3,3,0] row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %2, %6, %10 quad_perm:[3,3,3,0] row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %3, %7, %10 quad_perm:[3,3,3,0] row_mask:0xf bank_mask:0xf"
+      : "=&v"(t[0]), "=&v"(t[1]), "=&v"(t[2]), "=&v"(t[3])
+      : "v"(z[0]), "v"(z[1]), "v"(z[2]), "v"(z[3]), "v"(sb), "v"(sc), "v"(sd));
+}
+
+// H64 of the lane's chunk d (bf16 values, exact in float64), rounded once to fp32, then the fp32 H4 combine of
+// the quad's four chunks in the reference's order. t = 2 y: the reference's final halving is folded into the
+// quantization scale (rot_scale), which gives the same scale and codes (see there).
+__device__ __forceinline__ void rot_combine(double (&d)[64], float sb, float sc, float sd, float (&t)[64]) {
   h64(d);
+  float z[64];
 #pragma unroll
-  for (int i = 0; i < 64; ++i) {
-    const float z = static_cast<float>(d[i] * 0.125);
-    // lane q computes y_q = ((A + sB*B) + sC*C) + sD*D with the chunk values of its quad (fma with +-1 is
-    // the exact sum rounded once, i.e. the same as the add or subtract of the reference's formula)
-    const float A = quad_f<0x40>(z), B = quad_f<0x95>(z), C = quad_f<0xEA>(z), D = quad_f<0x3F>(z);
-    float t = fmaf(sb, B, A);
-    t = fmaf(sc, C, t);
-    t = fmaf(sd, D, t);
-    y[i] = t * 0.5f;
-  }
+  for (int i = 0; i < 64; ++i) z[i] = static_cast<float>(d[i] * 0.125);
+#pragma unroll
+  for (int i = 0; i < 64; i += 4) quad_combine4(z + i, sb, sc, sd, t + i);
 }
 
-__device__ __forceinline__ void store64(int8_t* q, const float (&y)[64], float inv) {
+// Row scale and quantization multiplier from the largest |t| (t = 2 y). With y = t / 2 the reference computes
+// s = max(max|y| / 127, 1e-12) and q = rint(clamp(y * (1 / s), +-127)). Halving is exact for every normal t, so
+// max|y| = max|t| / 2 and y * inv = t * (inv / 2); where t / 2 would be subnormal (|t| < 2^-125) both products lie
+// below 2^-125 * 1e12 and round to the code 0, and a subnormal max|t| / 2 leaves s at its 1e-12 floor either way.
+// The clamp never binds: |y * inv| <= 127 (1 + 2^-22) < 127.5.
+__device__ __forceinline__ float rot_scale(float amax_t, float* inv_half) {
+  const float s = fmaxf((amax_t * 0.5f) / 127.0f, 1e-12f);
+  *inv_half = (1.0f / s) * 0.5f;
+  return s;
+}
+
+// y = the rotated values (times 2) of chunk ch. A lane past the row (valid false; its whole quad is past it) works on
+// chunk 0 of its row instead, an in-bounds read whose results the caller discards.
+template <int KIND>
+__device__ __forceinline__ void rot_act_chunk(const RotArgs& a, int64_t m, int64_t ch, bool valid, float sb, float sc,
+                                              float sd, float (&y)[64]) {
+  double d[64];
+  const int64_t c0 = valid ? ch * 64 : 0;
 #pragma unroll
   for (int t = 0; t < 8; ++t) {
-    uint32_t b[8];
+    float v[8];
+    prologue8<KIND>(a, m, c0 + 8 * t, v);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float r = rintf(fminf(fmaxf(y[8 * t + e] * inv, -127.0f), 127.0f));
-      b[e] = static_cast<uint32_t>(static_cast<int32_t>(r)) & 0xffu;
+    for (int e = 0; e < 8; e += 2) {  // bf16 round to nearest even (v_cvt_pk_bf16_f32), back to fp32 exactly
+      const uint32_t pk = pk_bf16_hw(v[e], v[e + 1]);
+      d[8 * t + e] = static_cast<double>(__uint_as_float(pk << 16));
+      d[8 * t + e + 1] = static_cast<double>(__uint_as_float(pk & 0xffff0000u));
     }
-    uint2 o;
-    o.x = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
-    o.y = b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24);
-    *reinterpret_cast<uint2*>(q + 8 * t) = o;
+  }
+  rot_combine(d, sb, sc, sd, y);
+}
+
+// codes rint(t * inv_half) of the 64 values of a chunk: pack4_codes rounds to nearest even by its magic-number add
+// (|t * inv_half| < 127.5 < 2^22) and packs the low bytes
+__device__ __forceinline__ void store64(int8_t* q, const float (&t)[64], float inv_half) {
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    float n[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) n[e] = t[8 * k + e] * inv_half;
+    *reinterpret_cast<uint2*>(q + 8 * k) = make_uint2(pack4_codes(n), pack4_codes(n + 4));
   }
 }
 
@@ -197,7 +219,7 @@ __device__ __forceinline__ void store64(int8_t* q, const float (&y)[64], float i
 // lane, lane-interleaved float4s, a private region per wave) until the row scale is known.
 template <int NP> constexpr int rot_waves() { return NP <= 2 ? 4 : 2; }
 
-template <int KIND, typename TabT, int NP, bool VEC>
+template <int KIND, int NP>
 __global__ void __launch_bounds__(64 * rot_waves<NP>()) rot_quant_kernel(const RotArgs a) {
   constexpr int W = rot_waves<NP>();
   __shared__ float4 stash[NP > 1 ? W * (NP - 1) * 16 * 64 : 1];  // [wave][pass][i / 4][lane]
@@ -206,29 +228,7 @@ __global__ void __launch_bounds__(64 * rot_waves<NP>()) rot_quant_kernel(const R
   if (m >= a.M) return;  // whole wavefront: DPP partners never leave; no workgroup barrier below
   const int q4 = lane & 3;
   const float sb = q4 == 2 ? -1.0f : 1.0f, sc = q4 == 1 ? -1.0f : 1.0f, sd = (q4 == 0 || q4 == 3) ? -1.0f : 1.0f;
-  float rstd = 0.0f;
-  int64_t trow = 0;
-  if (KIND == ROT_NORMMOD) {
-    // sum of squares in the order of quant.hip (lane chunks 512 j + 8 l, (j, e) sequential, butterfly);
-    // all of the row's loads are issued before the first product (K <= 4096 * NP, so j < 8 * NP)
-    uint4 r[8 * NP];
-#pragma unroll
-    for (int j = 0; j < 8 * NP; ++j) {
-      const int64_t c = 512 * j + 8 * lane;
-      r[j] = c < a.K ? *reinterpret_cast<const uint4*>(a.x + m * a.ldx + c) : make_uint4(0, 0, 0, 0);
-    }
-    float ss = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 8 * NP; ++j) {
-      float v[8];
-      unpack8(r[j], v);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) ss = ss + v[e] * v[e];
-    }
-    ss = wave_sum_tree(ss);
-    rstd = 1.0f / sqrtf(ss / static_cast<float>(a.K) + a.eps);
-    trow = static_cast<int64_t>(a.idx[m]) * a.ld_tab;
-  }
+  static_assert(KIND != ROT_NORMMOD, "RMSNorm + modulation runs in rot_normmod_kernel");
   const int64_t nchunks = a.K / 64;
   float4* my = stash + wave * (NP - 1) * 16 * 64 + lane;
   float y[64];
@@ -236,17 +236,19 @@ __global__ void __launch_bounds__(64 * rot_waves<NP>()) rot_quant_kernel(const R
 #pragma unroll
   for (int p = 0; p < NP; ++p) {
     const int64_t ch = 64 * p + lane;
-    rot_act_chunk<KIND, TabT, VEC>(a, m, ch, ch < nchunks, rstd, trow, sb, sc, sd, y);
+    rot_act_chunk<KIND>(a, m, ch, ch < nchunks, sb, sc, sd, y);
+    float am = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 64; ++i) amax = fmaxf(amax, fabsf(y[i]));
+    for (int i = 0; i < 64; i += 2) am = max3_abs(am, y[i], y[i + 1]);
+    if (ch < nchunks) amax = fmaxf(amax, am);
     if (p < NP - 1) {
 #pragma unroll
       for (int t = 0; t < 16; ++t) my[(p * 16 + t) * 64] = make_float4(y[4 * t], y[4 * t + 1], y[4 * t + 2], y[4 * t + 3]);
     }
   }
   amax = wave_max(amax);
-  const float s = fmaxf(amax / 127.0f, 1e-12f);
-  const float inv = 1.0f / s;
+  float inv;
+  const float s = rot_scale(amax, &inv);
   if (lane == 0) a.s[m] = s;
   const int64_t last = 64 * (NP - 1) + lane;
   if (last < nchunks) store64(a.q + m * a.ldq + 64 * last, y, inv);
@@ -259,6 +261,134 @@ __global__ void __launch_bounds__(64 * rot_waves<NP>()) rot_quant_kernel(const R
       y[4 * t] = u.x; y[4 * t + 1] = u.y; y[4 * t + 2] = u.z; y[4 * t + 3] = u.w;
     }
     if (ch < nchunks) store64(a.q + m * a.ldq + 64 * ch, y, inv);
+  }
+}
+
+// RMSNorm + modulation, rotation and INT8 with the prologue staged through LDS. Phase 1 works in the coalesced
+// layout of the sum of squares (lane l holds columns 512 j + 8 l .. +7): the row, the norm weight and both
+// modulation rows are read with whole-wave 16-byte accesses, the prologue values are computed there (the same
+// operations in the same order as the unrotated quantizer's prologue) and written to the wave's LDS region as bf16,
+// chunk-major with a 144-byte chunk pitch (lanes reading their own chunk then hit 16 distinct bank quads). Phase 2 is
+// the rotation of rot_quant_kernel with each lane's chunk read from LDS instead of gathered from global memory. A wave
+// can walk RPW consecutive rows, issuing the next row's loads before the current row's rotation; that holds the loaded
+// row through the rotation (222 registers, 2 waves per SIMD) and measured slower than one row per wave at 3 waves per
+// SIMD (0.71 vs 0.64 ms at 145,152 x 3072), so RPW is 1. A wave uses only its own LDS region (in order: a row's
+// phase-1 writes follow the previous row's phase-2 reads), so no workgroup barrier is needed.
+constexpr int STAGE_PITCH = 144;
+template <int NP> constexpr int nm_waves() { return NP == 1 ? 4 : (NP == 2 ? 2 : 1); }
+template <int NP> constexpr int nm_rows() { return 1; }
+
+template <typename TabT, int NP, bool VEC>
+__global__ void __launch_bounds__(64 * nm_waves<NP>()) rot_normmod_kernel(const RotArgs a) {
+  constexpr int W = nm_waves<NP>(), RPW = nm_rows<NP>();
+  __shared__ __attribute__((aligned(16))) uint8_t stage[W * 64 * NP * STAGE_PITCH];
+  __shared__ float4 stash[NP > 1 ? W * (NP - 1) * 16 * 64 : 1];  // [wave][pass][i / 4][lane]
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t m0 = (static_cast<int64_t>(blockIdx.x) * W + wave) * RPW;
+  if (m0 >= a.M) return;  // whole wavefront: DPP partners never leave; no workgroup barrier below
+  const int nrows = static_cast<int>(min(static_cast<int64_t>(RPW), a.M - m0));
+  uint8_t* st = stage + wave * 64 * NP * STAGE_PITCH;
+  const int q4 = lane & 3;
+  const float sb = q4 == 2 ? -1.0f : 1.0f, sc = q4 == 1 ? -1.0f : 1.0f, sd = (q4 == 0 || q4 == 3) ? -1.0f : 1.0f;
+  const int64_t nchunks = a.K / 64;
+  float4* my = stash + wave * (NP - 1) * 16 * 64 + lane;
+  // the row's loads, all issued before the first product (K <= 4096 * NP, so j < 8 * NP)
+  uint4 r[8 * NP];
+  auto load_row = [&](int64_t m) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < 8 * NP; ++j) {
+      const int64_t c = 512 * j + 8 * lane;
+      r[j] = c < a.K ? *reinterpret_cast<const uint4*>(a.x + m * a.ldx + c) : make_uint4(0, 0, 0, 0);
+    }
+  };
+  load_row(m0);
+  for (int ri = 0; ri < nrows; ++ri) {
+    const int64_t m = m0 + ri;
+    const int64_t trow = static_cast<int64_t>(a.idx[m]) * a.ld_tab;
+    // phase 1. Sum of squares in the order of quant.hip (lane chunks 512 j + 8 l, (j, e) sequential, butterfly)
+    float xv[8 * NP][8];
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8 * NP; ++j) {
+      unpack8(r[j], xv[j]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss = fmaf(xv[j][e], xv[j][e], ss);  // x * x is exact (bf16 x): = ss + x * x
+    }
+    if (ri + 1 < nrows) load_row(m + 1);
+    ss = wave_sum_tree(ss);
+    const float rstd = 1.0f / sqrtf(ss / static_cast<float>(a.K) + a.eps);
+#pragma unroll
+    for (int j = 0; j < 8 * NP; ++j) {
+      const int64_t c = 512 * j + 8 * lane;
+      if (c < a.K) {
+        float* v = xv[j];
+        float wv[8], scl[8], shf[8];
+        if (a.w) unpack8(*reinterpret_cast<const uint4*>(a.w + c), wv);
+        tab8<TabT, VEC>(a.scale, trow + c, scl);
+        tab8<TabT, VEC>(a.shift, trow + c, shf);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          float y = v[e] * rstd;
+          if (a.w) y = y * wv[e];
+          v[e] = y * (1.0f + scl[e]) + shf[e];
+        }
+        uint4 o;
+        o.x = pk_bf16_hw(v[0], v[1]);
+        o.y = pk_bf16_hw(v[2], v[3]);
+        o.z = pk_bf16_hw(v[4], v[5]);
+        o.w = pk_bf16_hw(v[6], v[7]);
+        *reinterpret_cast<uint4*>(st + (c >> 6) * STAGE_PITCH + (c & 63) * 2) = o;
+      }
+    }
+    // the wave's own LDS writes are complete before its lanes read each other's columns
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_wave_barrier();
+    // phase 2: lane l rotates chunk 64 p + l
+    float y[64];
+    float amax = 0.0f;
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      const int64_t ch = 64 * p + lane;
+      // a lane past the row (its whole quad is) reads its slot of the wave's region all the same (ch < 64 NP) and
+      // its results are discarded
+      double d[64];
+      const uint8_t* src = st + ch * STAGE_PITCH;
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        const uint4 u = *reinterpret_cast<const uint4*>(src + 16 * t);
+        const uint32_t w4[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          d[8 * t + 2 * e] = static_cast<double>(__uint_as_float(w4[e] << 16));
+          d[8 * t + 2 * e + 1] = static_cast<double>(__uint_as_float(w4[e] & 0xffff0000u));
+        }
+      }
+      rot_combine(d, sb, sc, sd, y);
+      float am = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 64; i += 2) am = max3_abs(am, y[i], y[i + 1]);
+      if (ch < nchunks) amax = fmaxf(amax, am);
+      if (p < NP - 1) {
+#pragma unroll
+        for (int t = 0; t < 16; ++t) my[(p * 16 + t) * 64] = make_float4(y[4 * t], y[4 * t + 1], y[4 * t + 2], y[4 * t + 3]);
+      }
+    }
+    amax = wave_max(amax);
+    float inv;
+    const float s = rot_scale(amax, &inv);
+    if (lane == 0) a.s[m] = s;
+    const int64_t last = 64 * (NP - 1) + lane;
+    if (last < nchunks) store64(a.q + m * a.ldq + 64 * last, y, inv);
+#pragma unroll
+    for (int p = 0; p < NP - 1; ++p) {
+      const int64_t ch = 64 * p + lane;
+#pragma unroll
+      for (int t = 0; t < 16; ++t) {
+        const float4 u = my[(p * 16 + t) * 64];
+        y[4 * t] = u.x; y[4 * t + 1] = u.y; y[4 * t + 2] = u.z; y[4 * t + 3] = u.w;
+      }
+      if (ch < nchunks) store64(a.q + m * a.ldq + 64 * ch, y, inv);
+    }
   }
 }
 
@@ -373,28 +503,40 @@ __global__ void __launch_bounds__(256) rot_exact_kernel(const ExactArgs a) {
   }
 }
 
-template <int KIND, typename TabT, bool VEC>
-void launch_act_np(const RotArgs& a, hipStream_t st) {
-  if (a.K <= 4096) {
-    hipLaunchKernelGGL((rot_quant_kernel<KIND, TabT, 1, VEC>), dim3(static_cast<unsigned>((a.M + 3) / 4)), dim3(256), 0,
-                       st, a);
-  } else if (a.K <= 8192) {
-    hipLaunchKernelGGL((rot_quant_kernel<KIND, TabT, 2, VEC>), dim3(static_cast<unsigned>((a.M + 3) / 4)), dim3(256), 0,
-                       st, a);
-  } else {
-    hipLaunchKernelGGL((rot_quant_kernel<KIND, TabT, 4, VEC>), dim3(static_cast<unsigned>((a.M + 1) / 2)), dim3(128), 0,
-                       st, a);
-  }
+template <typename TabT, bool VEC>
+void launch_normmod(const RotArgs& a, hipStream_t st) {
+  if (a.K <= 4096)
+    hipLaunchKernelGGL((rot_normmod_kernel<TabT, 1, VEC>), dim3(static_cast<unsigned>((a.M + 3) / 4)), dim3(256), 0, st,
+                       a);
+  else if (a.K <= 8192)
+    hipLaunchKernelGGL((rot_normmod_kernel<TabT, 2, VEC>), dim3(static_cast<unsigned>((a.M + 1) / 2)), dim3(128), 0, st,
+                       a);
+  else
+    hipLaunchKernelGGL((rot_normmod_kernel<TabT, 4, VEC>), dim3(static_cast<unsigned>(a.M)), dim3(64), 0, st, a);
+}
+
+template <int KIND>
+void launch_rot(const RotArgs& a, hipStream_t st) {
+  if (a.K <= 4096)
+    hipLaunchKernelGGL((rot_quant_kernel<KIND, 1>), dim3(static_cast<unsigned>((a.M + 3) / 4)), dim3(256), 0, st, a);
+  else if (a.K <= 8192)
+    hipLaunchKernelGGL((rot_quant_kernel<KIND, 2>), dim3(static_cast<unsigned>((a.M + 3) / 4)), dim3(256), 0, st, a);
+  else
+    hipLaunchKernelGGL((rot_quant_kernel<KIND, 4>), dim3(static_cast<unsigned>((a.M + 1) / 2)), dim3(128), 0, st, a);
 }
 
 template <int KIND, typename TabT>
 int launch_act(const RotArgs& a, hipStream_t st, const char* name) {
   if (a.M == 0) return RH3_OK;
-  // 16-byte modulation-table loads when every row start is 16-byte aligned
-  const bool vec = KIND != ROT_NORMMOD ||
-                   (aligned16(a.shift) && aligned16(a.scale) && (a.ld_tab * static_cast<int64_t>(sizeof(TabT))) % 16 == 0);
-  if (vec) launch_act_np<KIND, TabT, true>(a, st);
-  else launch_act_np<KIND, TabT, false>(a, st);
+  if constexpr (KIND == ROT_NORMMOD) {
+    // 16-byte modulation-table loads when every row start is 16-byte aligned
+    if (aligned16(a.shift) && aligned16(a.scale) && (a.ld_tab * static_cast<int64_t>(sizeof(TabT))) % 16 == 0)
+      launch_normmod<TabT, true>(a, st);
+    else
+      launch_normmod<TabT, false>(a, st);
+  } else {
+    launch_rot<KIND>(a, st);
+  }
   return launch_status(name);
 }
 
