@@ -168,7 +168,7 @@ struct FwdArgs {
   int nmain;    // workgroups 0 .. nmain-1 run ids 0 .. nmain-1 whole
   int npair;    // items nmain + i and nmain + npair + i run the two key halves of id nmain + i
   float* tail;  // [2][npair][FWD_BQ][TAIL_ROW] fp32 partials of the split ids
-  int* ctr;     // work counter, zero at launch: a starting workgroup takes item ctr++
+  int* ctr;     // CLAIM_COUNTERS work counters, zero at launch (claim_item)
 };
 
 // a wave-uniform float (lane 0's value), held in an SGPR
@@ -473,20 +473,20 @@ __device__ __forceinline__ void fwd_body(const FwdArgs& a, const int bid, int8_t
 }
 
 // One launch over nmain + 2 npair items, the unsplit ids first, then the split halves (which take CUs as the last
-// unsplit items finish). A workgroup runs the item it takes from the work counter when it starts, not the one its
-// position names: the grid is dealt to the XCDs in fixed shares, and the XCDs run at different clocks (workgroup
-// times differ by up to 7 % between them), so fixed items would leave the fast XCDs idle while the slowest
-// finishes. The grid holds more workgroups than items; a fast XCD starts its queued workgroups sooner and takes
-// more items, and the workgroups that find the items gone return at once. The LDS rings and scale table are
+// unsplit items finish). A workgroup runs the item it claims when it starts (claim_item: its XCD's share of the
+// unsplit ids first), not the one its position names: the grid is dealt to the XCDs in fixed shares, and the XCDs
+// run at different clocks (workgroup times differ by up to 7 % between them), so fixed items would leave the fast
+// XCDs idle while the slowest finishes. The grid holds more workgroups than items; a fast XCD starts its queued
+// workgroups sooner and takes more items, and the workgroups that find the items gone return at once. The LDS rings and scale table are
 // declared once, shared by both bodies.
 __global__ void __launch_bounds__(FWD_NT, 1) attn_fwd_kernel(const FwdArgs a) {
   __shared__ __attribute__((aligned(16))) int8_t ring[NRING * (KSLOT + VSLOT)];
   __shared__ float2 kscale[4096];  // per-128-key-block (K scale, K scale x key-norm bound) of this head
   __shared__ int item_s;
-  if (threadIdx.x == 0) item_s = atomicAdd(a.ctr, 1);
+  if (threadIdx.x == 0) item_s = claim_item(a.ctr, a.nmain, 2 * a.npair, blockIdx.x);
   __syncthreads();
   const int item = __builtin_amdgcn_readfirstlane(item_s);
-  if (item >= a.nmain + 2 * a.npair) return;
+  if (item < 0) return;
   if (item < a.nmain)
     fwd_body<false>(a, item, ring, ring + NRING * KSLOT, kscale);
   else
@@ -592,7 +592,7 @@ int forward(const Work& w, int64_t Sq, int64_t Sk, int64_t H, float scale, uint1
   const int64_t items = nmain + 2 * static_cast<int64_t>(npair);
   const int64_t grid = items + (items + 3) / 4;
   // the counter is cleared by a fill kernel, not hipMemsetAsync, so the call stays safe inside a captured HIP graph
-  hipLaunchKernelGGL(zero_kernel, dim3(1), dim3(64), 0, st, reinterpret_cast<float*>(w.ctr), int64_t{1});
+  hipLaunchKernelGGL(zero_kernel, dim3(1), dim3(64), 0, st, reinterpret_cast<float*>(w.ctr), CLAIM_COUNTERS);
   hipLaunchKernelGGL(attn_fwd_kernel, dim3(static_cast<uint32_t>(grid)), dim3(FWD_NT), 0, st, f);
   if (npair > 0)
     hipLaunchKernelGGL(attn_combine_kernel, dim3(npair, FWD_BQ / 16), dim3(256), 0, st, w.tail, npair, nmain, nqb, Sq,

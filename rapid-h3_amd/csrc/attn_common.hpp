@@ -71,6 +71,29 @@ __global__ void zero_kernel(float* __restrict__ p, int64_t n) {
   if (i < n) p[i] = 0.0f;
 }
 
+// The main kernels' work items, claimed per XCD. The dispatcher deals workgroups to the 8 XCDs round-robin (linear
+// workgroup id bid on XCD bid % 8); XCD x owns the contiguous share [x nmain / 8, (x + 1) nmain / 8) of the main items,
+// whose order (query blocks fastest) makes a share a few whole heads, so the K / V tiles its workgroups stream stay
+// in that XCD's L2. A workgroup takes the next item of its own XCD's share, then of the other XCDs' shares in turn
+// (so a fast XCD finishes a slow one's share), then of the tail items [nmain, nmain + ntail); -1 when every item is
+// taken. ctr[0 .. 8] are zero at launch. The grid holds more workgroups than items, so every item is taken: a
+// workgroup that gets -1 saw every counter past its end.
+__device__ __forceinline__ int claim_item(int* ctr, int nmain, int ntail, int bid) {
+  const int x = bid & 7;
+#pragma unroll 1
+  for (int k = 0; k < 8; ++k) {
+    const int y = (x + k) & 7;
+    const int lo = static_cast<int>((static_cast<int64_t>(y) * nmain) >> 3);
+    const int n = static_cast<int>((static_cast<int64_t>(y + 1) * nmain) >> 3) - lo;
+    if (__hip_atomic_load(ctr + y, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= n) continue;
+    const int c = atomicAdd(ctr + y, 1);
+    if (c < n) return lo + c;
+  }
+  const int c = atomicAdd(ctr + 8, 1);
+  return c < ntail ? nmain + c : -1;
+}
+constexpr int64_t CLAIM_COUNTERS = 9;
+
 // grid (H), KMEAN_NT threads: group j of 128 channels sums chunks j, j + 8, ..., then the 8 groups
 constexpr int KMEAN_NT = 1024;
 __global__ void __launch_bounds__(KMEAN_NT) kmean_kernel(const double* __restrict__ part, int nchunk, int64_t S,

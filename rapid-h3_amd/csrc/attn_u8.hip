@@ -392,8 +392,9 @@ __global__ void __launch_bounds__(U8_NT, 1) attn_u8_kernel(const U8Args a) {
   constexpr bool BK = MODE == 1;
   constexpr int KB = TILE * D, VB = D * TILE, SLOT = KB + VB + SIDE;
   __shared__ __attribute__((aligned(16))) int8_t ring[4 * SLOT];
-  // the workgroup runs the item it takes from the work counter when it starts (a fast XCD takes more; see the
-  // launch), the (head, query block) pair h * nqb + qb
+  // the workgroup runs the item it takes from one work counter when it starts (a fast XCD takes more; see the
+  // launch), the (head, query block) pair h * nqb + qb. Per-XCD shares (claim_item) measured 1.6 % slower here
+  // (180.3 vs 177.4 ms at C4), so this kernel keeps the single counter.
   __shared__ int item_s;
   if (threadIdx.x == 0) item_s = atomicAdd(a.ctr, 1);
   __syncthreads();
