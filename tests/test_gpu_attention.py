@@ -1,6 +1,6 @@
 """GPU parity of the INT8 attention (librh3 rh3_int8_attention*, rh3_attention_prepass) against the CPU
-oracle: bit-exact Q/K int8 codes, per-block scales and kmean; V^T layout exact; output within
-rel-L2 1e-2 of the oracle's float64 attention on the same int8 operands."""
+oracle: bit-exact Q/K int8 codes, per-block scales and kmean; V^T layout exact; output within rel-L2 4e-3 (GUARD,
+tighter than the north star's 1e-2) of the oracle's float64 attention on the same int8 operands."""
 import numpy as np
 import pytest
 
@@ -11,7 +11,12 @@ from oracle.numerics import bf16_to_f32, f32_to_bf16
 
 pytestmark = pytest.mark.gpu
 
-TOL = 1e-2
+TOL = 1e-2     # the north star's bar for the attention output (rel-L2)
+# The regression guard every output check here asserts: measured errors against the oracle are 2.25e-3 to 2.40e-3
+# on every case (and 6e-4 between the split and whole schedules), so an error that grows by 70 % fails, well before
+# the 1e-2 bar would.
+GUARD = 4e-3
+assert GUARD < TOL
 
 
 def _bf(a):
@@ -46,7 +51,7 @@ def test_attention_golden(dev, golden):
     pp = attention.prepass(q, k, v)
     _check_prepass(pp, g["q8"], g["qs"], g["k8"], g["ks"], g["kmean"], g["v"], g["v"].shape[0])
     out = bf16_to_f32(to_np(attention.attention(q, k, v)))
-    assert rel_l2(out, g["out"]) < TOL
+    assert rel_l2(out, g["out"]) < GUARD
 
 
 def test_attention_rr_golden(dev, golden):
@@ -62,7 +67,7 @@ def test_attention_rr_golden(dev, golden):
     q0, k0 = q.clone(), k.clone()
     out = attention.attention_rr(q, k, v, tab, qw, kw, 1e-5, config=None)     # the per-block recipe
     assert torch.equal(q, q0) and torch.equal(k, k0)        # q, k untouched
-    assert rel_l2(bf16_to_f32(to_np(out)), g["rout"]) < TOL
+    assert rel_l2(bf16_to_f32(to_np(out)), g["rout"]) < GUARD
 
 
 def test_cross_attention_golden(dev, golden):
@@ -74,7 +79,7 @@ def test_cross_attention_golden(dev, golden):
     pp = attention.prepass(q, k, v)
     assert np.array_equal(to_np(pp["k8"]), g["ck8"]) and np.array_equal(to_np(pp["ks"]), g["cks"])
     out = bf16_to_f32(to_np(attention.attention(q, k, v)))
-    assert rel_l2(out, g["cout"]) < TOL
+    assert rel_l2(out, g["cout"]) < GUARD
 
 
 @pytest.mark.parametrize("sq,sk,h", [(1, 1, 1), (129, 129, 3), (77, 512, 2), (1000, 257, 1)])
@@ -87,7 +92,7 @@ def test_attention_ragged(dev, sq, sk, h):
     out = bf16_to_f32(to_np(attention.attention(to_dev(q, dev), to_dev(k, dev), to_dev(v, dev))))
     q8, qs, k8, ks, _ = oa.prepass(q, k)
     ref = oa.attention_from_codes(q8, qs, k8, ks, v, 128 ** -0.5)[:sq]
-    assert rel_l2(out, ref) < TOL
+    assert rel_l2(out, ref) < GUARD
 
 
 def test_attention_strided_out(dev):
@@ -106,7 +111,7 @@ def test_attention_strided_out(dev):
     q8, qs, k8, ks, _ = oa.prepass(b[:, 0], b[:, 1])
     ref = oa.attention_from_codes(q8, qs, k8, ks, b[:, 2], 128 ** -0.5)[:s]
     got = bf16_to_f32(to_np(o[0].transpose(0, 1)))
-    assert rel_l2(got, ref) < TOL
+    assert rel_l2(got, ref) < GUARD
 
 
 @pytest.mark.parametrize("sk,head_major", [(2600, False), (1100, True), (2600, "padded")])
@@ -142,12 +147,12 @@ def test_attention_split_tail(dev, sk, head_major):
     for hh in [0] + tail_heads:
         q8, qs, k8, ks, _ = oa.prepass(q[:, hh:hh + 1], k[:, hh:hh + 1])
         ref = oa.attention_from_codes(q8, qs, k8, ks, v[:, hh:hh + 1], 128 ** -0.5)[:s, 0]
-        assert rel_l2(out[:, hh], ref) < TOL, hh
+        assert rel_l2(out[:, hh], ref) < GUARD, hh
         # each split query block on its own, so a wrong merge of one pair cannot hide in the head's norm
         for i in range(nqb * h - last, nqb * h):
             if i // nqb == hh:
                 r0, r1 = (i % nqb) * 384, min((i % nqb + 1) * 384, s)
-                assert rel_l2(out[r0:r1, hh], ref[r0:r1]) < TOL, (hh, i % nqb)
+                assert rel_l2(out[r0:r1, hh], ref[r0:r1]) < GUARD, (hh, i % nqb)
 
 
 def test_attention_split_switch(dev, monkeypatch):
@@ -168,11 +173,11 @@ def test_attention_split_switch(dev, monkeypatch):
     monkeypatch.setenv("RH3_ATTN_SPLIT", "0")
     whole = bf16_to_f32(to_np(attention.attention(*args)))
     monkeypatch.delenv("RH3_ATTN_SPLIT")
-    assert rel_l2(split, whole) < TOL
+    assert rel_l2(split, whole) < GUARD
     hh = h - 1                                               # the last head holds split workgroups
     q8, qs, k8, ks, _ = oa.prepass(q[:, hh:hh + 1], k[:, hh:hh + 1])
     ref = oa.attention_from_codes(q8, qs, k8, ks, v[:, hh:hh + 1], 128 ** -0.5)[:s, 0]
-    assert rel_l2(whole[:, hh], ref) < TOL
+    assert rel_l2(whole[:, hh], ref) < GUARD
 
 
 def test_attention_work_counter_reused(dev):
@@ -200,7 +205,7 @@ def test_attention_work_counter_reused(dev):
     hh = h - 1
     q8, qs, k8, ks, _ = oa.prepass(q[:, hh:hh + 1], k[:, hh:hh + 1])
     ref = oa.attention_from_codes(q8, qs, k8, ks, v[:, hh:hh + 1], 128 ** -0.5)[:s, 0]
-    assert rel_l2(bf16_to_f32(outs[1])[:, hh], ref) < TOL
+    assert rel_l2(bf16_to_f32(outs[1])[:, hh], ref) < GUARD
     pu = attention.prepass_u8(qd, kd, vd)
     outs = []
     for _ in range(2):
@@ -239,7 +244,7 @@ def test_attention_full_size_sampled(dev):
         assert np.array_equal(to_np(pp["kmean"][hh]), km[0])
         ref = oa.attention_from_codes(q8, qs, k8, ks, vn[:, hh:hh + 1], 128 ** -0.5, rows=rows)[:, 0]
         got = bf16_to_f32(to_np(out[torch.from_numpy(rows).to(dev), hh]))
-        assert rel_l2(got, ref) < TOL
+        assert rel_l2(got, ref) < GUARD
         exact = oa.attention_exact(qn[:, hh:hh + 1], kn[:, hh:hh + 1], vn[:, hh:hh + 1], 128 ** -0.5,
                                    rows=rows)[:, 0]
         assert rel_l2(got, exact) < 0.03
