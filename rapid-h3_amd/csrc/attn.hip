@@ -333,10 +333,11 @@ __device__ __forceinline__ void fwd_body(const FwdArgs& a, const int bid, int8_t
   };
   // online softmax of step j's scores and O^T += V^T(j) . P^T; TAIL steps hold 1..63 keys below Sk
   uint32_t pk[2][8];  // P of the current step, bf16 pairs, the B operand of the P.V MFMAs
-  auto softmax = [&](const int j, auto tail) __attribute__((always_inline)) {
+  // kk: the step's key-block (scale, scale x code-norm bound), read from LDS before the step's Q.K^T so that the
+  // read's latency runs under the MFMAs (read after them, the wave waited for it: 0.7 % of the kernel)
+  auto softmax = [&](const int j, auto tail, const float2 kk) __attribute__((always_inline)) {
     constexpr bool TAIL = decltype(tail)::value;
     const int nvalid = TAIL ? static_cast<int>(a.Sk - static_cast<int64_t>(j) * STEP) : STEP;
-    const float2 kk = kscale[j >> 1];
     const float c = qscale * kk.x;
     // Every logit of the step is at most qbound * kk.y (Cauchy-Schwarz on the codes, in the exp2 domain). While
     // that is below mref + 64 for all the wave's queries the step needs no max; otherwise scan the step's
@@ -424,9 +425,10 @@ __device__ __forceinline__ void fwd_body(const FwdArgs& a, const int bid, int8_t
   };
   auto step = [&](const int j, auto tail) __attribute__((always_inline)) {
     const uint32_t slot = static_cast<uint32_t>(j - j0) & (NRING - 1);
+    const float2 kk = kscale[j >> 1];
     load_step(j + 2);
     qk(slot);
-    softmax(j, tail);
+    softmax(j, tail, kk);
     pv(slot);
     barrier();
   };
