@@ -863,10 +863,8 @@ __global__ void __launch_bounds__(512, 2) gemm_persistent_kernel(const GemmArgs 
       }
     } else {
       // block (j, i) = rows j*32.., columns i*32.. of the wave's 128 x 64: bf16(y) (plain: bf16(y + bias))
-      // staged with row r at r * 64 B, 16-byte chunk c at c ^ ((r >> 2) & 3), its two 8-byte halves swapped in
-      // rows 16..31 (the 8-byte writes of rows r and r + 16 then fall in different banks: 32 lanes, 64 banks, no
-      // conflict), then lane l handles row 16*it + l/4, columns 8*(l%4)..+7, so global accesses are 64-byte row
-      // segments
+      // staged with row r at r * 64 B, 16-byte chunk c at c ^ ((r >> 2) & 3), then lane l handles row
+      // 16*it + l/4, columns 8*(l%4)..+7, so global accesses are 64-byte row segments
       int8_t* const ep = ep_lds + wave * 2048;
       const float* xs_s = rec;
       const float* ws_s = rec + BM;
@@ -911,15 +909,14 @@ __global__ void __launch_bounds__(512, 2) gemm_persistent_kernel(const GemmArgs 
             uint2 o;
             o.x = pack_bf2(y[0], y[1]);
             o.y = pack_bf2(y[2], y[3]);
-            *reinterpret_cast<uint2*>(ep + l32 * 64 + ((rq ^ ((l32 >> 2) & 3)) << 4) + 8 * (g ^ (l32 >> 4))) = o;
+            *reinterpret_cast<uint2*>(ep + l32 * 64 + ((rq ^ ((l32 >> 2) & 3)) << 4) + 8 * g) = o;
           }
           // each lane reads back what other lanes of its own wave wrote: LDS executes a wave's accesses
           // in order, and the compiler keeps the reads after the writes (same array)
 #pragma unroll
           for (int it = 0; it < 2; ++it) {
             const int r = it * 16 + (lane >> 2);
-            uint4 v = *reinterpret_cast<const uint4*>(ep + r * 64 + ((chr ^ ((r >> 2) & 3)) << 4));
-            if (it == 1) v = make_uint4(v.z, v.w, v.x, v.y);  // rows 16..31 hold their halves swapped
+            const uint4 v = *reinterpret_cast<const uint4*>(ep + r * 64 + ((chr ^ ((r >> 2) & 3)) << 4));
             const int64_t m = m0 + wm * WM + j * 32 + r;
             const int64_t n = n0 + wn * WN + i * 32 + chr * 8;
             if (m < a.M && n < a.N) {
