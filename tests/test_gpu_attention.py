@@ -248,3 +248,24 @@ def test_attention_full_size_sampled(dev):
         exact = oa.attention_exact(qn[:, hh:hh + 1], kn[:, hh:hh + 1], vn[:, hh:hh + 1], 128 ** -0.5,
                                    rows=rows)[:, 0]
         assert rel_l2(got, exact) < 0.03
+
+
+@pytest.mark.parametrize("s,h,rot", [(331, 3, 96), (200, 5, 128), (1, 1, 128)])
+def test_rms_rope_in_place(dev, s, h, rot):
+    """attention.rms_rope_ (rh3_rms_rope_qk, the unfused route's RMSNorm + RoPE) on strided q / k views of one qkv
+    buffer, in place: bit-exact against oracle.attn.rms_rope for both RoPE widths (rot 128 exchanges partners by a DPP
+    move, 96 through the LDS crossbar) and row counts that leave the last 16-row group ragged; v is untouched."""
+    import torch
+    from rapid_h3 import attention
+    rng = np.random.default_rng(s + h + rot)
+    buf = _bf(rng.standard_normal((s, 3 * h * 128)) * np.exp(rng.standard_normal((s, 1))))
+    bt = to_dev(buf, dev)
+    q, k, v = (t.view(s, h, 128) for t in bt.split(h * 128, dim=-1))
+    tab = _bf(oa.rope_table(np.arange(s) * 7 % 61, rot=rot))
+    qw, kw = _bf(1 + 0.3 * rng.standard_normal(128)), _bf(1 + 0.3 * rng.standard_normal(128))
+    v0 = v.clone()
+    attention.rms_rope_(q, k, to_dev(tab, dev).view(1, s, 1, rot // 2, 2, 2), to_dev(qw, dev), to_dev(kw, dev), 1e-6)
+    b = buf.reshape(s, 3, h, 128)
+    assert np.array_equal(to_np(q), _bf(oa.rms_rope(b[:, 0], tab, qw, 1e-6)))
+    assert np.array_equal(to_np(k), _bf(oa.rms_rope(b[:, 1], tab, kw, 1e-6)))
+    assert torch.equal(v, v0)
