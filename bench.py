@@ -143,7 +143,7 @@ def cpu_baseline(m, x, w, mod, segments, tab, trace, ms=4096, rows=1024):
     """The CPU baseline: the build's CPU restatement of the reference's PyTorch path (oracle/, a numpy port:
     kernels.quantize_rows / quantize_weight, the exact int32 product, the (acc * xs) * ws epilogues, the per-block
     attention emulation), on the host cores of the GPU box, each part the median of 5 runs after 1 warm-up, sampled
-    as BASELINE.md's CPU plan says:
+    as follows:
       * C1 (X [4096, 3072] with 1 % outlier channels, W [3072, 3072] ~ N(0, 0.02), seed 0): measured in full;
       * C2: each of the block's four GEMMs with the quantizer that feeds it, on the first `ms` = 4,096 tokens of the
         GPU leg's own inputs (x, the block's int8 weights, its modulation, and the o / h / x of a traced run of the
