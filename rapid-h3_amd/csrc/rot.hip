@@ -192,11 +192,16 @@ __device__ __forceinline__ void rot_act_chunk(const RotArgs& a, int64_t m, int64
   for (int t = 0; t < 8; ++t) {
     float v[8];
     prologue8<KIND>(a, m, c0 + 8 * t, v);
+    if constexpr (KIND == ROT_SWIGLU) {
 #pragma unroll
-    for (int e = 0; e < 8; e += 2) {  // bf16 round to nearest even (v_cvt_pk_bf16_f32), back to fp32 exactly
-      const uint32_t pk = pk_bf16_hw(v[e], v[e + 1]);
-      d[8 * t + e] = static_cast<double>(__uint_as_float(pk << 16));
-      d[8 * t + e + 1] = static_cast<double>(__uint_as_float(pk & 0xffff0000u));
+      for (int e = 0; e < 8; e += 2) {  // bf16 round to nearest even (v_cvt_pk_bf16_f32), back to fp32 exactly
+        const uint32_t pk = pk_bf16_hw(v[e], v[e + 1]);
+        d[8 * t + e] = static_cast<double>(__uint_as_float(pk << 16));
+        d[8 * t + e + 1] = static_cast<double>(__uint_as_float(pk & 0xffff0000u));
+      }
+    } else {  // the plain and head-major values are bf16 already: the rounding would give them back unchanged
+#pragma unroll
+      for (int e = 0; e < 8; ++e) d[8 * t + e] = static_cast<double>(v[e]);
     }
   }
   rot_combine(d, sb, sc, sd, y);
