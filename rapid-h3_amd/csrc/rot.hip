@@ -130,18 +130,20 @@ __device__ __forceinline__ void prologue8(const RotArgs& a, int64_t m, int64_t c
 }
 
 // The fp32 H4 combine of four chunk values z of a lane quad, before the halving: lane q computes
-// t_q = ((A + sB B) + sC C) + sD D with (A, B, C, D) its quad's z in the order of the reference's formula for y_q
-// (lanes 0-2: z0, z1, z2, z3; lane 3: z1, z2, z3, z0) and the lane's signs. Each term is one v_fmac_f32 whose first
-// operand arrives through a DPP quad permutation (the product with +-1 is exact, so each step is the reference's add
-// or subtract rounded once). Four elements per block; s_nop 1 gives the DPP reads of z the two wait states a VALU
-// write needs before them.
-__device__ __forceinline__ void quad_combine4(const float* z, float sb, float sc, float sd, float* t) {
+// t_q = ((sA A + sB B) + sC C) + sD D with (A, B, C, D) its quad's z in the order of the reference's formula for y_q
+// (lanes 0-2: z0, z1, z2, z3; lane 3: z1, z2, z3, z0) and the lane's signs times a power of two (the H64
+// normalization 1/8, applied here instead of to each z). The first term is one v_mul_f32 and each further term one
+// v_fmac_f32 whose first operand arrives through a DPP quad permutation; the products with +-2^-k are exact, so each
+// step is the reference's add or subtract of the scaled z rounded once, and scaling by a power of two commutes with
+// the rounding. Four elements per block; s_nop 1 gives the DPP reads of z the two wait states a VALU write needs
+// before them.
+__device__ __forceinline__ void quad_combine4(const float* z, float sa, float sb, float sc, float sd, float* t) {
   asm volatile(
       "s_nop 1\n\t"
-      "v_mov_b32_dpp %0, %4 quad_perm:[0,0,0,1] row_mask:0xf bank_mask:0xf\n\t"
-      "v_mov_b32_dpp %1, %5 quad_perm:[0,0,0,1] row_mask:0xf bank_mask:0xf\n\t"
-      "v_mov_b32_dpp %2, %6 quad_perm:[0,0,0,1] row_mask:0xf bank_mask:0xf\n\t"
-      "v_mov_b32_dpp %3, %7 quad_perm:[0,0,0,1] row_mask:0xf bank_mask:0xf\n\t"
+      "v_mul_f32_dpp %0, %4, %11 quad_perm:[0,0,0,1] row_mask:0xf bank_mask:0xf\n\t"
+      "v_mul_f32_dpp %1, %5, %11 quad_perm:[0,0,0,1] row_mask:0xf bank_mask:0xf\n\t"
+      "v_mul_f32_dpp %2, %6, %11 quad_perm:[0,0,0,1] row_mask:0xf bank_mask:0xf\n\t"
+      "v_mul_f32_dpp %3, %7, %11 quad_perm:[0,0,0,1] row_mask:0xf bank_mask:0xf\n\t"
       "v_fmac_f32_dpp %0, %4, %8 quad_perm:[1,1,1,2] row_mask:0xf bank_mask:0xf\n\t"
       "v_fmac_f32_dpp %1, %5, %8 quad_perm:[1,1,1,2] row_mask:0xf bank_mask:0xf\n\t"
       "v_fmac_f32_dpp %2, %6, %8 quad_perm:[1,1,1,2] row_mask:0xf bank_mask:0xf\n\t"
@@ -155,19 +157,23 @@ __device__ __forceinline__ void quad_combine4(const float* z, float sb, float sc
       "v_fmac_f32_dpp %2, %6, %10 quad_perm:[3,3,3,0] row_mask:0xf bank_mask:0xf\n\t"
       "v_fmac_f32_dpp %3, %7, %10 quad_perm:[3,3,3,0] row_mask:0xf bank_mask:0xf"
       : "=&v"(t[0]), "=&v"(t[1]), "=&v"(t[2]), "=&v"(t[3])
-      : "v"(z[0]), "v"(z[1]), "v"(z[2]), "v"(z[3]), "v"(sb), "v"(sc), "v"(sd));
+      : "v"(z[0]), "v"(z[1]), "v"(z[2]), "v"(z[3]), "v"(sb), "v"(sc), "v"(sd), "v"(sa));
 }
 
 // H64 of the lane's chunk d (bf16 values, exact in float64), rounded once to fp32, then the fp32 H4 combine of
-// the quad's four chunks in the reference's order. t = 2 y: the reference's final halving is folded into the
-// quantization scale (rot_scale), which gives the same scale and codes (see there).
+// the quad's four chunks in the reference's order. The H64 normalization 1/8 rides on the combine's signs: fp32(d)/8
+// is fp32(d/8) (a power-of-two scaling commutes with the rounding; below 2^-126, where the two could differ, every
+// code is 0 and the scale sits at its 1e-12 floor either way; |d| stays below 2^128 for inputs below 2^122, the
+// range in which t = 2 y below is finite too). t = 2 y: the reference's final halving is folded
+// into the quantization scale (rot_scale), which gives the same scale and codes (see there).
 __device__ __forceinline__ void rot_combine(double (&d)[64], float sb, float sc, float sd, float (&t)[64]) {
   h64(d);
   float z[64];
 #pragma unroll
-  for (int i = 0; i < 64; ++i) z[i] = static_cast<float>(d[i] * 0.125);
+  for (int i = 0; i < 64; ++i) z[i] = static_cast<float>(d[i]);
+  const float qb = sb * 0.125f, qc = sc * 0.125f, qd = sd * 0.125f;
 #pragma unroll
-  for (int i = 0; i < 64; i += 4) quad_combine4(z + i, sb, sc, sd, t + i);
+  for (int i = 0; i < 64; i += 4) quad_combine4(z + i, 0.125f, qb, qc, qd, t + i);
 }
 
 // Row scale and quantization multiplier from the largest |t| (t = 2 y). With y = t / 2 the reference computes
