@@ -115,6 +115,30 @@ def test_rot_shapes(dev, m, k):
     _eq(q, s, eq, es)
 
 
+def test_rot_extreme_magnitudes(dev):
+    """Rows from bf16's subnormal range (2^-133) to 2^118, and a row mixing 2^-128 columns into normal ones, through
+    the plain and head-major rotations: bit-exact against the oracle, which rounds each chunk value to fp32 after
+    the 1/8 normalization (the kernel applies the 1/8 in the combine instead; the two agree wherever it matters:
+    tiny rows sit at the 1e-12 scale floor with codes 0 and the large ones stay finite)."""
+    from rapid_h3 import quant
+    rng = np.random.default_rng(11)
+    k = 768
+    rows = [(rng.standard_normal(k) * 2.0 ** e).astype(np.float32)
+            for e in (-133, -130, -126, -120, -100, -40, -36, 0, 60, 100, 118)]
+    mixed = rng.standard_normal(k).astype(np.float32)
+    mixed[::3] *= np.float32(2.0 ** -128)
+    rows.append(mixed)
+    x = f32_to_bf16(np.stack(rows))
+    q, s = quant.rot_quant_rows_i8(to_dev(x, dev))
+    eq, es = oq.rot_quant_rows_i8(x)
+    _eq(q, s, eq, es)
+    assert (np.abs(eq[5:7].astype(np.int32)).max(axis=1) > 0).all()   # the 1e-12 floor rows with nonzero codes
+    o = np.ascontiguousarray(x.reshape(len(rows), k // 128, 128).transpose(1, 0, 2))
+    q, s = quant.rot_quant_heads_i8(to_dev(o, dev))
+    eq, es = oq.rot_quant_heads_i8(o)
+    _eq(q, s, eq, es)
+
+
 def test_rot_strided_rows(dev):
     from rapid_h3 import quant
     rng = np.random.default_rng(7)
