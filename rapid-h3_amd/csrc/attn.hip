@@ -553,8 +553,12 @@ int prepass(const uint16_t* q, int64_t q_ss, int64_t q_sh, const uint16_t* k, in
   const int64_t sqp = pad(Sq), skp = pad(Sk);
   const int nchunk = static_cast<int>((Sk + CHUNK - 1) / CHUNK);
   const float* mean = nullptr;
+  // With smoothing and the RMSNorm + RoPE prologue, the statistics pass already computes every K row's prologue:
+  // it stores those rows (bf16, [H][Skpad][128]) in the V^T region, which vt_kernel fills only afterwards, and the K
+  // quantizer reads them back without running the prologue a second time (the same values, so the same codes).
+  const bool staged = smooth_k && rk.tab;
   if (smooth_k) {
-    launch_stats(dim3(H, nchunk), st, k, k_ss, k_sh, Sk, rk, w.part);
+    launch_stats(dim3(H, nchunk), st, k, k_ss, k_sh, Sk, rk, w.part, staged ? w.vt : nullptr, skp * D);
     hipLaunchKernelGGL(kmean_kernel, dim3(H), dim3(KMEAN_NT), 0, st, w.part, nchunk, Sk, w.kmean);
     mean = w.kmean;
   } else {
@@ -563,7 +567,11 @@ int prepass(const uint16_t* q, int64_t q_ss, int64_t q_sh, const uint16_t* k, in
   }
   launch_quant(dim3(H, sqp / BLK), st, q, q_ss, q_sh, Sq, sqp, rq, static_cast<const float*>(nullptr), w.q8, w.qs,
                nullptr);
-  launch_quant(dim3(H, skp / BLK), st, k, k_ss, k_sh, Sk, skp, rk, mean, w.k8, w.ks, w.kn);
+  if (staged)
+    launch_quant(dim3(H, skp / BLK), st, w.vt, D, skp * D, Sk, skp, RR{nullptr, nullptr, 0.f, 0}, mean, w.k8, w.ks,
+                 w.kn);
+  else
+    launch_quant(dim3(H, skp / BLK), st, k, k_ss, k_sh, Sk, skp, rk, mean, w.k8, w.ks, w.kn);
   hipLaunchKernelGGL(vt_kernel, dim3(H, skp / 64), dim3(256), 0, st, v, v_ss, v_sh, Sk, skp, w.vt);
   return launch_status("attention prepass");
 }

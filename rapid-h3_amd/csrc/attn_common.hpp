@@ -28,7 +28,8 @@ typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 constexpr int STATS_NT = 256;
 template <bool RRON>
 __global__ void __launch_bounds__(STATS_NT) stats_kernel(const uint16_t* __restrict__ k, int64_t k_ss, int64_t k_sh,
-                                                    int64_t S, RR rr, double* __restrict__ part) {
+                                                    int64_t S, RR rr, double* __restrict__ part,
+                                                    uint16_t* __restrict__ kn, int64_t kn_sh) {
   __shared__ double red[16][D];
   const int h = blockIdx.x, c = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
   const int slot = tid >> 4, l16 = tid & 15;
@@ -47,6 +48,14 @@ __global__ void __launch_bounds__(STATS_NT) stats_kernel(const uint16_t* __restr
     if (s < S) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc[e] += static_cast<double>(x[e]);
+      if (RRON && kn) {  // the RMSNorm + RoPE'd row (bf16 values: the packing is exact) for the K quantizer
+        uint4 o;
+        o.x = pack_bf2(x[0], x[1]);
+        o.y = pack_bf2(x[2], x[3]);
+        o.z = pack_bf2(x[4], x[5]);
+        o.w = pack_bf2(x[6], x[7]);
+        *reinterpret_cast<uint4*>(kn + h * kn_sh + s * D + 8 * l16) = o;
+      }
     }
   }
 #pragma unroll
@@ -59,11 +68,15 @@ __global__ void __launch_bounds__(STATS_NT) stats_kernel(const uint16_t* __restr
   }
 }
 
-// the K statistics of one launch: stats_kernel with or without the RMSNorm + RoPE prologue
+// the K statistics of one launch: stats_kernel with or without the RMSNorm + RoPE prologue; with the prologue and
+// kn, also the prologue's rows as bf16 into kn [H][..][128] (head stride kn_sh elements)
 inline void launch_stats(dim3 grid, hipStream_t st, const uint16_t* k, int64_t k_ss, int64_t k_sh, int64_t S,
-                         const RR& rr, double* part) {
-  if (rr.tab) hipLaunchKernelGGL(stats_kernel<true>, grid, dim3(STATS_NT), 0, st, k, k_ss, k_sh, S, rr, part);
-  else hipLaunchKernelGGL(stats_kernel<false>, grid, dim3(STATS_NT), 0, st, k, k_ss, k_sh, S, rr, part);
+                         const RR& rr, double* part, uint16_t* kn = nullptr, int64_t kn_sh = 0) {
+  if (rr.tab)
+    hipLaunchKernelGGL(stats_kernel<true>, grid, dim3(STATS_NT), 0, st, k, k_ss, k_sh, S, rr, part, kn, kn_sh);
+  else
+    hipLaunchKernelGGL(stats_kernel<false>, grid, dim3(STATS_NT), 0, st, k, k_ss, k_sh, S, rr, part, nullptr,
+                       int64_t{0});
 }
 
 __global__ void zero_kernel(float* __restrict__ p, int64_t n) {
