@@ -44,6 +44,25 @@ def _check_prepass(pp, q8, qs, k8, ks, km, v, s):
     assert np.array_equal(vt, vpad[keys].transpose(1, 2, 0))
 
 
+@pytest.mark.parametrize("s,h", [(1000, 3), (257, 2)])
+def test_prepass_rope128_staged_k(dev, s, h):
+    """The pre-pass with the full-width RoPE (rot 128, the DPP partner exchange) and K smoothing, at ragged lengths
+    (a partial last 256-token statistics chunk and a partial last 128-token block): K's RMSNorm + RoPE rows are
+    staged by the statistics pass and read back by the K quantizer. Codes, scales, kmean and the V^T layout
+    bit-exact against the oracle."""
+    from rapid_h3 import attention
+    rng = np.random.default_rng(s * 7 + h)
+    q, k, v = (f32_to_bf16((rng.standard_normal((s, h, 128)) + off).astype(np.float32))
+               for off in (0.0, rng.standard_normal((1, h, 128)) * 2.0, 0.0))
+    tab = f32_to_bf16(oa.rope_table(np.arange(s) % 97, rot=128).reshape(s, 64, 2, 2))
+    qw = f32_to_bf16((1.0 + 0.1 * rng.standard_normal(128)).astype(np.float32))
+    kw = f32_to_bf16((1.0 + 0.1 * rng.standard_normal(128)).astype(np.float32))
+    pp = attention.prepass(to_dev(q, dev), to_dev(k, dev), to_dev(v, dev), to_dev(tab, dev).view(1, s, 1, 64, 2, 2),
+                           to_dev(qw, dev), to_dev(kw, dev), 1e-5)
+    q8, qs, k8, ks, km = oa.prepass(q, k, rr=(tab, qw, kw, 1e-5))
+    _check_prepass(pp, q8, qs, k8, ks, km, v, s)
+
+
 def test_attention_golden(dev, golden):
     from rapid_h3 import attention
     g = golden("attention")
